@@ -1,0 +1,164 @@
+/*
+ * tklab_hip.h — C ABI of libtklab_hip.so, the gfx950 (MI355X) kernels behind
+ * the tklab Python entry points.
+ *
+ * Each entry point replaces one `kernel[grid](...)` launch of the reference's
+ * Python launchers (v1olegrace/triton-kernel-lab, src/tklab/kernels/<kernel>.py); the
+ * replaced launch is cited above every declaration. Validation, allocation and
+ * autograd stay in Python exactly as in the reference; these functions only
+ * check what the kernels themselves assume and then enqueue work.
+ *
+ * Conventions
+ *   - Pointers are device pointers; `const` marks inputs. Nothing here
+ *     allocates or frees device memory: every output and workspace is passed in.
+ *   - Sizes and strides are in ELEMENTS, as int64_t. Every feature dimension is
+ *     unit-stride; the strides given are the remaining (row/batch/head) ones.
+ *   - `dtype` is one of TK_DTYPE_*; all tensors of one call share it unless a
+ *     parameter says otherwise (statistics and workspaces are float32).
+ *   - `stream` is a hipStream_t (0 = the null stream). Work is enqueued
+ *     asynchronously; no function synchronizes the device.
+ *   - Return value: 0 on success; non-zero when the arguments break a kernel
+ *     assumption or the launch failed. tk_last_error() then returns a message
+ *     (thread-local, valid until the next failing call on the same thread).
+ */
+#ifndef TKLAB_HIP_H
+#define TKLAB_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TK_ABI_VERSION 1
+
+enum tk_dtype { TK_DTYPE_F32 = 0, TK_DTYPE_F16 = 1, TK_DTYPE_BF16 = 2 };
+
+/* ABI version of the loaded library (TK_ABI_VERSION at build time). */
+int tk_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* tk_last_error(void);
+
+/* Row-wise softmax y = exp(x - max) / sum, float32 math, stored in `dtype`.
+ * Replaces `_softmax_kernel[(rows,)](...)`, src/tklab/kernels/fused_softmax.py:116-124.
+ * cols <= 65536. */
+int tk_softmax_fwd(int dtype, const void* x, void* y, int64_t rows, int64_t cols,
+                   int64_t x_row_stride, int64_t y_row_stride, void* stream);
+
+/* RMSNorm forward with an optional fused residual add.
+ *   s = residual ? round_dtype(x + residual) : x
+ *   rstd = 1 / sqrt(mean(s^2) + eps);  y = s * rstd * weight
+ * `residual`, `residual_sum` (written when non-null) and `rstd` (float32[rows],
+ * written when non-null) may be NULL.
+ * Replaces `_rms_norm_forward_kernel[(rows,)]`, src/tklab/kernels/rms_norm.py:248-260,
+ * and `_residual_rms_norm_forward_kernel[(rows,)]`,
+ * src/tklab/kernels/residual_rms_norm.py:149-167. cols * sizeof(dtype) <= 65536. */
+int tk_rmsnorm_fwd(int dtype, const void* x, const void* residual, const void* weight,
+                   void* residual_sum, void* y, float* rstd, int64_t rows, int64_t cols,
+                   int64_t x_row_stride, int64_t residual_row_stride,
+                   int64_t residual_sum_row_stride, int64_t y_row_stride, float eps,
+                   void* stream);
+
+/* RMSNorm backward, stage 1: per-row dx (plus `incoming_dx` when non-null) and
+ * one float32 dweight partial row per group, partial_dw[group_count][cols].
+ * Group g (g < group_count = min(group_size, rows)) owns rows r with
+ * r % group_size == g and writes partial_dw[g] with a plain store, in a fixed
+ * summation order (deterministic, no atomics). `locks` is int32[2*group_size]:
+ * the first half is left untouched (zero), the second half gets 1 in every
+ * slot g < group_count, marking partial row g as written.
+ * Replaces `_rms_norm_backward_stage1_kernel[(rows,)]`, src/tklab/kernels/rms_norm.py:309-327. */
+int tk_rmsnorm_bwd_stage1(int dtype, void* dx, const void* dy, const void* incoming_dx,
+                          float* partial_dw, const void* x, const void* weight,
+                          const float* rstd, int32_t* locks, int64_t rows, int64_t cols,
+                          int64_t x_row_stride, int64_t dy_row_stride,
+                          int64_t incoming_dx_row_stride, int64_t dx_row_stride,
+                          int64_t group_size, void* stream);
+
+/* RMSNorm backward, stage 2: dw[c] = sum_{g < group_count} partial_dw[g][c], summed
+ * in increasing g, stored in `dtype`.
+ * Replaces `_rms_norm_backward_stage2_kernel[...]`, src/tklab/kernels/rms_norm.py:335-343. */
+int tk_rmsnorm_bwd_stage2(int dtype, const float* partial_dw, void* dw, int64_t group_count,
+                          int64_t cols, void* stream);
+
+/* SwiGLU forward y = value * gate * sigmoid(gate).
+ * Replaces `_swiglu_forward_kernel[...]`, src/tklab/kernels/swiglu.py:157-167. */
+int tk_swiglu_fwd(int dtype, const void* value, const void* gate, void* y, int64_t rows,
+                  int64_t cols, int64_t value_row_stride, int64_t gate_row_stride,
+                  int64_t y_row_stride, void* stream);
+
+/* SwiGLU backward: dvalue = dy * silu(gate), dgate = dy * value * silu'(gate).
+ * Replaces `_swiglu_backward_kernel[...]`, src/tklab/kernels/swiglu.py:185-199. */
+int tk_swiglu_bwd(int dtype, const void* dy, const void* value, const void* gate,
+                  void* dvalue, void* dgate, int64_t rows, int64_t cols,
+                  int64_t dy_row_stride, int64_t value_row_stride, int64_t gate_row_stride,
+                  int64_t dvalue_row_stride, int64_t dgate_row_stride, void* stream);
+
+/* Rotate-half RoPE forward on x[rows][2*half_dim] with cos/sin[rows][half_dim]:
+ *   y1 = x1*cos - x2*sin,  y2 = x2*cos + x1*sin.
+ * Replaces `_rope_forward_kernel[...]`, src/tklab/kernels/rope.py:213-225. */
+int tk_rope_fwd(int dtype, const void* x, const void* cos, const void* sin, void* y,
+                int64_t rows, int64_t half_dim, int64_t x_row_stride, int64_t cos_row_stride,
+                int64_t sin_row_stride, int64_t y_row_stride, void* stream);
+
+/* RoPE backward: dx = RoPE(dy, cos, -sin); when non-null,
+ * dcos = dy1*x1 + dy2*x2 and dsin = -dy1*x2 + dy2*x1 (x is read only then).
+ * Replaces `_rope_backward_kernel[...]`, src/tklab/kernels/rope.py:251-271. */
+int tk_rope_bwd(int dtype, const void* dy, const void* x, const void* cos, const void* sin,
+                void* dx, void* dcos, void* dsin, int64_t rows, int64_t half_dim,
+                int64_t dy_row_stride, int64_t x_row_stride, int64_t cos_row_stride,
+                int64_t sin_row_stride, int64_t dx_row_stride, int64_t dcos_row_stride,
+                int64_t dsin_row_stride, void* stream);
+
+/* GEMM C[M][N] = A[M][K] * B[K][N] on MFMA, float32 accumulation, C stored in
+ * `dtype` (TK_DTYPE_F16 or TK_DTYPE_BF16). All strides are element strides
+ * and must be positive. `acc_fp16` != 0 requests the reference's FP16
+ * accumulation mode; gfx950 MFMA accumulates f16/bf16 products in float32
+ * only, so the flag is accepted and the result is the FP32-accumulated one.
+ * Replaces `_matmul_kernel[grid](...)`, src/tklab/kernels/matmul.py:217-232. */
+int tk_gemm(int dtype, const void* a, const void* b, void* c, int64_t m, int64_t n,
+            int64_t k, int64_t stride_am, int64_t stride_ak, int64_t stride_bk,
+            int64_t stride_bn, int64_t stride_cm, int64_t stride_cn, int acc_fp16,
+            void* stream);
+
+/* Flash attention forward over q/k/v/o[batch][heads][seq][head_dim]
+ * (head_dim unit-stride; strides given for batch, head and seq), head_dim in
+ * {64, 128}, dtype TK_DTYPE_F16 or TK_DTYPE_BF16. Online softmax in base 2
+ * with scale*log2(e); O = acc / l. When `lse` (float32[batch][heads][seq],
+ * contiguous) is non-null it receives m + log2(l), the base-2 log-sum-exp of
+ * the scaled scores.
+ * Replaces `_flash_attention_forward_kernel[grid](...)`,
+ * src/tklab/kernels/flash_attention.py:331-347. */
+int tk_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+                int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                const int64_t* o_strides, float sm_scale, int causal, void* stream);
+
+/* Attention backward preprocess: delta[b][h][i] = sum_d o[i][d] * do[i][d] (float32).
+ * o and do share `strides` (batch, head, seq).
+ * Replaces `_attn_bwd_preprocess_kernel[...]`, src/tklab/kernels/flash_attention.py:560-569. */
+int tk_attn_bwd_preprocess(int dtype, const void* o, const void* dout, float* delta,
+                           int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                           const int64_t* strides, void* stream);
+
+/* Attention backward, dK and dV for every key block (single writer per block):
+ *   P = exp2(S*scale*log2e - lse) (masked), dV = P^T dO, dS = P (dO V^T - delta),
+ *   dK = scale * dS^T Q.  All of q/k/v/dout/dk/dv share `strides`.
+ * Replaces `_attn_bwd_dkdv_kernel[...]`, src/tklab/kernels/flash_attention.py:570-587. */
+int tk_attn_bwd_dkdv(int dtype, const void* q, const void* k, const void* v, const void* dout,
+                     void* dk, void* dv, const float* lse, const float* delta, int64_t batch,
+                     int64_t heads, int64_t seq, int64_t head_dim, const int64_t* strides,
+                     float sm_scale, int causal, void* stream);
+
+/* Attention backward, dQ = scale * dS K for every query block (single writer).
+ * Replaces `_attn_bwd_dq_kernel[...]`, src/tklab/kernels/flash_attention.py:588-605. */
+int tk_attn_bwd_dq(int dtype, const void* q, const void* k, const void* v, const void* dout,
+                   void* dq, const float* lse, const float* delta, int64_t batch,
+                   int64_t heads, int64_t seq, int64_t head_dim, const int64_t* strides,
+                   float sm_scale, int causal, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TKLAB_HIP_H */

@@ -1,0 +1,110 @@
+"""Pre-launch validation on CPU and meta tensors: no GPU, no library load.
+
+Covers the message fragments the reference's tests pin
+(tests/test_kernel_validation.py) for the hot-path entry points, plus the
+order in which the checks fire.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from tklab.kernels.fused_softmax import softmax
+from tklab.kernels.residual_rms_norm import residual_rms_norm
+from tklab.kernels.rms_norm import _make_backward_buffers, rms_norm
+from tklab.kernels.rope import rope
+from tklab.kernels.swiglu import swiglu
+
+
+def test_softmax_rejects_column_strided_rows() -> None:
+    with pytest.raises(ValueError, match="contiguous final dimension"):
+        softmax(torch.zeros(4, 8)[:, ::2])
+
+
+def test_softmax_requires_a_gpu_tensor() -> None:
+    with pytest.raises(ValueError, match="requires CUDA"):
+        softmax(torch.zeros(2, 8))
+
+
+@pytest.mark.parametrize(
+    ("x", "fragment"),
+    [
+        (torch.zeros(8), "2D tensor"),
+        (torch.zeros(0, 8), "empty"),
+        (torch.zeros(2, 65537, device="meta"), "single-pass limit"),
+        (torch.zeros(2, 8, dtype=torch.float64), "float16"),
+    ],
+)
+def test_softmax_contract(x: torch.Tensor, fragment: str) -> None:
+    with pytest.raises(ValueError, match=fragment):
+        softmax(x)
+
+
+def test_rms_norm_rejects_mismatched_weight() -> None:
+    with pytest.raises(ValueError, match="match the final input dimension"):
+        rms_norm(torch.zeros(2, 8), torch.ones(7))
+
+
+@pytest.mark.parametrize("eps", [0.0, -1e-5, float("nan"), float("inf")])
+def test_rms_norm_rejects_invalid_epsilon(eps: float) -> None:
+    with pytest.raises(ValueError, match="finite and positive"):
+        rms_norm(torch.zeros(2, 8), torch.ones(8), eps=eps)
+
+
+def test_rms_norm_checks_weight_layout_before_device() -> None:
+    with pytest.raises(ValueError, match="must be contiguous"):
+        rms_norm(torch.zeros(2, 8), torch.ones(16)[::2])
+    with pytest.raises(ValueError, match="requires CUDA"):
+        rms_norm(torch.zeros(2, 8), torch.ones(8))
+
+
+def test_rms_norm_rejects_rows_beyond_the_fused_budget() -> None:
+    x = torch.zeros(2, 32769, dtype=torch.float16, device="meta")
+    w = torch.zeros(32769, dtype=torch.float16, device="meta")
+    with pytest.raises(ValueError):
+        rms_norm(x, w)
+
+
+def test_backward_buffers_keep_the_reference_layout() -> None:
+    x = torch.zeros(1025, 1000)
+    w = torch.zeros(1000)
+    buffers = _make_backward_buffers(x, w, group_size=1)
+    assert buffers.locks.tolist() == [0, 0]
+    assert buffers.partial_dw.shape == (1, 1000)
+    assert buffers.group_count == 1
+    default = _make_backward_buffers(x, w)
+    assert default.group_count == min(default.group_size, 1025)
+    assert default.locks.shape == (2 * default.group_size,)
+    with pytest.raises(ValueError, match="group_size must be positive"):
+        _make_backward_buffers(x, w, group_size=0)
+
+
+def test_residual_rms_norm_rejects_shape_mismatch() -> None:
+    with pytest.raises(ValueError, match="residual must match"):
+        residual_rms_norm(torch.zeros(2, 8), torch.zeros(3, 8), torch.ones(8))
+
+
+def test_residual_rms_norm_rejects_invalid_epsilon() -> None:
+    with pytest.raises(ValueError, match="finite and positive"):
+        residual_rms_norm(torch.zeros(2, 8), torch.zeros(2, 8), torch.ones(8), eps=float("nan"))
+
+
+def test_swiglu_rejects_shape_mismatch() -> None:
+    with pytest.raises(ValueError, match="identical shapes"):
+        swiglu(torch.zeros(2, 8), torch.zeros(3, 8))
+
+
+def test_swiglu_requires_a_gpu_tensor() -> None:
+    with pytest.raises(ValueError, match="requires CUDA"):
+        swiglu(torch.zeros(2, 8), torch.zeros(2, 8))
+
+
+def test_rope_rejects_odd_feature_dimension() -> None:
+    with pytest.raises(ValueError, match="even feature dimension"):
+        rope(torch.zeros(2, 7), torch.zeros(2, 3), torch.zeros(2, 3))
+
+
+def test_rope_rejects_full_width_tables() -> None:
+    with pytest.raises(ValueError, match="columns // 2"):
+        rope(torch.zeros(2, 8), torch.zeros(2, 8), torch.zeros(2, 8))

@@ -1,0 +1,49 @@
+"""The C-ABI library: it is built, loads, and exports every declared symbol.
+
+Loading needs no GPU; nothing here launches a kernel.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+from tklab import _hip
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "tklab_hip.h"
+
+
+def _declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^(?:int|const char\*)\s+(tk_\w+)\(", text, flags=re.MULTILINE))
+
+
+def test_header_and_binding_agree() -> None:
+    assert _declared_functions() == set(_hip.EXPORTED_SYMBOLS)
+
+
+def test_library_loads_and_exports_every_declared_symbol() -> None:
+    lib = _hip.load_library()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.tk_abi_version() == _hip.ABI_VERSION
+    assert lib.tk_last_error() == b""
+
+
+def test_library_has_gfx950_code_only() -> None:
+    data = _hip.LIBRARY_PATH.read_bytes()
+    assert b"gfx950" in data
+    for other in (b"gfx942", b"gfx90a", b"gfx1100"):
+        assert other not in data
+
+
+def test_invalid_arguments_fail_before_any_launch() -> None:
+    lib = _hip.load_library()
+    status = lib.tk_softmax_fwd(0, None, None, 4, 4, 4, 4, None)
+    assert status != 0
+    assert b"null pointer" in lib.tk_last_error()
+    status = lib.tk_softmax_fwd(7, ctypes.c_void_p(16), ctypes.c_void_p(16), 4, 4, 4, 4, None)
+    assert status != 0
+    assert b"dtype" in lib.tk_last_error()

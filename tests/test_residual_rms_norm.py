@@ -1,0 +1,136 @@
+"""GPU parity of the fused residual-add RMSNorm (forward, both-output backward).
+
+Reference cases follow the reference's tests/test_residual_rms_norm.py (seeds
+20-24, strides 2/3/4/5, thresholds); bitwise residual-sum checks and the
+oracle comparisons at the config shape are this build's own.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from _helpers import bits_equal, dev, host, name, strided_rows
+from oracle import oracle
+from tklab.harness.tolerances import assert_close, assert_relative_frobenius
+from tklab.kernels._norm_common import EPS
+from tklab.kernels.residual_rms_norm import _launch_forward, residual_rms_norm
+from tklab.kernels.rms_norm import (
+    _launch_backward_stage1,
+    _launch_backward_stage2,
+    _make_backward_buffers,
+)
+
+pytestmark = pytest.mark.gpu
+
+
+def _problem(rows: int = 37, cols: int = 1000):
+    x = strided_rows(rows, cols, 2, requires_grad=True)
+    r = strided_rows(rows, cols, 3, requires_grad=True)
+    dsum = strided_rows(rows, cols, 4)
+    dout = strided_rows(rows, cols, 5)
+    w = torch.randn(cols, device="cuda", requires_grad=True)
+    return x, r, w, dsum, dout
+
+
+def _reference(x, r, w):
+    s = x + r
+    return s, F.rms_norm(s, (s.shape[-1],), w, EPS)
+
+
+def test_forward_matches_pytorch() -> None:
+    torch.manual_seed(20)
+    x, r, w, _, _ = _problem()
+    s, y = residual_rms_norm(x, r, w)
+    s_ref, y_ref = _reference(x, r, w)
+    assert_relative_frobenius(s, s_ref, max_relative_error=1e-7)
+    assert_relative_frobenius(y, y_ref, max_relative_error=1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_half_precision_sum_is_bitwise_torch_add(dtype: torch.dtype) -> None:
+    torch.manual_seed(24)
+    x = torch.randn(37, 1000, device="cuda", dtype=dtype)
+    r = torch.randn_like(x)
+    w = torch.randn(1000, device="cuda", dtype=dtype)
+    s, y = residual_rms_norm(x, r, w)
+    assert bits_equal(s, x + r)
+    assert_relative_frobenius(y, F.rms_norm(x + r, (1000,), w, EPS), max_relative_error=1e-3)
+
+
+def test_combined_output_gradients_match_autograd() -> None:
+    torch.manual_seed(21)
+    x, r, w, dsum, dout = _problem(rows=67)
+    s_ref, y_ref = _reference(x, r, w)
+    refs = torch.autograd.grad((s_ref, y_ref), (x, r, w), grad_outputs=(dsum, dout))
+    x2, r2, w2 = (t.detach().requires_grad_(True) for t in (x, r, w))
+    s, y = residual_rms_norm(x2, r2, w2)
+    dx, dr, dw = torch.autograd.grad((s, y), (x2, r2, w2), grad_outputs=(dsum, dout))
+    for got, want in zip((dx, dr, dw), refs):
+        assert_relative_frobenius(got, want, max_relative_error=1e-2)
+    assert bits_equal(dx, dr)
+
+
+@pytest.mark.parametrize("deterministic", [False, True])
+def test_sum_only_gradient_passes_through(deterministic: bool) -> None:
+    torch.manual_seed(22)
+    x, r, w, dsum, _ = _problem(rows=17)
+    previous = torch.are_deterministic_algorithms_enabled()
+    previous_warn = torch.is_deterministic_algorithms_warn_only_enabled()
+    try:
+        torch.use_deterministic_algorithms(deterministic)
+        s, _ = residual_rms_norm(x, r, w)
+        dx, dr = torch.autograd.grad(s, (x, r), grad_outputs=dsum)
+    finally:
+        torch.use_deterministic_algorithms(previous, warn_only=previous_warn)
+    torch.testing.assert_close(dx, dsum, rtol=0, atol=0)
+    torch.testing.assert_close(dr, dsum, rtol=0, atol=0)
+
+
+def test_single_group_adds_incoming_gradient() -> None:
+    torch.manual_seed(23)
+    rows, cols = 1025, 1000
+    x, r, w, dsum, dout = _problem(rows=rows, cols=cols)
+    s = torch.empty_like(x)
+    y = torch.empty_like(x)
+    rstd = torch.empty(rows, device="cuda")
+    _launch_forward(x, r, w, s, y, rstd, eps=EPS, store_residual=True, store_stats=True)
+    buffers = _make_backward_buffers(s, w, group_size=1)
+    x_hat = s * rstd[:, None]
+    g = w * dout
+    dx_expected = dsum + rstd[:, None] * (g - x_hat * torch.mean(g * x_hat, dim=1, keepdim=True))
+    dw_expected = torch.sum(dout * x_hat, dim=0)
+    for _ in range(10):
+        buffers.locks.zero_()
+        _launch_backward_stage1(dout, s, w, rstd, buffers, incoming_dx=dsum)
+        torch.cuda.synchronize()
+        assert buffers.locks.cpu().tolist() == [0, 1]
+        _launch_backward_stage2(buffers, cols)
+        torch.cuda.synchronize()
+        assert_relative_frobenius(buffers.dx, dx_expected, max_relative_error=1e-2)
+        assert_relative_frobenius(buffers.dw, dw_expected, max_relative_error=1e-2)
+
+
+def test_config_shape_bf16_16384x4096_matches_the_oracle() -> None:
+    """x, residual ~N(0,1), weight ~N(1, 0.02), eps 1e-6, both grads."""
+    torch.manual_seed(0)
+    rows, cols = 16384, 4096
+    x = torch.randn(rows, cols, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    r = torch.randn(rows, cols, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    w = (1 + 0.02 * torch.randn(cols, device="cuda")).to(torch.bfloat16).requires_grad_(True)
+    dsum = torch.randn(rows, cols, device="cuda", dtype=torch.bfloat16)
+    dout = torch.randn(rows, cols, device="cuda", dtype=torch.bfloat16)
+    s, y = residual_rms_norm(x, r, w, eps=1e-6)
+    dx, dr, dw = torch.autograd.grad((s, y), (x, r, w), grad_outputs=(dsum, dout))
+
+    s_ref, y_ref, rstd_ref = oracle.rmsnorm_fwd(host(x), host(w), 1e-6, "bfloat16", residual=host(r))
+    assert bits_equal(s, dev(s_ref, s).to(torch.bfloat16))
+    assert_close(y, dev(y_ref, y))
+    dx_ref, dw_ref = oracle.rmsnorm_bwd(
+        host(dout), s_ref, host(w), rstd_ref, "bfloat16", incoming=host(dsum)
+    )
+    assert_close(dx, dev(dx_ref, dx))
+    assert bits_equal(dx, dr)
+    assert_relative_frobenius(dw, dev(dw_ref, dw), max_relative_error=1e-2)
+    assert_close(dw, dev(dw_ref, dw))

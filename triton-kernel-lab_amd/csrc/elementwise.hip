@@ -1,0 +1,298 @@
+// Elementwise kernels: SwiGLU forward/backward and rotate-half RoPE
+// forward/backward.
+//
+// Every thread handles one chunk of VEC contiguous elements per step
+// (VEC = 16/sizeof(T): one 128-bit access per tensor) and walks a grid-stride
+// loop over all chunks of the (rows x chunks_per_row) problem. Row strides are
+// honoured, so row-sliced views need no copy; the row of a chunk comes from a
+// multiply-shift division by chunks_per_row.
+//
+// Floating-point contraction is disabled so each product and sum is rounded
+// separately, the same way PyTorch's pointwise ops evaluate these formulas.
+#include "tk_common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int kBlock = 256;
+
+// sigmoid from exp(-|z|), branch-stable for any z
+// (src/tklab/kernels/_elementwise_math.py:12-18).
+__device__ __forceinline__ float stable_sigmoid(float z) {
+  const float e = expf(-fabsf(z));
+  const float d = 1.0f + e;
+  return z >= 0.f ? 1.0f / d : e / d;
+}
+
+struct Grid1D {
+  unsigned blocks;
+};
+
+inline Grid1D chunk_grid(int64_t chunks) {
+  // Enough blocks to fill 256 CUs many times over; the loop covers the rest.
+  int64_t blocks = tk::cdiv(chunks, kBlock);
+  const int64_t cap = 256 * 64;
+  if (blocks > cap) blocks = cap;
+  return {static_cast<unsigned>(blocks)};
+}
+
+// ------------------------------------------------------------------ SwiGLU
+
+// y = value * gate * sigmoid(gate)  (src/tklab/kernels/swiglu.py:44-58)
+template <typename T, int VEC>
+__global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(
+    const T* __restrict__ value, const T* __restrict__ gate, T* __restrict__ y, int chunks,
+    tk::FastDiv per_row, int64_t vs, int64_t gs, int64_t ys) {
+  for (int i = blockIdx.x * kBlock + threadIdx.x; i < chunks; i += gridDim.x * kBlock) {
+    const int row = per_row.div(i);
+    const int c = (i - row * static_cast<int>(per_row.d)) * VEC;
+    float v[VEC], g[VEC];
+    tk::load_vec<T, VEC>(value + row * vs + c, v);
+    tk::load_vec<T, VEC>(gate + row * gs + c, g);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) v[j] = v[j] * g[j] * stable_sigmoid(g[j]);
+    tk::store_vec<T, VEC>(y + row * ys + c, v);
+  }
+}
+
+// dvalue = dy * silu(g); dgate = dy * value * sigmoid(g) * (1 + g * (1 - sigmoid(g)))
+// (src/tklab/kernels/swiglu.py:82-108)
+template <typename T, int VEC>
+__global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(
+    const T* __restrict__ dy, const T* __restrict__ value, const T* __restrict__ gate,
+    T* __restrict__ dvalue, T* __restrict__ dgate, int chunks, tk::FastDiv per_row, int64_t dys,
+    int64_t vs, int64_t gs, int64_t dvs, int64_t dgs) {
+  for (int i = blockIdx.x * kBlock + threadIdx.x; i < chunks; i += gridDim.x * kBlock) {
+    const int row = per_row.div(i);
+    const int c = (i - row * static_cast<int>(per_row.d)) * VEC;
+    float d[VEC], v[VEC], g[VEC], dv[VEC], dg[VEC];
+    tk::load_vec<T, VEC>(dy + row * dys + c, d);
+    tk::load_vec<T, VEC>(value + row * vs + c, v);
+    tk::load_vec<T, VEC>(gate + row * gs + c, g);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      const float sg = stable_sigmoid(g[j]);
+      const float silu = g[j] * sg;
+      const float dsilu = sg * (1.0f + g[j] * (1.0f - sg));
+      dv[j] = d[j] * silu;
+      dg[j] = d[j] * v[j] * dsilu;
+    }
+    tk::store_vec<T, VEC>(dvalue + row * dvs + c, dv);
+    tk::store_vec<T, VEC>(dgate + row * dgs + c, dg);
+  }
+}
+
+// ------------------------------------------------------------------ RoPE
+
+// y1 = x1*cos - x2*sin; y2 = x2*cos + x1*sin  (src/tklab/kernels/rope.py:44-73)
+template <typename T, int VEC>
+__global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
+    const T* __restrict__ x, const T* __restrict__ cosv, const T* __restrict__ sinv,
+    T* __restrict__ y, int chunks, tk::FastDiv per_row, int half, int64_t xs, int64_t cs,
+    int64_t ss, int64_t ys) {
+  for (int i = blockIdx.x * kBlock + threadIdx.x; i < chunks; i += gridDim.x * kBlock) {
+    const int row = per_row.div(i);
+    const int c = (i - row * static_cast<int>(per_row.d)) * VEC;
+    float x1[VEC], x2[VEC], co[VEC], si[VEC], y1[VEC], y2[VEC];
+    const T* xr = x + row * xs;
+    tk::load_vec<T, VEC>(xr + c, x1);
+    tk::load_vec<T, VEC>(xr + half + c, x2);
+    tk::load_vec<T, VEC>(cosv + row * cs + c, co);
+    tk::load_vec<T, VEC>(sinv + row * ss + c, si);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      y1[j] = x1[j] * co[j] - x2[j] * si[j];
+      y2[j] = x2[j] * co[j] + x1[j] * si[j];
+    }
+    T* yr = y + row * ys;
+    tk::store_vec<T, VEC>(yr + c, y1);
+    tk::store_vec<T, VEC>(yr + half + c, y2);
+  }
+}
+
+// dx1 = dy1*cos + dy2*sin; dx2 = dy2*cos - dy1*sin;
+// dcos = dy1*x1 + dy2*x2; dsin = -dy1*x2 + dy2*x1  (src/tklab/kernels/rope.py:102-160)
+template <typename T, int VEC>
+__global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
+    const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ cosv,
+    const T* __restrict__ sinv, T* __restrict__ dx, T* __restrict__ dcos, T* __restrict__ dsin,
+    int chunks, tk::FastDiv per_row, int half, int64_t dys, int64_t xs, int64_t cs, int64_t ss,
+    int64_t dxs, int64_t dcs, int64_t dss) {
+  const bool need_x = dcos != nullptr || dsin != nullptr;
+  for (int i = blockIdx.x * kBlock + threadIdx.x; i < chunks; i += gridDim.x * kBlock) {
+    const int row = per_row.div(i);
+    const int c = (i - row * static_cast<int>(per_row.d)) * VEC;
+    float d1[VEC], d2[VEC], co[VEC], si[VEC], o1[VEC], o2[VEC];
+    const T* dyr = dy + row * dys;
+    tk::load_vec<T, VEC>(dyr + c, d1);
+    tk::load_vec<T, VEC>(dyr + half + c, d2);
+    tk::load_vec<T, VEC>(cosv + row * cs + c, co);
+    tk::load_vec<T, VEC>(sinv + row * ss + c, si);
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) {
+      o1[j] = d1[j] * co[j] + d2[j] * si[j];
+      o2[j] = d2[j] * co[j] - d1[j] * si[j];
+    }
+    T* dxr = dx + row * dxs;
+    tk::store_vec<T, VEC>(dxr + c, o1);
+    tk::store_vec<T, VEC>(dxr + half + c, o2);
+    if (need_x) {
+      float x1[VEC], x2[VEC];
+      const T* xr = x + row * xs;
+      tk::load_vec<T, VEC>(xr + c, x1);
+      tk::load_vec<T, VEC>(xr + half + c, x2);
+      if (dcos != nullptr) {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) o1[j] = d1[j] * x1[j] + d2[j] * x2[j];
+        tk::store_vec<T, VEC>(dcos + row * dcs + c, o1);
+      }
+      if (dsin != nullptr) {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) o2[j] = -d1[j] * x2[j] + d2[j] * x1[j];
+        tk::store_vec<T, VEC>(dsin + row * dss + c, o2);
+      }
+    }
+  }
+}
+
+bool vector_ok(int dtype, int64_t width, std::initializer_list<const void*> ptrs,
+               std::initializer_list<int64_t> strides) {
+  const int es = tk::elem_size(dtype);
+  if (width % (16 / es) != 0) return false;
+  for (const void* p : ptrs)
+    if (p != nullptr && !tk::aligned16(p)) return false;
+  for (int64_t s : strides)
+    if ((s * es) % 16 != 0) return false;
+  return true;
+}
+
+int check_problem(const char* what, int dtype, int64_t rows, int64_t width, int vec,
+                  int64_t* chunks_per_row, int64_t* chunks) {
+  if (!tk::valid_dtype(dtype)) return tk::fail("%s: unsupported dtype code %d", what, dtype);
+  if (rows <= 0 || width <= 0) return tk::fail("%s: empty problem", what);
+  *chunks_per_row = width / vec;
+  *chunks = rows * *chunks_per_row;
+  if (*chunks > INT32_MAX - 64 * kBlock * 256) return tk::fail("%s: problem too large", what);
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int tk_swiglu_fwd(int dtype, const void* value, const void* gate, void* y, int64_t rows,
+                             int64_t cols, int64_t value_row_stride, int64_t gate_row_stride,
+                             int64_t y_row_stride, void* stream) {
+  if (value == nullptr || gate == nullptr || y == nullptr) return tk::fail("swiglu_fwd: null pointer");
+  // A fully contiguous problem is one long row: no per-chunk division work.
+  if (value_row_stride == cols && gate_row_stride == cols && y_row_stride == cols) {
+    cols *= rows;
+    rows = 1;
+  }
+  const bool vok = tk::valid_dtype(dtype) &&
+                   vector_ok(dtype, cols, {value, gate, y},
+                             {value_row_stride, gate_row_stride, y_row_stride});
+  const int vec = vok ? 16 / tk::elem_size(dtype) : 1;
+  int64_t per_row, chunks;
+  if (check_problem("swiglu_fwd", dtype, rows, cols, vec, &per_row, &chunks)) return 1;
+  const tk::FastDiv div(static_cast<uint32_t>(per_row));
+  const Grid1D g = chunk_grid(chunks);
+  hipStream_t s = tk::as_stream(stream);
+  TK_DISPATCH_DTYPE(dtype, T,
+    TK_DISPATCH_VEC(T, vok,
+      hipLaunchKernelGGL((swiglu_fwd_kernel<T, VEC>), dim3(g.blocks), dim3(kBlock), 0, s,
+                         static_cast<const T*>(value), static_cast<const T*>(gate),
+                         static_cast<T*>(y), (int)chunks, div, value_row_stride,
+                         gate_row_stride, y_row_stride)));
+  return tk::check_launch("swiglu_fwd");
+}
+
+extern "C" int tk_swiglu_bwd(int dtype, const void* dy, const void* value, const void* gate,
+                             void* dvalue, void* dgate, int64_t rows, int64_t cols,
+                             int64_t dy_row_stride, int64_t value_row_stride,
+                             int64_t gate_row_stride, int64_t dvalue_row_stride,
+                             int64_t dgate_row_stride, void* stream) {
+  if (dy == nullptr || value == nullptr || gate == nullptr || dvalue == nullptr || dgate == nullptr)
+    return tk::fail("swiglu_bwd: null pointer");
+  if (dy_row_stride == cols && value_row_stride == cols && gate_row_stride == cols &&
+      dvalue_row_stride == cols && dgate_row_stride == cols) {
+    cols *= rows;
+    rows = 1;
+  }
+  const bool vok = tk::valid_dtype(dtype) &&
+                   vector_ok(dtype, cols, {dy, value, gate, dvalue, dgate},
+                             {dy_row_stride, value_row_stride, gate_row_stride,
+                              dvalue_row_stride, dgate_row_stride});
+  const int vec = vok ? 16 / tk::elem_size(dtype) : 1;
+  int64_t per_row, chunks;
+  if (check_problem("swiglu_bwd", dtype, rows, cols, vec, &per_row, &chunks)) return 1;
+  const tk::FastDiv div(static_cast<uint32_t>(per_row));
+  const Grid1D g = chunk_grid(chunks);
+  hipStream_t s = tk::as_stream(stream);
+  TK_DISPATCH_DTYPE(dtype, T,
+    TK_DISPATCH_VEC(T, vok,
+      hipLaunchKernelGGL((swiglu_bwd_kernel<T, VEC>), dim3(g.blocks), dim3(kBlock), 0, s,
+                         static_cast<const T*>(dy), static_cast<const T*>(value),
+                         static_cast<const T*>(gate), static_cast<T*>(dvalue),
+                         static_cast<T*>(dgate), (int)chunks, div, dy_row_stride,
+                         value_row_stride, gate_row_stride, dvalue_row_stride,
+                         dgate_row_stride)));
+  return tk::check_launch("swiglu_bwd");
+}
+
+extern "C" int tk_rope_fwd(int dtype, const void* x, const void* cos, const void* sin, void* y,
+                           int64_t rows, int64_t half_dim, int64_t x_row_stride,
+                           int64_t cos_row_stride, int64_t sin_row_stride, int64_t y_row_stride,
+                           void* stream) {
+  if (x == nullptr || cos == nullptr || sin == nullptr || y == nullptr)
+    return tk::fail("rope_fwd: null pointer");
+  // The second half starts half_dim elements in, so half_dim joins the strides.
+  const bool vok = tk::valid_dtype(dtype) &&
+                   vector_ok(dtype, half_dim, {x, cos, sin, y},
+                             {x_row_stride, cos_row_stride, sin_row_stride, y_row_stride});
+  const int vec = vok ? 16 / tk::elem_size(dtype) : 1;
+  int64_t per_row, chunks;
+  if (check_problem("rope_fwd", dtype, rows, half_dim, vec, &per_row, &chunks)) return 1;
+  const tk::FastDiv div(static_cast<uint32_t>(per_row));
+  const Grid1D g = chunk_grid(chunks);
+  hipStream_t s = tk::as_stream(stream);
+  TK_DISPATCH_DTYPE(dtype, T,
+    TK_DISPATCH_VEC(T, vok,
+      hipLaunchKernelGGL((rope_fwd_kernel<T, VEC>), dim3(g.blocks), dim3(kBlock), 0, s,
+                         static_cast<const T*>(x), static_cast<const T*>(cos),
+                         static_cast<const T*>(sin), static_cast<T*>(y), (int)chunks, div,
+                         (int)half_dim, x_row_stride, cos_row_stride, sin_row_stride,
+                         y_row_stride)));
+  return tk::check_launch("rope_fwd");
+}
+
+extern "C" int tk_rope_bwd(int dtype, const void* dy, const void* x, const void* cos,
+                           const void* sin, void* dx, void* dcos, void* dsin, int64_t rows,
+                           int64_t half_dim, int64_t dy_row_stride, int64_t x_row_stride,
+                           int64_t cos_row_stride, int64_t sin_row_stride, int64_t dx_row_stride,
+                           int64_t dcos_row_stride, int64_t dsin_row_stride, void* stream) {
+  if (dy == nullptr || cos == nullptr || sin == nullptr || dx == nullptr)
+    return tk::fail("rope_bwd: null pointer");
+  const bool need_x = dcos != nullptr || dsin != nullptr;
+  if (need_x && x == nullptr) return tk::fail("rope_bwd: x is required for dcos/dsin");
+  const bool vok =
+      tk::valid_dtype(dtype) &&
+      vector_ok(dtype, half_dim, {dy, need_x ? x : nullptr, cos, sin, dx, dcos, dsin},
+                {dy_row_stride, need_x ? x_row_stride : 0, cos_row_stride, sin_row_stride,
+                 dx_row_stride, dcos ? dcos_row_stride : 0, dsin ? dsin_row_stride : 0});
+  const int vec = vok ? 16 / tk::elem_size(dtype) : 1;
+  int64_t per_row, chunks;
+  if (check_problem("rope_bwd", dtype, rows, half_dim, vec, &per_row, &chunks)) return 1;
+  const tk::FastDiv div(static_cast<uint32_t>(per_row));
+  const Grid1D g = chunk_grid(chunks);
+  hipStream_t s = tk::as_stream(stream);
+  TK_DISPATCH_DTYPE(dtype, T,
+    TK_DISPATCH_VEC(T, vok,
+      hipLaunchKernelGGL((rope_bwd_kernel<T, VEC>), dim3(g.blocks), dim3(kBlock), 0, s,
+                         static_cast<const T*>(dy), static_cast<const T*>(x),
+                         static_cast<const T*>(cos), static_cast<const T*>(sin),
+                         static_cast<T*>(dx), static_cast<T*>(dcos), static_cast<T*>(dsin),
+                         (int)chunks, div, (int)half_dim, dy_row_stride, x_row_stride,
+                         cos_row_stride, sin_row_stride, dx_row_stride, dcos_row_stride,
+                         dsin_row_stride)));
+  return tk::check_launch("rope_bwd");
+}

@@ -1,0 +1,279 @@
+// RMSNorm (optionally with a fused residual add): forward, and the two-stage
+// deterministic backward.
+//
+// Forward math (src/tklab/kernels/rms_norm.py:61-78 and
+// src/tklab/kernels/residual_rms_norm.py:52-82): s = x (+ residual, rounded to
+// the storage dtype), rstd = 1/sqrt(sum(s*s)/n + eps), y = s * rstd * w.
+//
+// Backward math (src/tklab/kernels/rms_norm.py:105-133): x_hat = x*rstd,
+// g = w*dy, dx = rstd*(g - x_hat*sum(g*x_hat)/n) (+ incoming_dx),
+// dweight = sum over rows of dy*x_hat.
+//
+// The reference accumulates dweight partials under a global spin lock in an
+// order that depends on scheduling. Here each workgroup is one group: it owns
+// the rows r with r % group_size == g, keeps its column partials in registers
+// (a thread always holds the same columns), folds its waves together in LDS
+// in a fixed order and writes partial_dw[g] once. Stage 2 sums the partial
+// rows in a fixed order. Both stages are bitwise reproducible.
+#include "rows.hpp"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int kNormBlock = 256;
+
+template <typename T, int VEC, int RT, int VALS>
+__global__ __launch_bounds__(RT >= kNormBlock ? RT : kNormBlock) void rmsnorm_fwd_kernel(
+    const T* __restrict__ x, const T* __restrict__ residual, const T* __restrict__ weight,
+    T* __restrict__ residual_sum, T* __restrict__ y, float* __restrict__ rstd_out, int rows,
+    int cols, int64_t x_stride, int64_t r_stride, int64_t s_stride, int64_t y_stride, float eps) {
+  constexpr int SLOTS = RT >= kNormBlock ? 1 : kNormBlock / RT;
+  __shared__ float scratch[RT / 64];
+  const int lane = threadIdx.x % RT;
+  const int row = blockIdx.x * SLOTS + threadIdx.x / RT;
+  if (row >= rows) return;  // SLOTS > 1 only for barrier-free single-wave rows
+
+  float v[VALS];
+  tk::load_row<T, VEC, RT, VALS>(x + row * x_stride, cols, lane, v, 0.f);
+  if (residual != nullptr) {
+    float r[VALS];
+    tk::load_row<T, VEC, RT, VALS>(residual + row * r_stride, cols, lane, r, 0.f);
+#pragma unroll
+    for (int e = 0; e < VALS; ++e) v[e] = tk::round_to<T>(v[e] + r[e]);
+    if (residual_sum != nullptr)
+      tk::store_row<T, VEC, RT, VALS>(residual_sum + row * s_stride, cols, lane, v);
+  }
+
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < VALS; ++e) ss += v[e] * v[e];
+  ss = tk::group_allreduce<RT>(ss, tk::SumOp{}, scratch);
+  const float rstd = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+
+  float w[VALS];
+  tk::load_row<T, VEC, RT, VALS>(weight, cols, lane, w, 0.f);
+#pragma unroll
+  for (int e = 0; e < VALS; ++e) v[e] = v[e] * rstd * w[e];
+  tk::store_row<T, VEC, RT, VALS>(y + row * y_stride, cols, lane, v);
+  if (rstd_out != nullptr && lane == 0) rstd_out[row] = rstd;
+}
+
+// Threads per workgroup of the backward stage 1: eight single-wave row slots,
+// or one multi-wave row group.
+template <int RT>
+constexpr int bwd_block() { return RT == 64 ? 512 : RT; }
+
+template <typename T, int VEC, int RT, int VALS>
+__global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
+    T* __restrict__ dx, const T* __restrict__ dy, const T* __restrict__ incoming,
+    float* __restrict__ partial, const T* __restrict__ x, const T* __restrict__ weight,
+    const float* __restrict__ rstd, int32_t* __restrict__ counts, int rows, int cols,
+    int64_t x_stride, int64_t dy_stride, int64_t inc_stride, int64_t dx_stride, int group_size) {
+  constexpr int SLOTS = bwd_block<RT>() / RT;
+  // Cross-slot fold buffer (one float per column) and the row-reduction scratch.
+  __shared__ float fold[SLOTS > 1 ? RT * VALS : 1];
+  __shared__ float scratch[RT / 64];
+
+  const int group = blockIdx.x;
+  const int slot = threadIdx.x / RT;
+  const int lane = threadIdx.x % RT;
+  // Rows of this group: group + k*group_size, k = 0, 1, ...; slot s takes k = s mod SLOTS.
+  const int group_rows = (rows - 1 - group) / group_size + 1;
+  const int iters = (group_rows + SLOTS - 1) / SLOTS;
+
+  float w[VALS];
+  tk::load_row<T, VEC, RT, VALS>(weight, cols, lane, w, 0.f);
+  float acc[VALS];
+#pragma unroll
+  for (int e = 0; e < VALS; ++e) acc[e] = 0.f;
+
+  for (int it = 0; it < iters; ++it) {
+    const int k = it * SLOTS + slot;
+    // Every thread of a multi-wave group runs the same trip count so the block
+    // barriers inside group_allreduce line up; an idle slot computes on zeros.
+    const bool valid = k < group_rows;
+    const int64_t row = static_cast<int64_t>(group) + static_cast<int64_t>(k) * group_size;
+    float xv[VALS], g[VALS];
+    float r = 0.f;
+    if (valid) {
+      tk::load_row<T, VEC, RT, VALS>(x + row * x_stride, cols, lane, xv, 0.f);
+      tk::load_row<T, VEC, RT, VALS>(dy + row * dy_stride, cols, lane, g, 0.f);
+      r = rstd[row];
+    } else {
+#pragma unroll
+      for (int e = 0; e < VALS; ++e) xv[e] = g[e] = 0.f;
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < VALS; ++e) {
+      const float dyv = g[e];
+      xv[e] = xv[e] * r;      // x_hat
+      acc[e] += dyv * xv[e];  // dweight partial
+      g[e] = w[e] * dyv;      // g = w * dy
+      dot += g[e] * xv[e];
+    }
+    dot = tk::group_allreduce<RT>(dot, tk::SumOp{}, scratch);
+    const float mean = dot / static_cast<float>(cols);
+#pragma unroll
+    for (int e = 0; e < VALS; ++e) g[e] = r * (g[e] - xv[e] * mean);
+    if (valid) {
+      if (incoming != nullptr) {
+        float inc[VALS];
+        tk::load_row<T, VEC, RT, VALS>(incoming + row * inc_stride, cols, lane, inc, 0.f);
+#pragma unroll
+        for (int e = 0; e < VALS; ++e) g[e] += inc[e];
+      }
+      tk::store_row<T, VEC, RT, VALS>(dx + row * dx_stride, cols, lane, g);
+    }
+  }
+
+  float* out = partial + static_cast<int64_t>(group) * cols;
+  if constexpr (SLOTS == 1) {
+#pragma unroll
+    for (int e = 0; e < VALS; ++e) {
+      const int c = tk::row_column<VEC, RT>(e, lane);
+      if (c < cols) out[c] = acc[e];
+    }
+  } else {
+    // Fold the slots in increasing slot order: slot 0 writes, the others add in turn.
+    for (int s = 0; s < SLOTS; ++s) {
+      if (slot == s) {
+#pragma unroll
+        for (int e = 0; e < VALS; ++e) {
+          const int c = tk::row_column<VEC, RT>(e, lane);
+          if (c < cols) fold[c] = (s == 0) ? acc[e] : fold[c] + acc[e];
+        }
+      }
+      __syncthreads();
+    }
+    for (int c = threadIdx.x; c < cols; c += bwd_block<RT>()) out[c] = fold[c];
+  }
+  if (threadIdx.x == 0) counts[group] = 1;
+}
+
+constexpr int kStage2Waves = 8;
+
+// dw[c] = sum over g of partial[g][c]. Block = 64 columns x 8 waves; wave w
+// sums a contiguous slice of g in increasing order, then the eight slice sums
+// are added in wave order.
+template <typename T>
+__global__ __launch_bounds__(64 * kStage2Waves) void rmsnorm_bwd_stage2_kernel(
+    const float* __restrict__ partial, T* __restrict__ dw, int group_count, int cols) {
+  __shared__ float slices[kStage2Waves][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
+  const int per = (group_count + kStage2Waves - 1) / kStage2Waves;
+  const int g0 = wave * per;
+  const int g1 = min(group_count, g0 + per);
+  float s = 0.f;
+  if (c < cols) {
+    for (int g = g0; g < g1; ++g) s += partial[static_cast<int64_t>(g) * cols + c];
+  }
+  slices[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && c < cols) {
+    float t = slices[0][lane];
+#pragma unroll
+    for (int w = 1; w < kStage2Waves; ++w) t += slices[w][lane];
+    dw[c] = tk::from_f32<T>(t);
+  }
+}
+
+bool rows_vector_ok(int dtype, int64_t cols, std::initializer_list<const void*> ptrs,
+                    std::initializer_list<int64_t> strides) {
+  const int es = tk::elem_size(dtype);
+  if (cols % (16 / es) != 0) return false;
+  for (const void* p : ptrs)
+    if (p != nullptr && !tk::aligned16(p)) return false;
+  for (int64_t s : strides)
+    if ((s * es) % 16 != 0) return false;
+  return true;
+}
+
+int check_rows(const char* what, int dtype, int64_t rows, int64_t cols, tk::RowShape* shape) {
+  if (!tk::valid_dtype(dtype)) return tk::fail("%s: unsupported dtype code %d", what, dtype);
+  if (rows <= 0 || cols <= 0) return tk::fail("%s: empty problem", what);
+  if (rows > INT32_MAX) return tk::fail("%s: too many rows", what);
+  if (cols * tk::elem_size(dtype) > 65536 || !tk::pick_row_shape(cols, shape))
+    return tk::fail("%s: feature row exceeds the 65536-byte fused limit", what);
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int tk_rmsnorm_fwd(int dtype, const void* x, const void* residual, const void* weight,
+                              void* residual_sum, void* y, float* rstd, int64_t rows, int64_t cols,
+                              int64_t x_row_stride, int64_t residual_row_stride,
+                              int64_t residual_sum_row_stride, int64_t y_row_stride, float eps,
+                              void* stream) {
+  tk::RowShape shape;
+  if (check_rows("rmsnorm_fwd", dtype, rows, cols, &shape)) return 1;
+  if (x == nullptr || weight == nullptr || y == nullptr) return tk::fail("rmsnorm_fwd: null pointer");
+  if (!(eps > 0.f)) return tk::fail("rmsnorm_fwd: eps must be finite and positive");
+  const bool vector_ok = rows_vector_ok(
+      dtype, cols, {x, residual, weight, residual_sum, y},
+      {x_row_stride, residual ? residual_row_stride : 0, residual_sum ? residual_sum_row_stride : 0,
+       y_row_stride});
+  const int slots = shape.rt >= kNormBlock ? 1 : kNormBlock / shape.rt;
+  const dim3 grid(static_cast<unsigned>(tk::cdiv(rows, slots)));
+  const dim3 block(shape.rt >= kNormBlock ? shape.rt : kNormBlock);
+  hipStream_t s = tk::as_stream(stream);
+  TK_DISPATCH_DTYPE(dtype, T,
+    TK_DISPATCH_VEC(T, vector_ok,
+      TK_DISPATCH_ROW_SHAPE(shape,
+        hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, VEC, RT, VALS>), grid, block, 0, s,
+                           static_cast<const T*>(x), static_cast<const T*>(residual),
+                           static_cast<const T*>(weight), static_cast<T*>(residual_sum),
+                           static_cast<T*>(y), rstd, (int)rows, (int)cols, x_row_stride,
+                           residual_row_stride, residual_sum_row_stride, y_row_stride, eps))));
+  return tk::check_launch("rmsnorm_fwd");
+}
+
+extern "C" int tk_rmsnorm_bwd_stage1(int dtype, void* dx, const void* dy, const void* incoming_dx,
+                                     float* partial_dw, const void* x, const void* weight,
+                                     const float* rstd, int32_t* locks, int64_t rows, int64_t cols,
+                                     int64_t x_row_stride, int64_t dy_row_stride,
+                                     int64_t incoming_dx_row_stride, int64_t dx_row_stride,
+                                     int64_t group_size, void* stream) {
+  tk::RowShape shape;
+  if (check_rows("rmsnorm_bwd_stage1", dtype, rows, cols, &shape)) return 1;
+  if (dx == nullptr || dy == nullptr || partial_dw == nullptr || x == nullptr ||
+      weight == nullptr || rstd == nullptr || locks == nullptr)
+    return tk::fail("rmsnorm_bwd_stage1: null pointer");
+  if (group_size <= 0 || group_size > INT32_MAX)
+    return tk::fail("rmsnorm_bwd_stage1: group_size must be positive");
+  const int64_t group_count = group_size < rows ? group_size : rows;
+  const bool vector_ok = rows_vector_ok(
+      dtype, cols, {dx, dy, incoming_dx, x, weight},
+      {x_row_stride, dy_row_stride, incoming_dx ? incoming_dx_row_stride : 0, dx_row_stride});
+  const dim3 grid(static_cast<unsigned>(group_count));
+  hipStream_t s = tk::as_stream(stream);
+  int32_t* counts = locks + group_size;
+  TK_DISPATCH_DTYPE(dtype, T,
+    TK_DISPATCH_VEC(T, vector_ok,
+      TK_DISPATCH_ROW_SHAPE(shape,
+        hipLaunchKernelGGL((rmsnorm_bwd_stage1_kernel<T, VEC, RT, VALS>), grid,
+                           dim3(bwd_block<RT>()), 0, s, static_cast<T*>(dx),
+                           static_cast<const T*>(dy), static_cast<const T*>(incoming_dx),
+                           partial_dw, static_cast<const T*>(x), static_cast<const T*>(weight),
+                           rstd, counts, (int)rows, (int)cols, x_row_stride, dy_row_stride,
+                           incoming_dx_row_stride, dx_row_stride, (int)group_size))));
+  return tk::check_launch("rmsnorm_bwd_stage1");
+}
+
+extern "C" int tk_rmsnorm_bwd_stage2(int dtype, const float* partial_dw, void* dw,
+                                     int64_t group_count, int64_t cols, void* stream) {
+  if (!tk::valid_dtype(dtype)) return tk::fail("rmsnorm_bwd_stage2: unsupported dtype code %d", dtype);
+  if (partial_dw == nullptr || dw == nullptr) return tk::fail("rmsnorm_bwd_stage2: null pointer");
+  if (group_count <= 0 || cols <= 0 || group_count > INT32_MAX || cols > INT32_MAX ||
+      group_count * cols > INT32_MAX)
+    return tk::fail("rmsnorm_bwd_stage2: bad partial shape");
+  const dim3 grid(static_cast<unsigned>(tk::cdiv(cols, 64)));
+  hipStream_t s = tk::as_stream(stream);
+  TK_DISPATCH_DTYPE(dtype, T,
+    hipLaunchKernelGGL((rmsnorm_bwd_stage2_kernel<T>), grid, dim3(64 * kStage2Waves), 0, s,
+                       partial_dw, static_cast<T*>(dw), (int)group_count, (int)cols));
+  return tk::check_launch("rmsnorm_bwd_stage2");
+}

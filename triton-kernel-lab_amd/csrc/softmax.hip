@@ -1,0 +1,70 @@
+// Row-wise softmax, one row per thread group, the whole row in registers.
+//
+// Math follows the reference kernel (src/tklab/kernels/fused_softmax.py:32-39):
+// float32 values, masked tail = -inf, shifted = x - rowmax, numerator = exp,
+// y = numerator / rowsum (here numerator * (1/rowsum)), stored in the input dtype.
+// One HBM read and one HBM write per element.
+#include "rows.hpp"
+
+namespace {
+
+template <typename T, int VEC, int RT, int VALS>
+__global__ __launch_bounds__(RT >= 256 ? RT : 256) void softmax_fwd_kernel(
+    const T* __restrict__ x, T* __restrict__ y, int rows, int cols, int64_t x_stride,
+    int64_t y_stride) {
+  constexpr int SLOTS = RT >= 256 ? 1 : 256 / RT;
+  __shared__ float scratch[RT / 64];
+  const int lane = threadIdx.x % RT;
+  const int row = blockIdx.x * SLOTS + threadIdx.x / RT;
+  // SLOTS > 1 only for single-wave rows, which never reach a block barrier.
+  if (row >= rows) return;
+
+  float v[VALS];
+  tk::load_row<T, VEC, RT, VALS>(x + row * x_stride, cols, lane, v, -INFINITY);
+
+  float m = v[0];
+#pragma unroll
+  for (int e = 1; e < VALS; ++e) m = fmaxf(m, v[e]);
+  m = tk::group_allreduce<RT>(m, tk::MaxOp{}, scratch);
+
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < VALS; ++e) {
+    v[e] = expf(v[e] - m);
+    s += v[e];
+  }
+  s = tk::group_allreduce<RT>(s, tk::SumOp{}, scratch);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int e = 0; e < VALS; ++e) v[e] *= inv;
+  tk::store_row<T, VEC, RT, VALS>(y + row * y_stride, cols, lane, v);
+}
+
+}  // namespace
+
+extern "C" int tk_softmax_fwd(int dtype, const void* x, void* y, int64_t rows, int64_t cols,
+                              int64_t x_row_stride, int64_t y_row_stride, void* stream) {
+  if (!tk::valid_dtype(dtype)) return tk::fail("softmax: unsupported dtype code %d", dtype);
+  if (x == nullptr || y == nullptr) return tk::fail("softmax: null pointer");
+  if (rows <= 0 || cols <= 0) return tk::fail("softmax: empty problem");
+  if (rows > INT32_MAX) return tk::fail("softmax: too many rows");
+  tk::RowShape shape;
+  if (cols > 65536 || !tk::pick_row_shape(cols, &shape))
+    return tk::fail("softmax: %lld columns exceed the 65536-column single-pass limit",
+                    (long long)cols);
+  const int es = tk::elem_size(dtype);
+  const int vec = 16 / es;
+  const bool vector_ok = tk::aligned16(x) && tk::aligned16(y) && cols % vec == 0 &&
+                         (x_row_stride * es) % 16 == 0 && (y_row_stride * es) % 16 == 0;
+  const int slots = shape.rt >= 256 ? 1 : 256 / shape.rt;
+  const dim3 grid(static_cast<unsigned>(tk::cdiv(rows, slots)));
+  const dim3 block(shape.rt >= 256 ? shape.rt : 256);
+  hipStream_t s = tk::as_stream(stream);
+  TK_DISPATCH_DTYPE(dtype, T,
+    TK_DISPATCH_VEC(T, vector_ok,
+      TK_DISPATCH_ROW_SHAPE(shape,
+        hipLaunchKernelGGL((softmax_fwd_kernel<T, VEC, RT, VALS>), grid, block, 0, s,
+                           static_cast<const T*>(x), static_cast<T*>(y), (int)rows, (int)cols,
+                           x_row_stride, y_row_stride))));
+  return tk::check_launch("softmax");
+}

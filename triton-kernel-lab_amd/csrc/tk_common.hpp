@@ -1,0 +1,179 @@
+// Shared device and host helpers for the gfx950 kernels of libtklab_hip.so.
+//
+// Storage types are float, _Float16 and __bf16; all arithmetic is float32.
+// Conversions to the 16-bit types round to nearest even (the hardware
+// v_cvt instructions), which is also how PyTorch rounds.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tklab_hip.h"
+
+namespace tk {
+
+// ---------------------------------------------------------------- host side
+
+// Record a failure message for tk_last_error() and return 1.
+int fail(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+// After a launch: turn a pending HIP error into a failure.
+int check_launch(const char* what);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int elem_size(int dtype) { return dtype == TK_DTYPE_F32 ? 4 : 2; }
+
+inline bool valid_dtype(int dtype) {
+  return dtype == TK_DTYPE_F32 || dtype == TK_DTYPE_F16 || dtype == TK_DTYPE_BF16;
+}
+
+// ---------------------------------------------------------------- conversions
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(_Float16 v) { return static_cast<float>(v); }
+__device__ __forceinline__ float to_f32(__bf16 v) { return static_cast<float>(v); }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v) { return static_cast<T>(v); }
+
+// Round a float32 value to T and back (T = float is the identity).
+template <typename T>
+__device__ __forceinline__ float round_to(float v) { return to_f32(from_f32<T>(v)); }
+
+// ---------------------------------------------------------------- vector IO
+
+template <typename T, int N>
+struct alignas(sizeof(T) * N) Vec {
+  T v[N];
+};
+
+// Load N consecutive elements starting at p into f[0..N). For N*sizeof(T) == 16
+// the pointer must be 16-byte aligned; the load is one 128-bit access.
+template <typename T, int N>
+__device__ __forceinline__ void load_vec(const T* p, float* f) {
+  Vec<T, N> r = *reinterpret_cast<const Vec<T, N>*>(p);
+#pragma unroll
+  for (int j = 0; j < N; ++j) f[j] = to_f32(r.v[j]);
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_vec(T* p, const float* f) {
+  Vec<T, N> r;
+#pragma unroll
+  for (int j = 0; j < N; ++j) r.v[j] = from_f32<T>(f[j]);
+  *reinterpret_cast<Vec<T, N>*>(p) = r;
+}
+
+// ---------------------------------------------------------------- wave64 reductions
+//
+// Butterfly all-reduce: xor 1 and xor 2 with DPP quad permutes, then the
+// 8-lane half-mirror and 16-lane mirror (after the quad steps every lane of a
+// quad holds the quad's value, so mirroring pairs distinct quads), xor 16 with
+// ds_swizzle, and the two 32-lane halves combined through readlane. Every
+// lane ends with the full result.
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kSwizzleXor16 = 0x401F;  // bit mode: and 0x1F, or 0, xor 0x10
+
+struct SumOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+struct MaxOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+template <typename Op>
+__device__ __forceinline__ float wave_allreduce(float v, Op op) {
+  v = op(v, dpp_f32<kDppQuadXor1>(v));
+  v = op(v, dpp_f32<kDppQuadXor2>(v));
+  v = op(v, dpp_f32<kDppRowHalfMirror>(v));
+  v = op(v, dpp_f32<kDppRowMirror>(v));
+  v = op(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), kSwizzleXor16)));
+  const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  return op(lo, hi);
+}
+
+// All-reduce over a group of RT threads (RT a multiple of 64). For RT > 64 the
+// per-wave results meet in `scratch` (RT/64 floats of LDS); the call contains
+// two block barriers, so every thread of the block must reach it.
+template <int RT, typename Op>
+__device__ __forceinline__ float group_allreduce(float v, Op op, float* scratch) {
+  v = wave_allreduce(v, op);
+  if constexpr (RT > 64) {
+    constexpr int W = RT / 64;
+    const int wave = (threadIdx.x % RT) / 64;
+    if ((threadIdx.x & 63) == 0) scratch[wave] = v;
+    __syncthreads();
+    float r = scratch[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) r = op(r, scratch[w]);
+    __syncthreads();
+    v = r;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------- integer division
+
+// Division by a runtime constant d >= 1 for 0 <= n < 2^31 (round-up multiply
+// and shift, Granlund & Montgomery 1994).
+struct FastDiv {
+  uint32_t d, m, s;
+  FastDiv() = default;
+  explicit FastDiv(uint32_t divisor) : d(divisor), m(0), s(0) {
+    while ((1u << s) < d) ++s;
+    m = static_cast<uint32_t>(((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1);
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    const uint64_t t = __umulhi(n, m);
+    return static_cast<uint32_t>((t + n) >> s);
+  }
+};
+
+}  // namespace tk
+
+// Dispatch on a runtime dtype code to a templated functor call.
+#define TK_DISPATCH_DTYPE(dtype, T, ...)                      \
+  switch (dtype) {                                            \
+    case TK_DTYPE_F32: {                                      \
+      using T = float;                                        \
+      __VA_ARGS__;                                            \
+      break;                                                  \
+    }                                                         \
+    case TK_DTYPE_F16: {                                      \
+      using T = _Float16;                                     \
+      __VA_ARGS__;                                            \
+      break;                                                  \
+    }                                                         \
+    case TK_DTYPE_BF16: {                                     \
+      using T = __bf16;                                       \
+      __VA_ARGS__;                                            \
+      break;                                                  \
+    }                                                         \
+    default:                                                  \
+      return tk::fail("unsupported dtype code %d", (int)dtype); \
+  }
+
+// Expands `__VA_ARGS__` with constexpr VEC = 16/sizeof(T) when `vector_ok`, else 1.
+#define TK_DISPATCH_VEC(T, vector_ok, ...)                         \
+  if (vector_ok) {                                                 \
+    constexpr int VEC = 16 / int(sizeof(T));                       \
+    __VA_ARGS__;                                                   \
+  } else {                                                         \
+    constexpr int VEC = 1;                                         \
+    __VA_ARGS__;                                                   \
+  }

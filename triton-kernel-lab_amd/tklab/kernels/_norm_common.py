@@ -1,0 +1,67 @@
+"""Launch policy shared by the RMSNorm kernels.
+
+Same role as the reference's ``src/tklab/kernels/_norm_common.py:17-75``: one
+place for the epsilon rule, the single-pass row budget, the row launch shape
+and the number of dweight partial groups. The shape and group numbers are the
+MI355X ones used by ``csrc/rmsnorm.hip``.
+"""
+
+from __future__ import annotations
+
+import math
+
+# A normalized row is held in registers by one thread group, so it must fit
+# the single-pass budget (reference ``_norm_common.py:17``).
+MAX_FEATURE_BYTES = 65_536
+EPS = 1e-5
+
+# Groups of the backward dweight reduction: one workgroup per group, and
+# MI355X has 256 compute units.
+DEFAULT_GROUPS = 256
+
+
+def validate_epsilon(eps: float) -> None:
+    """Require a finite, strictly positive epsilon (reference ``_norm_common.py:25-38``)."""
+    if not math.isfinite(eps) or eps <= 0:
+        raise ValueError("eps must be finite and positive")
+
+
+def row_launch_shape(columns: int, element_size: int) -> tuple[int, int]:
+    """Return ``(threads_per_row, values_per_thread)`` for a row width.
+
+    Mirrors ``pick_row_shape`` in ``csrc/rows.hpp``: one 64-lane wave per row
+    up to 4096 columns, 256 threads up to 16384, 1024 threads up to 65536, with
+    16 or 64 register-resident values per thread.
+
+    Raises:
+        ValueError: if the row exceeds the single-pass budget.
+    """
+    if columns * element_size > MAX_FEATURE_BYTES:
+        raise ValueError("feature dimension exceeds the fused normalization limit")
+    for threads in (64, 256, 1024):
+        for values in (16, 64):
+            if columns <= threads * values:
+                return threads, values
+    raise ValueError("feature dimension exceeds the fused normalization limit")
+
+
+def block_size_and_warps(columns: int, element_size: int) -> tuple[int, int]:
+    """Return ``(columns covered per row group, wavefronts per row group)``.
+
+    Keeps the reference's helper name (``_norm_common.py:41-60``); on MI355X
+    the "warp" count is the number of 64-lane wavefronts sharing one row.
+    """
+    threads, values = row_launch_shape(columns, element_size)
+    return threads * values, threads // 64
+
+
+def group_size_m(columns: int) -> int:
+    """Number of dweight partial groups for the backward stage 1.
+
+    The reference trades lock contention against stage-two work
+    (``_norm_common.py:63-75``). Without locks the only concern is filling the
+    GPU while keeping the float32 partial buffer small, so every width uses one
+    group per compute unit.
+    """
+    del columns
+    return DEFAULT_GROUPS
