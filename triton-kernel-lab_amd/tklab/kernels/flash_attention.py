@@ -1,0 +1,347 @@
+"""Flash attention forward and recompute backward on the HIP MFMA kernels.
+
+Contract of ``src/tklab/kernels/flash_attention.py``: ``attention_causal`` and
+``attention_noncausal`` on contiguous ``(batch, heads, sequence, head_dim)``
+Q/K/V of one shape and dtype, scale ``1/sqrt(head_dim)``, base-2 online
+softmax, a float32 base-2 log-sum-exp saved for the backward, and a
+three-launch backward (delta preprocess, dK/dV, dQ). Validation order and
+messages follow ``flash_attention.py:267-288``. Beyond the reference: bfloat16
+as well as float16, head_dim 128 as well as 64, and any sequence length
+without a per-length recompile.
+
+The registry keeps the reference's spec shape (batch 1, 16 heads, head_dim
+64, ``flash_attention.py:27-29``) so its FLOP model and tests carry over.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any, cast
+
+import torch
+import torch.nn.functional as F
+from torch.autograd.function import once_differentiable
+
+from tklab import _hip
+from tklab.harness.addressing import assert_int32_addressable
+from tklab.harness.tolerances import assert_relative_frobenius
+from tklab.registry import (
+    BenchmarkMetadataFn,
+    BenchmarkScalar,
+    CostFn,
+    KernelSpec,
+    LaunchFn,
+    TensorArgs,
+    TensorFn,
+    register,
+)
+
+_BATCH = 1
+_HEADS = 16
+_HEAD_DIM = 64
+_HEAD_DIMS = (64, 128)
+_DTYPES = (torch.float16, torch.bfloat16)
+_LOG2_E = 1.4426950408889634
+
+# Tile configuration of csrc/attention.hip (forward / backward).
+FORWARD_TILE = {"block_m": 256, "block_n": 64, "num_warps": 4, "num_stages": 2}
+BACKWARD_TILE = {"block_m": 128, "block_n": 64}
+
+
+def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    """Dense self-attention contract (reference ``flash_attention.py:267-288``)."""
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("attention expects Q, K, and V shaped (batch, heads, sequence, dim)")
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("Q, K, and V must have identical shapes")
+    if 0 in q.shape:
+        raise ValueError("attention does not support empty dimensions")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("Q, K, and V must be on the same device")
+    if q.device.type != "cuda":
+        raise ValueError("attention requires CUDA (ROCm/HIP) tensors")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError("Q, K, and V must have the same dtype")
+    if q.dtype not in _DTYPES:
+        raise ValueError("attention supports float16 and bfloat16 inputs only")
+    if q.shape[-1] not in _HEAD_DIMS:
+        raise ValueError(f"attention requires head_dim in {_HEAD_DIMS}")
+    for name, tensor in (("Q", q), ("K", k), ("V", v)):
+        if not tensor.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+        assert_int32_addressable(tensor, name=name)
+
+
+def _make_output(args: TensorArgs) -> torch.Tensor:
+    """Dense attention output."""
+    return torch.empty_like(args[0])
+
+
+def _strides(t: torch.Tensor) -> Any:
+    """(batch, head, sequence) element strides as a C ``int64_t[3]``."""
+    return _hip.int64_array(list(t.stride()[:3]))
+
+
+def _launch_forward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    output: torch.Tensor,
+    softmax_lse: torch.Tensor,
+    *,
+    causal: bool,
+    store_lse: bool,
+) -> None:
+    """Forward into preallocated buffers; ``softmax_lse`` is written only with ``store_lse``."""
+    _validate(q, k, v)
+    if output.shape != q.shape or output.device != q.device or output.dtype != q.dtype:
+        raise ValueError("attention output metadata must match Q")
+    if not output.is_contiguous():
+        raise ValueError("attention output must be contiguous")
+    batch, heads, n_ctx, head_dim = q.shape
+    if store_lse:
+        if (
+            softmax_lse.shape != (batch, heads, n_ctx)
+            or softmax_lse.device != q.device
+            or softmax_lse.dtype != torch.float32
+            or not softmax_lse.is_contiguous()
+        ):
+            raise ValueError("attention log-sum-exp buffer must be contiguous float32 BxHxN")
+        assert_int32_addressable(softmax_lse, name="log-sum-exp buffer")
+    _hip.call(
+        "tk_attn_fwd",
+        _hip.dtype_code(q.dtype),
+        q.data_ptr(),
+        k.data_ptr(),
+        v.data_ptr(),
+        output.data_ptr(),
+        softmax_lse.data_ptr() if store_lse else None,
+        batch,
+        heads,
+        n_ctx,
+        head_dim,
+        _strides(q),
+        _strides(k),
+        _strides(v),
+        _strides(output),
+        1.0 / math.sqrt(head_dim),
+        int(causal),
+        _hip.stream_of(q),
+    )
+
+
+def _launch_factory(*, causal: bool) -> LaunchFn:
+    """Allocation-free inference launcher for one masking mode."""
+
+    def launch(args: TensorArgs, output: torch.Tensor) -> None:
+        q, k, v = args
+        _launch_forward(q, k, v, output, output, causal=causal, store_lse=False)
+
+    return launch
+
+
+_launch_noncausal = _launch_factory(causal=False)
+_launch_causal = _launch_factory(causal=True)
+
+
+def _launch_backward_into(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    output: torch.Tensor,
+    softmax_lse: torch.Tensor,
+    do: torch.Tensor,
+    delta: torch.Tensor,
+    dq: torch.Tensor,
+    dk: torch.Tensor,
+    dv: torch.Tensor,
+    *,
+    causal: bool,
+) -> None:
+    """The three backward launches into caller-provided buffers (all BxHxNxD contiguous)."""
+    batch, heads, n_ctx, head_dim = q.shape
+    code = _hip.dtype_code(q.dtype)
+    strides = _strides(q)
+    stream = _hip.stream_of(q)
+    scale = 1.0 / math.sqrt(head_dim)
+    _hip.call(
+        "tk_attn_bwd_preprocess", code, output.data_ptr(), do.data_ptr(), delta.data_ptr(),
+        batch, heads, n_ctx, head_dim, strides, stream,
+    )
+    _hip.call(
+        "tk_attn_bwd_dkdv", code, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+        dk.data_ptr(), dv.data_ptr(), softmax_lse.data_ptr(), delta.data_ptr(),
+        batch, heads, n_ctx, head_dim, strides, scale, int(causal), stream,
+    )
+    _hip.call(
+        "tk_attn_bwd_dq", code, q.data_ptr(), k.data_ptr(), v.data_ptr(), do.data_ptr(),
+        dq.data_ptr(), softmax_lse.data_ptr(), delta.data_ptr(),
+        batch, heads, n_ctx, head_dim, strides, scale, int(causal), stream,
+    )
+
+
+def _launch_backward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    output: torch.Tensor,
+    softmax_lse: torch.Tensor,
+    do: torch.Tensor,
+    *,
+    causal: bool,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Recompute backward; returns dQ, dK, dV (reference ``flash_attention.py:536-607``)."""
+    if do.shape != q.shape or do.device != q.device or do.dtype != q.dtype:
+        raise ValueError("attention upstream gradient metadata must match Q")
+    do = do.contiguous()
+    batch, heads, n_ctx, _ = q.shape
+    delta = torch.empty((batch, heads, n_ctx), dtype=torch.float32, device=q.device)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    _launch_backward_into(q, k, v, output, softmax_lse, do, delta, dq, dk, dv, causal=causal)
+    return dq, dk, dv
+
+
+class _FlashAttentionFunction(torch.autograd.Function):
+    """Autograd bridge: saves Q, K, V, O and the base-2 LSE."""
+
+    @staticmethod
+    def forward(
+        ctx: Any, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool
+    ) -> torch.Tensor:
+        _validate(q, k, v)
+        output = torch.empty_like(q)
+        batch, heads, n_ctx, _ = q.shape
+        softmax_lse = torch.empty((batch, heads, n_ctx), dtype=torch.float32, device=q.device)
+        _launch_forward(q, k, v, output, softmax_lse, causal=causal, store_lse=True)
+        ctx.save_for_backward(q, k, v, output, softmax_lse)
+        ctx.causal = causal
+        return output
+
+    @staticmethod
+    @once_differentiable
+    def backward(
+        ctx: Any, do: torch.Tensor
+    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, None]:
+        q, k, v, output, softmax_lse = ctx.saved_tensors
+        dq, dk, dv = _launch_backward(q, k, v, output, softmax_lse, do, causal=ctx.causal)
+        return dq, dk, dv, None
+
+
+def _attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool) -> torch.Tensor:
+    """Inference skips the LSE store; training goes through autograd."""
+    _validate(q, k, v)
+    needs_grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
+    if not needs_grad:
+        output = torch.empty_like(q)
+        _launch_forward(q, k, v, output, output, causal=causal, store_lse=False)
+        return output
+    return cast(torch.Tensor, _FlashAttentionFunction.apply(q, k, v, causal))
+
+
+def attention_noncausal(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """Dense non-causal scaled dot-product attention with autograd."""
+    return _attention(q, k, v, causal=False)
+
+
+def attention_causal(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """Dense causal scaled dot-product attention with autograd."""
+    return _attention(q, k, v, causal=True)
+
+
+def _reference_factory(*, causal: bool) -> TensorFn:
+    """PyTorch SDPA reference."""
+
+    def reference(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        return F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+
+    return reference
+
+
+def _make_inputs(sequence_length: int, device: torch.device, dtype: torch.dtype) -> TensorArgs:
+    """Contiguous (1, 16, N, 64) self-attention inputs."""
+    shape = (_BATCH, _HEADS, sequence_length, _HEAD_DIM)
+    return tuple(torch.randn(shape, device=device, dtype=dtype) for _ in range(3))
+
+
+def _make_adversarial(device: torch.device) -> TensorArgs:
+    """Sequence length 1000: partial query and key tiles."""
+    return _make_inputs(1000, device, torch.float16)
+
+
+def _assert_attention(output: torch.Tensor, reference: torch.Tensor) -> None:
+    """Relative Frobenius error below 2e-2 (reference ``flash_attention.py:732-734``)."""
+    assert_relative_frobenius(output, reference, max_relative_error=2e-2)
+
+
+def attention_flops(batch: int, heads: int, n_ctx: int, head_dim: int, *, causal: bool) -> int:
+    """Two matmuls over the attended (query, key) pairs: ``4 * B * H * pairs * D``."""
+    pairs = n_ctx * (n_ctx + 1) // 2 if causal else n_ctx * n_ctx
+    return 4 * batch * heads * pairs * head_dim
+
+
+def _flops_factory(*, causal: bool) -> CostFn:
+    """FLOP model of the registered (1, 16, N, 64) problem."""
+
+    def flops(sequence_length: int, _dtype: torch.dtype) -> int:
+        return attention_flops(_BATCH, _HEADS, sequence_length, _HEAD_DIM, causal=causal)
+
+    return flops
+
+
+def _metadata_factory(*, causal: bool) -> BenchmarkMetadataFn:
+    """Tile configuration and problem constants in the reference's keys."""
+
+    def metadata(_size: int, _dtype: torch.dtype) -> dict[str, BenchmarkScalar]:
+        return {**FORWARD_TILE, "heads": _HEADS, "head_dim": _HEAD_DIM, "causal": causal,
+                "mma_opcode": "v_mfma_f32_32x32x16"}
+
+    return metadata
+
+
+_SIZES = (512, 1024, 2048, 4096, 8192)
+
+ATTENTION_NONCAUSAL = register(
+    KernelSpec(
+        name="attention_noncausal",
+        description="Flash Attention forward with online softmax and no mask.",
+        triton_fn=attention_noncausal,
+        launch_fn=_launch_noncausal,
+        ref_fn=_reference_factory(causal=False),
+        make_inputs=_make_inputs,
+        make_output=_make_output,
+        make_adversarial=_make_adversarial,
+        sizes=_SIZES,
+        correctness_sizes=(128, 512),
+        bound="compute",
+        flops=_flops_factory(causal=False),
+        dtypes=(torch.float16, torch.bfloat16),
+        assert_fn=_assert_attention,
+        benchmark_metadata=_metadata_factory(causal=False),
+        compute_mode="attention_fp16_fp32acc",
+        supports_interpreter=False,
+    )
+)
+
+ATTENTION_CAUSAL = register(
+    KernelSpec(
+        name="attention_causal",
+        description="Flash Attention forward with causal masking and heaviest-first blocks.",
+        triton_fn=attention_causal,
+        launch_fn=_launch_causal,
+        ref_fn=_reference_factory(causal=True),
+        make_inputs=_make_inputs,
+        make_output=_make_output,
+        make_adversarial=_make_adversarial,
+        sizes=_SIZES,
+        correctness_sizes=(128, 512),
+        bound="compute",
+        flops=_flops_factory(causal=True),
+        dtypes=(torch.float16, torch.bfloat16),
+        assert_fn=_assert_attention,
+        benchmark_metadata=_metadata_factory(causal=True),
+        compute_mode="attention_fp16_fp32acc",
+        supports_interpreter=False,
+    )
+)
