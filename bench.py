@@ -1,0 +1,358 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X tklab kernels; prints one JSON line.
+
+Step (the timed unit): BASELINE config 2 — residual RMSNorm forward + backward
+on bfloat16 x, residual [16384, 4096] (weight ~ N(1, 0.02), eps 1e-6, both
+upstream gradients ~ N(0, 1)), i.e. three launches into preallocated buffers:
+tk_rmsnorm_fwd (with residual), tk_rmsnorm_bwd_stage1 (with the incoming sum
+gradient) and tk_rmsnorm_bwd_stage2. Algorithmic bytes per step:
+forward 4*M*D*2 + backward 4*M*D*2 = 1 073 741 824 (weight, rstd and the
+float32 partial rows are not counted).
+
+``value`` is that step's throughput in GB/s with inputs resident in HBM.
+``roofline`` prices the dominant kernel of the step against 8 TB/s: its
+algorithmic bytes per launch over its average duration, measured with events
+on the launch stream inside the timed region. ``traffic`` comes from the
+committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when present.
+``cpu_baseline`` times the CPU oracle (oracle/tklab_oracle.c) on a bounded
+row sample of the same workload on the host cores.
+``kernels`` times every other BASELINE configuration (softmax, SwiGLU, RoPE,
+GEMM, attention) per kernel with a 1 GiB cache flush before each launch.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "triton-kernel-lab_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "% of roofline: HBM GB/s (norm/softmax) + TFLOP/s (GEMM, causal FA fwd+bwd)"
+HBM_PEAK_GBPS = 8000.0
+MFMA_PEAK_TFLOPS = {"float16": 2500.0, "bfloat16": 2500.0}
+ROWS, COLS = 16384, 4096
+EPS = 1e-6
+TRAFFIC_SUMMARY = ROOT / "profiles" / "rmsnorm_bwd_stage1_traffic.txt"
+
+
+def parse_args() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-kernels", action="store_true", help="skip the per-config kernel table")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="first run three 1 GiB device copies (reference kernel for PMC byte counts)")
+    return p.parse_args()
+
+
+def _traffic_from_summary() -> float | None:
+    """HBM bytes per stage-1 launch from the committed rocprofv3 PMC summary."""
+    if not TRAFFIC_SUMMARY.is_file():
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", TRAFFIC_SUMMARY.read_text(), re.M)
+    return float(m.group(1)) if m else None
+
+
+class Step:
+    """Preallocated buffers and the three launches of one residual-RMSNorm fwd+bwd step."""
+
+    def __init__(self, torch, device) -> None:
+        from tklab.kernels import residual_rms_norm as rrn
+        from tklab.kernels import rms_norm as rn
+
+        self.rrn, self.rn = rrn, rn
+        g = torch.Generator(device=device).manual_seed(0)
+        bf16 = torch.bfloat16
+        self.x = torch.randn(ROWS, COLS, device=device, dtype=bf16, generator=g)
+        self.r = torch.randn(ROWS, COLS, device=device, dtype=bf16, generator=g)
+        self.w = (1 + 0.02 * torch.randn(COLS, device=device, generator=g)).to(bf16)
+        self.dsum = torch.randn(ROWS, COLS, device=device, dtype=bf16, generator=g)
+        self.dout = torch.randn(ROWS, COLS, device=device, dtype=bf16, generator=g)
+        self.s = torch.empty_like(self.x)
+        self.y = torch.empty_like(self.x)
+        self.rstd = torch.empty(ROWS, device=device, dtype=torch.float32)
+        self.buffers = rn._make_backward_buffers(self.s, self.w)
+
+    def launches(self):
+        b = self.buffers
+        return (
+            ("tk_rmsnorm_fwd", lambda: self.rrn._launch_forward(
+                self.x, self.r, self.w, self.s, self.y, self.rstd,
+                eps=EPS, store_residual=True, store_stats=True)),
+            ("tk_rmsnorm_bwd_stage1", lambda: self.rn._launch_backward_stage1(
+                self.dout, self.s, self.w, self.rstd, b, incoming_dx=self.dsum)),
+            ("tk_rmsnorm_bwd_stage2", lambda: self.rn._launch_backward_stage2(b, COLS)),
+        )
+
+
+# Algorithmic bytes per launch (4 bf16 matrices each for forward and stage 1).
+STEP_BYTES = {
+    "tk_rmsnorm_fwd": 4 * ROWS * COLS * 2,
+    "tk_rmsnorm_bwd_stage1": 4 * ROWS * COLS * 2,
+    "tk_rmsnorm_bwd_stage2": 0,
+}
+
+
+def time_step(torch, step: Step, steps: int, warmup: int) -> tuple[float, dict[str, float]]:
+    """Run W untimed and K timed steps; returns ms/step and mean ms per kernel."""
+    launches = step.launches()
+    for _ in range(warmup):
+        for _, fn in launches:
+            fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in launches] for _ in range(steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(steps):
+        for j, (_, fn) in enumerate(launches):
+            events[i][j][0].record(stream)
+            fn()
+            events[i][j][1].record(stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ms_step = start.elapsed_time(end) / steps
+    per_kernel = {}
+    for j, (name, _) in enumerate(launches):
+        per_kernel[name] = statistics.fmean(events[i][j][0].elapsed_time(events[i][j][1]) for i in range(steps))
+    # Guard against the event clock disagreeing with the host clock.
+    ms_step = max(ms_step, 0.0)
+    return ms_step, per_kernel | {"_wall_ms_per_step": wall_ms / steps}
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """Oracle residual RMSNorm fwd+bwd on a 2048-row sample, repeated for ~`seconds`."""
+    import numpy as np
+
+    from oracle import oracle
+
+    threads = min(16, os.cpu_count() or 1)
+    oracle.set_threads(threads)
+    rng = np.random.default_rng(0)
+    rows = 2048
+    to_bf16 = lambda a: oracle.round_to(a.astype(np.float32), "bfloat16")  # noqa: E731
+    x = to_bf16(rng.standard_normal((rows, COLS)))
+    r = to_bf16(rng.standard_normal((rows, COLS)))
+    w = to_bf16(1 + 0.02 * rng.standard_normal(COLS))
+    dsum = to_bf16(rng.standard_normal((rows, COLS)))
+    dout = to_bf16(rng.standard_normal((rows, COLS)))
+    passes = 0
+    t0 = time.perf_counter()
+    while True:
+        s, _, rstd = oracle.rmsnorm_fwd(x, w, EPS, "bfloat16", residual=r)
+        oracle.rmsnorm_bwd(dout, s, w, rstd, "bfloat16", incoming=dsum)
+        passes += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= seconds:
+            break
+    sample_bytes = 8 * rows * COLS * 2
+    return {
+        "value": round(sample_bytes * passes / elapsed / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle residual RMSNorm fwd+bwd, {rows} x {COLS} bf16-valued rows, "
+                  f"{passes} passes in {elapsed:.1f} s (OpenMP, {threads} threads)",
+    }
+
+
+def kernel_table(torch, device) -> list[dict]:
+    """Per-kernel timings of every BASELINE configuration (flushed, event-timed)."""
+    from tklab.kernels import flash_attention as fa
+    from tklab.kernels import fused_softmax as sm
+    from tklab.kernels import matmul as mm
+    from tklab.kernels import rope as rp
+    from tklab.kernels import swiglu as sg
+
+    flush = torch.empty(1 << 28, dtype=torch.float32, device=device)  # 1 GiB
+    rows: list[dict] = []
+
+    def timed(fn, reps: int) -> float:
+        fn()
+        times = []
+        for _ in range(reps):
+            flush.zero_()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            times.append((a, b))
+        torch.cuda.synchronize()
+        return statistics.median(x.elapsed_time(y) for x, y in times)
+
+    def mem_row(name, config, fn, nbytes, reps=20):
+        ms = timed(fn, reps)
+        gbps = nbytes / ms / 1e6
+        rows.append({"kernel": name, "config": config, "ms": round(ms, 4), "bytes": nbytes,
+                     "GB/s": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4)})
+
+    def mfma_row(name, config, fn, flops, dtype, reps=10):
+        ms = timed(fn, reps)
+        tf = flops / ms / 1e9
+        rows.append({"kernel": name, "config": config, "ms": round(ms, 4), "flops": flops,
+                     "TFLOP/s": round(tf, 1), "frac": round(tf / MFMA_PEAK_TFLOPS[dtype], 4)})
+
+    g = torch.Generator(device=device).manual_seed(0)
+    bf16 = torch.bfloat16
+    # Config 1: softmax float32 [4096, 4096].
+    x = torch.randn(4096, 4096, device=device, generator=g)
+    y = torch.empty_like(x)
+    mem_row("tk_softmax_fwd", "f32 4096x4096", lambda: sm._launch((x,), y), 2 * x.numel() * 4)
+    del x, y
+    # Config 3: SwiGLU bf16 [16384, 14336].
+    gate = torch.randn(16384, 14336, device=device, dtype=bf16, generator=g)
+    up = torch.randn(16384, 14336, device=device, dtype=bf16, generator=g)
+    dy = torch.randn(16384, 14336, device=device, dtype=bf16, generator=g)
+    out = torch.empty_like(gate)
+    dv = torch.empty_like(gate)
+    n = gate.numel()
+    mem_row("tk_swiglu_fwd", "bf16 16384x14336", lambda: sg._launch_forward(up, gate, out), 3 * n * 2)
+    mem_row("tk_swiglu_bwd", "bf16 16384x14336",
+            lambda: sg._launch_backward_into(dy, up, gate, dv, out), 5 * n * 2)
+    del gate, up, dy, out, dv
+    # Config 3: RoPE on q [4, 32, 4096, 128] viewed [524288, 128], per-row tables.
+    q = torch.randn(4 * 32 * 4096, 128, device=device, dtype=bf16, generator=g)
+    inv = 10000.0 ** (-torch.arange(0, 128, 2, device=device, dtype=torch.float32) / 128)
+    ang = torch.arange(4096, device=device, dtype=torch.float32)[:, None] * inv[None, :]
+    cos = torch.cos(ang).to(bf16).repeat(128, 1)
+    sin = torch.sin(ang).to(bf16).repeat(128, 1)
+    yq = torch.empty_like(q)
+    dq = torch.empty_like(q)
+    mem_row("tk_rope_fwd", "bf16 [4,32,4096,128]", lambda: rp._launch_forward(q, cos, sin, yq),
+            3 * q.numel() * 2)
+    mem_row("tk_rope_bwd", "bf16 [4,32,4096,128] dx only",
+            lambda: rp._launch_backward_into(yq, q, cos, sin, dq, None, None), 3 * q.numel() * 2)
+    del q, cos, sin, yq, dq
+    # Config 4: GEMM.
+    for dt_name, dt in (("float16", torch.float16), ("bfloat16", bf16)):
+        for m, nn, k in ((8192, 8192, 8192), (4096, 4096, 4096), (8191, 8192, 8192)):
+            if dt is bf16 and m != 8192:
+                continue
+            sc = k ** -0.25
+            a = (torch.randn(m, k, device=device, generator=g) * sc).to(dt)
+            b = (torch.randn(k, nn, device=device, generator=g) * sc).to(dt)
+            c = torch.empty(m, nn, device=device, dtype=dt)
+            mfma_row("tk_gemm", f"{dt_name} {m}x{nn}x{k}", lambda: mm._launch_fp32acc((a, b), c),
+                     2 * m * nn * k, dt_name)
+            del a, b, c
+    # Config 5: attention.
+    for causal, nctx, d in ((True, 8192, 128), (False, 4096, 128), (True, 8192, 64), (False, 4096, 64)):
+        shape = (4, 32, nctx, d)
+        qq, kk, vv, do = (torch.randn(shape, device=device, dtype=bf16, generator=g) for _ in range(4))
+        o = torch.empty_like(qq)
+        lse = torch.empty(shape[:-1], device=device, dtype=torch.float32)
+        delta = torch.empty_like(lse)
+        gq, gk, gv = torch.empty_like(qq), torch.empty_like(qq), torch.empty_like(qq)
+        flops = fa.attention_flops(4, 32, nctx, d, causal=causal)
+        tag = f"bf16 B4 H32 N{nctx} D{d} {'causal' if causal else 'non-causal'}"
+        mfma_row("tk_attn_fwd", tag,
+                 lambda: fa._launch_forward(qq, kk, vv, o, lse, causal=causal, store_lse=True),
+                 flops, "bfloat16", reps=5)
+        mfma_row("tk_attn_bwd (preprocess+dkdv+dq)", tag + ", 2.5x fwd FLOPs",
+                 lambda: fa._launch_backward_into(qq, kk, vv, o, lse, do, delta, gq, gk, gv,
+                                                  causal=causal),
+                 int(2.5 * flops), "bfloat16", reps=5)
+        del qq, kk, vv, do, o, lse, delta, gq, gk, gv
+    del flush
+    torch.cuda.empty_cache()
+    return rows
+
+
+def main() -> int:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build's kernels shard rows/heads with no "
+              "exchange, and no multi-GPU figure is produced (run with --gpus 1).", file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    step = Step(torch, device)
+    ms_step, per_kernel = time_step(torch, step, args.steps, args.warmup)
+    step_bytes = sum(STEP_BYTES.values())
+    value = step_bytes / (ms_step / 1e3) / 1e9
+
+    kernel_ms = {k: v for k, v in per_kernel.items() if not k.startswith("_")}
+    dominant = max(kernel_ms, key=kernel_ms.get)
+    achieved = STEP_BYTES[dominant] / (kernel_ms[dominant] / 1e3) / 1e9
+    traffic = _traffic_from_summary() if dominant == "tk_rmsnorm_bwd_stage1" else None
+    roofline = {
+        "bound": "hbm",
+        "kernel": dominant,
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBPS, 4),
+        "traffic": traffic,
+        "algorithmic_bytes": STEP_BYTES[dominant],
+        "kernel_ms": {k: round(v, 5) for k, v in kernel_ms.items()},
+    }
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded torch.randn on device)",
+        "config": {
+            "workload": "residual_rms_norm forward+backward (BASELINE config 2)",
+            "rows": ROWS,
+            "cols": COLS,
+            "eps": EPS,
+            "bytes_per_step": step_bytes,
+        },
+        "roofline": roofline,
+    }
+    del step
+    torch.cuda.empty_cache()
+    if not args.no_kernels:
+        line["kernels"] = kernel_table(torch, device)
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

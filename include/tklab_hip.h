@@ -157,6 +157,47 @@ int tk_attn_bwd_dq(int dtype, const void* q, const void* k, const void* v, const
                    int64_t heads, int64_t seq, int64_t head_dim, const int64_t* strides,
                    float sm_scale, int causal, void* stream);
 
+/* ---- Registry kernels outside the transformer hot path ---------------- */
+
+/* out[i*out_stride] = x[i*x_stride] + y[i*y_stride], i < n (strides may be 0).
+ * Replaces `_vector_add_kernel[grid](...)`, src/tklab/kernels/vector_add.py:98-107. */
+int tk_vector_add(int dtype, const void* x, const void* y, void* out, int64_t n,
+                  int64_t x_stride, int64_t y_stride, int64_t out_stride, void* stream);
+
+/* Pointwise activation forward, kind 0 = ReLU, 1 = exact (erf) GELU,
+ * 2 = SiLU, 3 = tanh (as 2*sigmoid(2x) - 1).
+ * Replaces `_activation_forward_kernel[...]`, src/tklab/kernels/activations.py:173-182. */
+int tk_activation_fwd(int dtype, int kind, const void* x, void* y, int64_t rows, int64_t cols,
+                      int64_t x_row_stride, int64_t y_row_stride, void* stream);
+
+/* dx = dy * activation'(x).
+ * Replaces `_activation_backward_kernel[...]`, src/tklab/kernels/activations.py:195-206. */
+int tk_activation_bwd(int dtype, int kind, const void* dy, const void* x, void* dx, int64_t rows,
+                      int64_t cols, int64_t dy_row_stride, int64_t x_row_stride,
+                      int64_t dx_row_stride, void* stream);
+
+/* LayerNorm forward y = (x - mean) * rstd * w + b; mean/rstd (float32[rows])
+ * written when non-null.
+ * Replaces `_layer_norm_forward_kernel[(rows,)]`, src/tklab/kernels/layer_norm.py:254-267. */
+int tk_layernorm_fwd(int dtype, const void* x, const void* weight, const void* bias, void* y,
+                     float* mean, float* rstd, int64_t rows, int64_t cols, int64_t x_row_stride,
+                     int64_t y_row_stride, float eps, void* stream);
+
+/* LayerNorm backward stage 1: dx per row and float32 dweight/dbias partial rows
+ * per group, with the same group, count and determinism contract as
+ * tk_rmsnorm_bwd_stage1.
+ * Replaces `_layer_norm_backward_stage1_kernel[(rows,)]`, src/tklab/kernels/layer_norm.py:316-333. */
+int tk_layernorm_bwd_stage1(int dtype, void* dx, const void* dy, float* partial_dw,
+                            float* partial_db, const void* x, const void* weight,
+                            const float* mean, const float* rstd, int32_t* locks, int64_t rows,
+                            int64_t cols, int64_t x_row_stride, int64_t dy_row_stride,
+                            int64_t dx_row_stride, int64_t group_size, void* stream);
+
+/* LayerNorm backward stage 2: fixed-order column sums of both partial buffers.
+ * Replaces `_layer_norm_backward_stage2_kernel[...]`, src/tklab/kernels/layer_norm.py:341-350. */
+int tk_layernorm_bwd_stage2(int dtype, const float* partial_dw, const float* partial_db, void* dw,
+                            void* db, int64_t group_count, int64_t cols, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

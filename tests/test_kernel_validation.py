@@ -108,3 +108,100 @@ def test_rope_rejects_odd_feature_dimension() -> None:
 def test_rope_rejects_full_width_tables() -> None:
     with pytest.raises(ValueError, match="columns // 2"):
         rope(torch.zeros(2, 8), torch.zeros(2, 8), torch.zeros(2, 8))
+
+
+# ---- registry kernels outside the hot path ---------------------------------
+
+from tklab.kernels.activations import gelu  # noqa: E402
+from tklab.kernels.flash_attention import attention_noncausal  # noqa: E402
+from tklab.kernels.layer_norm import layer_norm  # noqa: E402
+from tklab.kernels.matmul import matmul_fp32acc  # noqa: E402
+from tklab.kernels.vector_add import vector_add  # noqa: E402
+
+
+def test_vector_add_rejects_shape_mismatch() -> None:
+    with pytest.raises(ValueError, match="shape mismatch"):
+        vector_add(torch.zeros(2), torch.zeros(3))
+
+
+def test_vector_add_requires_a_gpu_tensor() -> None:
+    with pytest.raises(ValueError, match="requires CUDA"):
+        vector_add(torch.zeros(2), torch.zeros(2))
+
+
+def test_activation_contract() -> None:
+    with pytest.raises(ValueError, match="2D tensor"):
+        gelu(torch.zeros(3))
+    with pytest.raises(ValueError, match="requires CUDA"):
+        gelu(torch.zeros(2, 3))
+
+
+def test_layer_norm_rejects_mismatched_parameters() -> None:
+    with pytest.raises(ValueError, match="match the final input dimension"):
+        layer_norm(torch.zeros(2, 8), torch.zeros(7), torch.zeros(8))
+
+
+def test_layer_norm_rejects_strided_parameters() -> None:
+    with pytest.raises(ValueError, match="must be contiguous"):
+        layer_norm(torch.zeros(2, 8), torch.zeros(16)[::2], torch.zeros(16)[::2])
+
+
+def test_layer_norm_requires_a_gpu_tensor() -> None:
+    with pytest.raises(ValueError, match="requires CUDA"):
+        layer_norm(torch.zeros(2, 8), torch.ones(8), torch.zeros(8))
+
+
+@pytest.mark.parametrize("eps", [0.0, -1e-5, float("nan"), float("inf")])
+def test_layer_norm_rejects_invalid_epsilon(eps: float) -> None:
+    with pytest.raises(ValueError, match="finite and positive"):
+        layer_norm(torch.zeros(2, 8), torch.ones(8), torch.zeros(8), eps=eps)
+
+
+def test_matmul_rejects_incompatible_inner_dimensions() -> None:
+    with pytest.raises(ValueError, match="incompatible shapes"):
+        matmul_fp32acc(torch.zeros(2, 3, dtype=torch.float16), torch.zeros(4, 2, dtype=torch.float16))
+
+
+def test_matmul_requires_a_gpu_tensor() -> None:
+    with pytest.raises(ValueError, match="requires CUDA"):
+        matmul_fp32acc(torch.zeros(2, 3, dtype=torch.float16), torch.zeros(3, 2, dtype=torch.float16))
+
+
+def test_matmul_rejects_zero_strides() -> None:
+    left = torch.empty_strided((2, 3), (0, 1), dtype=torch.float16, device="meta")
+    right = torch.empty((3, 2), dtype=torch.float16, device="meta")
+    with pytest.raises(ValueError, match="strictly positive strides"):
+        matmul_fp32acc(left, right)
+
+
+def test_matmul_rejects_offsets_outside_int32_range() -> None:
+    left = torch.empty_strided((2, 2), (2**31, 1), dtype=torch.float16, device="meta")
+    right = torch.empty((2, 2), dtype=torch.float16, device="meta")
+    with pytest.raises(ValueError, match="int32 offset"):
+        matmul_fp32acc(left, right)
+
+
+def test_matmul_rejects_float32() -> None:
+    with pytest.raises(ValueError, match="float16 and bfloat16"):
+        matmul_fp32acc(torch.zeros(2, 3), torch.zeros(3, 2))
+
+
+def test_attention_rejects_shape_mismatch() -> None:
+    q = torch.zeros(1, 2, 8, 64, dtype=torch.float16)
+    k = torch.zeros(1, 2, 7, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="identical shapes"):
+        attention_noncausal(q, k, torch.zeros_like(q))
+
+
+@pytest.mark.parametrize(
+    ("shape", "dtype", "fragment"),
+    [
+        ((1, 2, 8, 64), torch.float32, "requires CUDA"),  # device is checked before dtype
+        ((2, 8, 64), torch.float16, "batch, heads, sequence, dim"),
+        ((1, 2, 0, 64), torch.float16, "empty dimensions"),
+    ],
+)
+def test_attention_contract(shape, dtype, fragment) -> None:
+    q = torch.zeros(shape, dtype=dtype, device="meta")
+    with pytest.raises(ValueError, match=fragment):
+        attention_noncausal(q, q, q)

@@ -29,33 +29,34 @@ __global__ __launch_bounds__(RT >= kNormBlock ? RT : kNormBlock) void rmsnorm_fw
     T* __restrict__ residual_sum, T* __restrict__ y, float* __restrict__ rstd_out, int rows,
     int cols, int64_t x_stride, int64_t r_stride, int64_t s_stride, int64_t y_stride, float eps) {
   constexpr int SLOTS = RT >= kNormBlock ? 1 : kNormBlock / RT;
+  using Row = tk::RawRow<T, VEC, RT, VALS>;
   __shared__ float scratch[RT / 64];
   const int lane = threadIdx.x % RT;
   const int row = blockIdx.x * SLOTS + threadIdx.x / RT;
   if (row >= rows) return;  // SLOTS > 1 only for barrier-free single-wave rows
 
-  float v[VALS];
-  tk::load_row<T, VEC, RT, VALS>(x + row * x_stride, cols, lane, v, 0.f);
+  // s is kept in the storage type: with a residual it is rounded there anyway.
+  Row sv;
+  sv.load(x + row * x_stride, cols, lane);
   if (residual != nullptr) {
-    float r[VALS];
-    tk::load_row<T, VEC, RT, VALS>(residual + row * r_stride, cols, lane, r, 0.f);
+    Row rv;
+    rv.load(residual + row * r_stride, cols, lane);
 #pragma unroll
-    for (int e = 0; e < VALS; ++e) v[e] = tk::round_to<T>(v[e] + r[e]);
-    if (residual_sum != nullptr)
-      tk::store_row<T, VEC, RT, VALS>(residual_sum + row * s_stride, cols, lane, v);
+    for (int e = 0; e < VALS; ++e) sv.set(e, sv.get(e) + rv.get(e));
+    if (residual_sum != nullptr) sv.store(residual_sum + row * s_stride, cols, lane);
   }
 
   float ss = 0.f;
 #pragma unroll
-  for (int e = 0; e < VALS; ++e) ss += v[e] * v[e];
+  for (int e = 0; e < VALS; ++e) ss += sv.get(e) * sv.get(e);
   ss = tk::group_allreduce<RT>(ss, tk::SumOp{}, scratch);
   const float rstd = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
 
-  float w[VALS];
-  tk::load_row<T, VEC, RT, VALS>(weight, cols, lane, w, 0.f);
+  Row wv;
+  wv.load(weight, cols, lane);
 #pragma unroll
-  for (int e = 0; e < VALS; ++e) v[e] = v[e] * rstd * w[e];
-  tk::store_row<T, VEC, RT, VALS>(y + row * y_stride, cols, lane, v);
+  for (int e = 0; e < VALS; ++e) wv.set(e, sv.get(e) * rstd * wv.get(e));
+  wv.store(y + row * y_stride, cols, lane);
   if (rstd_out != nullptr && lane == 0) rstd_out[row] = rstd;
 }
 
@@ -71,8 +72,14 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
     const float* __restrict__ rstd, int32_t* __restrict__ counts, int rows, int cols,
     int64_t x_stride, int64_t dy_stride, int64_t inc_stride, int64_t dx_stride, int group_size) {
   constexpr int SLOTS = bwd_block<RT>() / RT;
-  // Cross-slot fold buffer (one float per column) and the row-reduction scratch.
-  __shared__ float fold[SLOTS > 1 ? RT * VALS : 1];
+  constexpr int WIDTH = RT * VALS;  // columns one row slot covers
+  using Row = tk::RawRow<T, VEC, RT, VALS>;
+  // dweight partials live in LDS, one float per column per slot; each address
+  // belongs to one thread, so every sum has a fixed order. (Shapes whose
+  // accumulators would exceed 128 KiB are beyond the 64 KiB row budget and
+  // never launched; they keep registers so they still compile.)
+  constexpr bool ACC_LDS = SLOTS * WIDTH * 4 <= 131072;
+  __shared__ float acc_lds[ACC_LDS ? SLOTS * WIDTH : 1];
   __shared__ float scratch[RT / 64];
 
   const int group = blockIdx.x;
@@ -82,11 +89,15 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
   const int group_rows = (rows - 1 - group) / group_size + 1;
   const int iters = (group_rows + SLOTS - 1) / SLOTS;
 
-  float w[VALS];
-  tk::load_row<T, VEC, RT, VALS>(weight, cols, lane, w, 0.f);
-  float acc[VALS];
+  float acc[ACC_LDS ? 1 : VALS];
+  float* my_acc = acc_lds + slot * WIDTH;
+  if constexpr (ACC_LDS) {
 #pragma unroll
-  for (int e = 0; e < VALS; ++e) acc[e] = 0.f;
+    for (int e = 0; e < VALS; ++e) my_acc[tk::row_column<VEC, RT>(e, lane)] = 0.f;
+  } else {
+#pragma unroll
+    for (int e = 0; e < VALS; ++e) acc[e] = 0.f;
+  }
 
   for (int it = 0; it < iters; ++it) {
     const int k = it * SLOTS + slot;
@@ -94,60 +105,61 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
     // barriers inside group_allreduce line up; an idle slot computes on zeros.
     const bool valid = k < group_rows;
     const int64_t row = static_cast<int64_t>(group) + static_cast<int64_t>(k) * group_size;
-    float xv[VALS], g[VALS];
+    Row xv, dv, iv, wv;
     float r = 0.f;
     if (valid) {
-      tk::load_row<T, VEC, RT, VALS>(x + row * x_stride, cols, lane, xv, 0.f);
-      tk::load_row<T, VEC, RT, VALS>(dy + row * dy_stride, cols, lane, g, 0.f);
+      xv.load(x + row * x_stride, cols, lane);
+      dv.load(dy + row * dy_stride, cols, lane);
+      if (incoming != nullptr) iv.load(incoming + row * inc_stride, cols, lane);
       r = rstd[row];
     } else {
-#pragma unroll
-      for (int e = 0; e < VALS; ++e) xv[e] = g[e] = 0.f;
+      xv.load(x, 0, lane);  // all zeros
+      dv.load(dy, 0, lane);
     }
+    wv.load(weight, cols, lane);  // 2*cols bytes, served from cache
     float dot = 0.f;
 #pragma unroll
     for (int e = 0; e < VALS; ++e) {
-      const float dyv = g[e];
-      xv[e] = xv[e] * r;      // x_hat
-      acc[e] += dyv * xv[e];  // dweight partial
-      g[e] = w[e] * dyv;      // g = w * dy
-      dot += g[e] * xv[e];
+      const float x_hat = xv.get(e) * r;
+      const float d = dv.get(e);
+      if constexpr (ACC_LDS) {
+        my_acc[tk::row_column<VEC, RT>(e, lane)] += d * x_hat;
+      } else {
+        acc[e] += d * x_hat;
+      }
+      dot += (wv.get(e) * d) * x_hat;
     }
     dot = tk::group_allreduce<RT>(dot, tk::SumOp{}, scratch);
     const float mean = dot / static_cast<float>(cols);
-#pragma unroll
-    for (int e = 0; e < VALS; ++e) g[e] = r * (g[e] - xv[e] * mean);
     if (valid) {
-      if (incoming != nullptr) {
-        float inc[VALS];
-        tk::load_row<T, VEC, RT, VALS>(incoming + row * inc_stride, cols, lane, inc, 0.f);
 #pragma unroll
-        for (int e = 0; e < VALS; ++e) g[e] += inc[e];
+      for (int e = 0; e < VALS; ++e) {
+        const float x_hat = xv.get(e) * r;
+        const float g = wv.get(e) * dv.get(e);
+        float v = r * (g - x_hat * mean);
+        if (incoming != nullptr) v += iv.get(e);
+        xv.set(e, v);
       }
-      tk::store_row<T, VEC, RT, VALS>(dx + row * dx_stride, cols, lane, g);
+      xv.store(dx + row * dx_stride, cols, lane);
     }
   }
 
   float* out = partial + static_cast<int64_t>(group) * cols;
-  if constexpr (SLOTS == 1) {
+  if constexpr (!ACC_LDS) {
 #pragma unroll
     for (int e = 0; e < VALS; ++e) {
       const int c = tk::row_column<VEC, RT>(e, lane);
       if (c < cols) out[c] = acc[e];
     }
   } else {
-    // Fold the slots in increasing slot order: slot 0 writes, the others add in turn.
-    for (int s = 0; s < SLOTS; ++s) {
-      if (slot == s) {
+    __syncthreads();
+    // Sum the slots in increasing slot order.
+    for (int c = threadIdx.x; c < cols; c += bwd_block<RT>()) {
+      float t = acc_lds[c];
 #pragma unroll
-        for (int e = 0; e < VALS; ++e) {
-          const int c = tk::row_column<VEC, RT>(e, lane);
-          if (c < cols) fold[c] = (s == 0) ? acc[e] : fold[c] + acc[e];
-        }
-      }
-      __syncthreads();
+      for (int s2 = 1; s2 < SLOTS; ++s2) t += acc_lds[s2 * WIDTH + c];
+      out[c] = t;
     }
-    for (int c = threadIdx.x; c < cols; c += bwd_block<RT>()) out[c] = fold[c];
   }
   if (threadIdx.x == 0) counts[group] = 1;
 }
@@ -192,11 +204,15 @@ bool rows_vector_ok(int dtype, int64_t cols, std::initializer_list<const void*> 
   return true;
 }
 
-int check_rows(const char* what, int dtype, int64_t rows, int64_t cols, tk::RowShape* shape) {
+int check_rows(const char* what, int dtype, int64_t rows, int64_t cols, bool vector_ok,
+               tk::RowShape* shape) {
   if (!tk::valid_dtype(dtype)) return tk::fail("%s: unsupported dtype code %d", what, dtype);
   if (rows <= 0 || cols <= 0) return tk::fail("%s: empty problem", what);
   if (rows > INT32_MAX) return tk::fail("%s: too many rows", what);
-  if (cols * tk::elem_size(dtype) > 65536 || !tk::pick_row_shape(cols, shape))
+  // At most 32 registers per row tensor per thread: 64 packed 16-bit values,
+  // 32 float32 values, or 32 unpacked values on the unaligned scalar path.
+  const int max_vals = vector_ok ? 128 / tk::elem_size(dtype) : 32;
+  if (cols * tk::elem_size(dtype) > 65536 || !tk::pick_row_shape(cols, shape, max_vals))
     return tk::fail("%s: feature row exceeds the 65536-byte fused limit", what);
   return 0;
 }
@@ -208,14 +224,14 @@ extern "C" int tk_rmsnorm_fwd(int dtype, const void* x, const void* residual, co
                               int64_t x_row_stride, int64_t residual_row_stride,
                               int64_t residual_sum_row_stride, int64_t y_row_stride, float eps,
                               void* stream) {
-  tk::RowShape shape;
-  if (check_rows("rmsnorm_fwd", dtype, rows, cols, &shape)) return 1;
   if (x == nullptr || weight == nullptr || y == nullptr) return tk::fail("rmsnorm_fwd: null pointer");
   if (!(eps > 0.f)) return tk::fail("rmsnorm_fwd: eps must be finite and positive");
-  const bool vector_ok = rows_vector_ok(
+  const bool vector_ok = tk::valid_dtype(dtype) && rows_vector_ok(
       dtype, cols, {x, residual, weight, residual_sum, y},
       {x_row_stride, residual ? residual_row_stride : 0, residual_sum ? residual_sum_row_stride : 0,
        y_row_stride});
+  tk::RowShape shape;
+  if (check_rows("rmsnorm_fwd", dtype, rows, cols, vector_ok, &shape)) return 1;
   const int slots = shape.rt >= kNormBlock ? 1 : kNormBlock / shape.rt;
   const dim3 grid(static_cast<unsigned>(tk::cdiv(rows, slots)));
   const dim3 block(shape.rt >= kNormBlock ? shape.rt : kNormBlock);
@@ -237,17 +253,17 @@ extern "C" int tk_rmsnorm_bwd_stage1(int dtype, void* dx, const void* dy, const 
                                      int64_t x_row_stride, int64_t dy_row_stride,
                                      int64_t incoming_dx_row_stride, int64_t dx_row_stride,
                                      int64_t group_size, void* stream) {
-  tk::RowShape shape;
-  if (check_rows("rmsnorm_bwd_stage1", dtype, rows, cols, &shape)) return 1;
   if (dx == nullptr || dy == nullptr || partial_dw == nullptr || x == nullptr ||
       weight == nullptr || rstd == nullptr || locks == nullptr)
     return tk::fail("rmsnorm_bwd_stage1: null pointer");
   if (group_size <= 0 || group_size > INT32_MAX)
     return tk::fail("rmsnorm_bwd_stage1: group_size must be positive");
   const int64_t group_count = group_size < rows ? group_size : rows;
-  const bool vector_ok = rows_vector_ok(
+  const bool vector_ok = tk::valid_dtype(dtype) && rows_vector_ok(
       dtype, cols, {dx, dy, incoming_dx, x, weight},
       {x_row_stride, dy_row_stride, incoming_dx ? incoming_dx_row_stride : 0, dx_row_stride});
+  tk::RowShape shape;
+  if (check_rows("rmsnorm_bwd_stage1", dtype, rows, cols, vector_ok, &shape)) return 1;
   const dim3 grid(static_cast<unsigned>(group_count));
   hipStream_t s = tk::as_stream(stream);
   int32_t* counts = locks + group_size;

@@ -46,25 +46,104 @@ __device__ __forceinline__ int row_column(int e, int lane) {
   return ((e / VEC) * RT + lane) * VEC + (e % VEC);
 }
 
+// Bits of one storage element <-> float32.
+template <typename T>
+__device__ __forceinline__ float bits_to_f32(uint32_t b);
+template <>
+__device__ __forceinline__ float bits_to_f32<float>(uint32_t b) { return __uint_as_float(b); }
+template <>
+__device__ __forceinline__ float bits_to_f32<__bf16>(uint32_t b) { return __uint_as_float(b << 16); }
+template <>
+__device__ __forceinline__ float bits_to_f32<_Float16>(uint32_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+}
+template <typename T>
+__device__ __forceinline__ uint32_t f32_to_bits(float f) {
+  if constexpr (sizeof(T) == 4) {
+    return __float_as_uint(f);
+  } else {
+    return __builtin_bit_cast(uint16_t, static_cast<T>(f));
+  }
+}
+
+// A row held in registers as packed storage words (no float copy): 16-bit
+// rows take half the registers of their float32 values. Element e of thread
+// `lane` is column row_column<VEC, RT>(e, lane).
+template <typename T, int VEC, int RT, int VALS>
+struct RawRow {
+  static constexpr int ITEMS = VALS / VEC;
+  static constexpr int PER_WORD = 4 / int(sizeof(T));  // elements per 32-bit word
+  static constexpr int WORDS_PER_VEC = (VEC + PER_WORD - 1) / PER_WORD;
+  uint32_t w[ITEMS * WORDS_PER_VEC];
+
+  __device__ __forceinline__ void load(const T* __restrict__ row, int cols, int lane) {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int c = (i * RT + lane) * VEC;
+      uint32_t* dst = w + i * WORDS_PER_VEC;
+      if constexpr (VEC * sizeof(T) == 16) {
+        const uint4 u = c < cols ? *reinterpret_cast<const uint4*>(row + c) : make_uint4(0, 0, 0, 0);
+        dst[0] = u.x;
+        dst[1] = u.y;
+        dst[2] = u.z;
+        dst[3] = u.w;
+      } else {
+        static_assert(VEC == 1, "scalar fallback");
+        dst[0] = c < cols ? f32_to_bits<T>(to_f32(row[c])) : 0u;
+      }
+    }
+  }
+  __device__ __forceinline__ void store(T* __restrict__ row, int cols, int lane) const {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int c = (i * RT + lane) * VEC;
+      if (c >= cols) continue;
+      const uint32_t* src = w + i * WORDS_PER_VEC;
+      if constexpr (VEC * sizeof(T) == 16) {
+        *reinterpret_cast<uint4*>(row + c) = make_uint4(src[0], src[1], src[2], src[3]);
+      } else {
+        row[c] = from_f32<T>(bits_to_f32<T>(src[0]));
+      }
+    }
+  }
+  __device__ __forceinline__ uint32_t bits(int e) const {
+    if constexpr (VEC == 1 || PER_WORD == 1) {
+      return w[e];
+    } else {
+      const uint32_t word = w[e / PER_WORD];
+      return (e & 1) ? (word >> 16) : (word & 0xffffu);
+    }
+  }
+  __device__ __forceinline__ float get(int e) const { return bits_to_f32<T>(bits(e)); }
+  __device__ __forceinline__ void set(int e, float f) {
+    const uint32_t b = f32_to_bits<T>(f);
+    if constexpr (VEC == 1 || PER_WORD == 1) {
+      w[e] = b;
+    } else {
+      uint32_t& word = w[e / PER_WORD];
+      word = (e & 1) ? ((word & 0xffffu) | (b << 16)) : ((word & 0xffff0000u) | b);
+    }
+  }
+};
+
 // Launch shape for a row width: RT threads per row, VALS elements per thread.
 struct RowShape {
   int rt;
   int vals;
 };
 
-// Smallest group that covers `cols` with at most 64 register-resident
-// elements per thread: one wave up to 64*64 columns, 256 threads up to
-// 16384, 1024 threads up to 65536. Returns false when the row is wider.
-inline bool pick_row_shape(int64_t cols, RowShape* shape) {
+// Smallest thread group (64, 256 or 1024 threads) that covers `cols` with at
+// most `max_vals` register-resident elements per thread (VALS in {16, 32, 64}).
+// Returns false when the row is wider than 1024 * max_vals.
+inline bool pick_row_shape(int64_t cols, RowShape* shape, int max_vals = 64) {
   static const int kThreads[] = {64, 256, 1024};
+  static const int kVals[] = {16, 32, 64};
   for (int rt : kThreads) {
-    if (cols <= int64_t(rt) * 16) {
-      *shape = {rt, 16};
-      return true;
-    }
-    if (cols <= int64_t(rt) * 64) {
-      *shape = {rt, 64};
-      return true;
+    for (int vals : kVals) {
+      if (vals <= max_vals && cols <= int64_t(rt) * vals) {
+        *shape = {rt, vals};
+        return true;
+      }
     }
   }
   return false;
@@ -76,10 +155,13 @@ inline bool pick_row_shape(int64_t cols, RowShape* shape) {
 #define TK_DISPATCH_ROW_SHAPE(shape, ...)                                \
   switch ((shape).rt * 100 + (shape).vals) {                             \
     case 6416: { constexpr int RT = 64, VALS = 16; __VA_ARGS__; break; }      \
+    case 6432: { constexpr int RT = 64, VALS = 32; __VA_ARGS__; break; }      \
     case 6464: { constexpr int RT = 64, VALS = 64; __VA_ARGS__; break; }      \
     case 25616: { constexpr int RT = 256, VALS = 16; __VA_ARGS__; break; }    \
+    case 25632: { constexpr int RT = 256, VALS = 32; __VA_ARGS__; break; }    \
     case 25664: { constexpr int RT = 256, VALS = 64; __VA_ARGS__; break; }    \
     case 102416: { constexpr int RT = 1024, VALS = 16; __VA_ARGS__; break; }  \
+    case 102432: { constexpr int RT = 1024, VALS = 32; __VA_ARGS__; break; }  \
     case 102464: { constexpr int RT = 1024, VALS = 64; __VA_ARGS__; break; }  \
     default: return tk::fail("internal: no row kernel for shape %d/%d", (shape).rt, (shape).vals); \
   }

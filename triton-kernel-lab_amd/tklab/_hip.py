@@ -54,6 +54,14 @@ _SIGNATURES: dict[str, list[object]] = {
     "tk_attn_bwd_dq": [
         _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64P, _F32, _I32, _P,
     ],
+    "tk_vector_add": [_I32, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "tk_activation_fwd": [_I32, _I32, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "tk_activation_bwd": [_I32, _I32, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P],
+    "tk_layernorm_fwd": [_I32, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P],
+    "tk_layernorm_bwd_stage1": [
+        _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P,
+    ],
+    "tk_layernorm_bwd_stage2": [_I32, _P, _P, _P, _P, _I64, _I64, _P],
 }
 
 EXPORTED_SYMBOLS: tuple[str, ...] = ("tk_abi_version", "tk_last_error", *_SIGNATURES)

@@ -29,18 +29,19 @@ def validate_epsilon(eps: float) -> None:
 def row_launch_shape(columns: int, element_size: int) -> tuple[int, int]:
     """Return ``(threads_per_row, values_per_thread)`` for a row width.
 
-    Mirrors ``pick_row_shape`` in ``csrc/rows.hpp``: one 64-lane wave per row
-    up to 4096 columns, 256 threads up to 16384, 1024 threads up to 65536, with
-    16 or 64 register-resident values per thread.
+    Mirrors ``pick_row_shape`` in ``csrc/rows.hpp`` for aligned rows: the
+    smallest group of 64, 256 or 1024 threads whose threads each hold at most
+    128 bytes of the row (64 16-bit or 32 float32 values, as 16, 32 or 64).
 
     Raises:
         ValueError: if the row exceeds the single-pass budget.
     """
     if columns * element_size > MAX_FEATURE_BYTES:
         raise ValueError("feature dimension exceeds the fused normalization limit")
+    max_values = 128 // element_size
     for threads in (64, 256, 1024):
-        for values in (16, 64):
-            if columns <= threads * values:
+        for values in (16, 32, 64):
+            if values <= max_values and columns <= threads * values:
                 return threads, values
     raise ValueError("feature dimension exceeds the fused normalization limit")
 
