@@ -40,7 +40,10 @@ def _check_rows(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, rows: torch.T
 @pytest.mark.parametrize(
     ("m", "n", "k"),
     [(1, 1, 8), (1, 8, 1), (8, 8, 8), (256, 256, 64), (300, 520, 72), (512, 512, 512),
-     (129, 257, 193), (1024, 1024, 1024), (255, 264, 4096), (7, 9, 11)],
+     (129, 257, 193), (1024, 1024, 1024), (255, 264, 4096), (7, 9, 11),
+     # K % 32 == 0 goes through the DMA kernel: fewer K tiles than the prefetch depth,
+     # exactly the prefetch depth, and M/N edges inside one block tile.
+     (1, 8, 32), (33, 40, 32), (300, 520, 96), (257, 136, 160), (520, 1032, 128)],
 )
 def test_small_shapes_match_the_oracle(dtype: torch.dtype, m: int, n: int, k: int) -> None:
     torch.manual_seed(m * 7 + n * 3 + k)
@@ -94,4 +97,13 @@ def test_identity_is_exact() -> None:
     torch.manual_seed(3)
     a = torch.randn(384, 264, device="cuda", dtype=torch.bfloat16)
     eye = torch.eye(264, device="cuda", dtype=torch.bfloat16)
+    assert torch.equal(matmul_fp32acc(a, eye), a)
+
+
+@pytest.mark.parametrize("k", [264, 256])
+def test_identity_is_exact_on_both_paths(k: int) -> None:
+    """K = 264 takes the register-staged kernel, K = 256 the DMA kernel."""
+    torch.manual_seed(4)
+    a = torch.randn(300, k, device="cuda", dtype=torch.float16)
+    eye = torch.eye(k, device="cuda", dtype=torch.float16)
     assert torch.equal(matmul_fp32acc(a, eye), a)

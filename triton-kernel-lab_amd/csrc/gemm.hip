@@ -2,6 +2,10 @@
 // f16/bf16 output (src/tklab/kernels/matmul.py:72-164 computes the same
 // product; here the tiling is MI355X's own).
 //
+// tk_gemm sends row-major operands with K % 32 == 0 to the buffer->LDS DMA kernel
+// in gemm_dma.hip. This file's register-staged kernel takes everything else:
+// arbitrary strides (transposed views), K tails, unaligned rows.
+//
 // Block tile 256 x 256, K step 64, 256 threads = 4 wave64s in a 2 x 2 grid;
 // each wave owns a 128 x 128 sub-tile as 4 x 4 MFMA tiles of
 // v_mfma_f32_32x32x16 (256 float32 accumulators per lane, one wave per SIMD).
@@ -23,6 +27,7 @@
 // Tile order: workgroup w runs on XCD w % 8; tiles are renumbered so each XCD
 // works through a contiguous range, walked in groups of 4 M-tiles so
 // concurrently running tiles share A and B panels in that XCD's L2.
+#include "gemm.hpp"
 #include "tk_common.hpp"
 
 namespace {
@@ -263,11 +268,15 @@ extern "C" int tk_gemm(int dtype, const void* a, const void* b, void* c, int64_t
   if (tiles_m * tiles_n > INT32_MAX) return tk::fail("gemm: too many tiles");
   Problem p{(int)m, (int)n, (int)k, stride_am, stride_ak, stride_bk, stride_bn,
             stride_cm, stride_cn, (int)tiles_m, (int)tiles_n};
+  hipStream_t s = tk::as_stream(stream);
+  if (tk::gemm_dma_applies(a, b, m, n, k, stride_am, stride_ak, stride_bk, stride_bn)) {
+    tk::gemm_dma_launch(dtype, a, b, c, m, n, k, stride_am, stride_bk, stride_cm, stride_cn, s);
+    return tk::check_launch("gemm");
+  }
   const bool fast = stride_ak == 1 && stride_bn == 1 && k % 8 == 0 && n % 8 == 0 &&
                     stride_am % 8 == 0 && stride_bk % 8 == 0 && tk::aligned16(a) &&
                     tk::aligned16(b);
   const dim3 grid(static_cast<unsigned>(tiles_m * tiles_n));
-  hipStream_t s = tk::as_stream(stream);
   if (dtype == TK_DTYPE_F16) {
     using T = _Float16;
     if (fast)
