@@ -124,3 +124,48 @@ def test_config_shapes_per_head(causal, n, d) -> None:
         assert_relative_frobenius(
             lse[b, h], torch.logsumexp(s, dim=-1) * math.log2(math.e), max_relative_error=1e-5
         )
+
+
+def _abi_forward(q, k, v, causal):
+    """tk_attn_fwd through the C ABI with the tensors' own (possibly strided) layouts."""
+    from tklab import _hip
+
+    batch, heads, n_ctx, head_dim = q.shape
+    out = torch.empty(q.shape, device=q.device, dtype=q.dtype)
+    lse = torch.empty(q.shape[:-1], device=q.device, dtype=torch.float32)
+    strides = lambda t: _hip.int64_array(list(t.stride()[:3]))  # noqa: E731
+    _hip.call("tk_attn_fwd", _hip.dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+              out.data_ptr(), lse.data_ptr(), batch, heads, n_ctx, head_dim, strides(q),
+              strides(k), strides(v), strides(out), 1.0 / math.sqrt(head_dim), int(causal),
+              _hip.stream_of(q))
+    return out, lse
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_sequence_major_layout_through_the_abi(causal) -> None:
+    """[batch, seq, heads, dim] storage viewed as (B, H, N, D): sequence stride H * D."""
+    torch.manual_seed(11 + int(causal))
+    shape = (2, 333, 3, 128)
+    q, k, v = (torch.randn(shape, device="cuda", dtype=torch.bfloat16).transpose(1, 2)
+               for _ in range(3))
+    out, lse = _abi_forward(q, k, v, causal)
+    o_ref, lse_ref = oracle.attn_fwd(host(q.contiguous()), host(k.contiguous()),
+                                     host(v.contiguous()), 128 ** -0.5, causal, "bfloat16")
+    assert_close(out, dev(o_ref, out))
+    torch.testing.assert_close(lse, dev(lse_ref, lse), rtol=1e-5, atol=1e-5)
+
+
+def test_head_rows_spanning_two_gib_take_the_register_staged_kernel() -> None:
+    """K rows 2^20 elements apart (2.2 GiB per head) exceed 32-bit buffer offsets."""
+    torch.manual_seed(12)
+    n, d, stride = 1100, 64, 1 << 20
+    q, v = (torch.randn(1, 1, n, d, device="cuda", dtype=torch.float16) for _ in range(2))
+    backing = torch.empty(n, stride, device="cuda", dtype=torch.float16)
+    backing[:, :d] = torch.randn(n, d, device="cuda", dtype=torch.float16)
+    k = backing[:, :d].unsqueeze(0).unsqueeze(0)  # (1, 1, n, d), sequence stride 2^20
+    out, lse = _abi_forward(q, k, v, True)
+    o_ref, lse_ref = oracle.attn_fwd(host(q), host(k.contiguous()), host(v), d ** -0.5, True,
+                                     "float16")
+    del backing
+    assert_close(out, dev(o_ref, out))
+    torch.testing.assert_close(lse, dev(lse_ref, lse), rtol=1e-5, atol=1e-5)

@@ -22,6 +22,7 @@
 //  * Row-major LDS tiles ([64][D]) and transposed tiles ([D][64]) store 16-byte
 //    chunk c of row r at chunk c ^ (r % 8): 8 consecutive rows read by one
 //    operand load hit 8 distinct bank groups.
+#include "attention.hpp"
 #include "tk_common.hpp"
 
 namespace {
@@ -207,6 +208,8 @@ __device__ __forceinline__ void tile_of(const Shape& s, int& bh, int& qb) {
 
 // ---------------------------------------------------------------- forward
 //
+// Register-staged forward, used only when a head's K or V rows span 2 GiB or more
+// (the DMA forward in attention_fwd.hip addresses them with 32-bit offsets).
 // Workgroup: 256 queries (4 waves x 64); key blocks of 64.
 // Per wave and key block: S^T (2 key tiles x 2 query tiles) over D/16 steps,
 // softmax, O^T (D/32 feature tiles x 2 query tiles) += V^T P^T over 4 steps.
@@ -739,6 +742,12 @@ extern "C" int tk_attn_fwd(int dtype, const void* q, const void* k, const void* 
     return tk::fail("attn_fwd: strides must be positive multiples of 8 within int32 range");
   if (!tk::aligned16(q) || !tk::aligned16(k) || !tk::aligned16(v) || !tk::aligned16(o))
     return tk::fail("attn_fwd: tensors must be 16-byte aligned");
+  if (tk::attn_fwd_dma_applies(seq, head_dim, k_strides, v_strides)) {
+    tk::attn_fwd_dma_launch(dtype, q, k, v, o, lse, batch, heads, seq, head_dim, q_strides,
+                            k_strides, v_strides, o_strides, sm_scale, causal != 0,
+                            tk::as_stream(stream));
+    return tk::check_launch("attn_fwd");
+  }
   Shape s{};
   s.heads = (int)heads;
   s.seq = (int)seq;

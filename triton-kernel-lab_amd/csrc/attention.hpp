@@ -1,0 +1,20 @@
+// Internal interface between the attention entry points (attention.hip) and the
+// buffer->LDS DMA forward kernel (attention_fwd.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace tk {
+
+// True when each head's K and V rows span less than 2 GiB (32-bit buffer offsets).
+// The caller has already checked dtype, head_dim and 16-byte row alignment.
+bool attn_fwd_dma_applies(int64_t seq, int64_t head_dim, const int64_t* k_strides,
+                          const int64_t* v_strides);
+
+void attn_fwd_dma_launch(int dtype, const void* q, const void* k, const void* v, void* o,
+                         float* lse, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                         const int64_t* q_strides, const int64_t* k_strides,
+                         const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
+                         bool causal, hipStream_t stream);
+
+}  // namespace tk
