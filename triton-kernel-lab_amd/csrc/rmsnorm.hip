@@ -60,10 +60,10 @@ __global__ __launch_bounds__(RT >= kNormBlock ? RT : kNormBlock) void rmsnorm_fw
   if (rstd_out != nullptr && lane == 0) rstd_out[row] = rstd;
 }
 
-// Threads per workgroup of the backward stage 1: eight single-wave row slots,
+// Threads per workgroup of the backward stage 1: four single-wave row slots,
 // or one multi-wave row group.
 template <int RT>
-constexpr int bwd_block() { return RT == 64 ? 512 : RT; }
+constexpr int bwd_block() { return RT == 64 ? 256 : RT; }
 
 template <typename T, int VEC, int RT, int VALS>
 __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
@@ -74,12 +74,13 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
   constexpr int SLOTS = bwd_block<RT>() / RT;
   constexpr int WIDTH = RT * VALS;  // columns one row slot covers
   using Row = tk::RawRow<T, VEC, RT, VALS>;
-  // dweight partials live in LDS, one float per column per slot; each address
-  // belongs to one thread, so every sum has a fixed order. (Shapes whose
-  // accumulators would exceed 128 KiB are beyond the 64 KiB row budget and
-  // never launched; they keep registers so they still compile.)
-  constexpr bool ACC_LDS = SLOTS * WIDTH * 4 <= 131072;
-  __shared__ float acc_lds[ACC_LDS ? SLOTS * WIDTH : 1];
+  // dweight partials: registers, except for the widest launched rows (1024 threads
+  // x 32 values, beyond the 128 registers a 1024-thread workgroup allows), whose
+  // single slot keeps them in 128 KiB of LDS; each address belongs to one thread.
+  // (1024 x 64 is never launched: rows are limited to 65536 bytes.)
+  constexpr bool ACC_LDS = SLOTS == 1 && RT == 1024 && VALS == 32;
+  // Slot partials are folded through LDS once, at the end (single-wave slots only).
+  __shared__ float fold[SLOTS > 1 || ACC_LDS ? WIDTH : 1];
   __shared__ float scratch[RT / 64];
 
   const int group = blockIdx.x;
@@ -89,106 +90,134 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
   const int group_rows = (rows - 1 - group) / group_size + 1;
   const int iters = (group_rows + SLOTS - 1) / SLOTS;
 
+  // dweight partials of this thread's columns, accumulated over its rows in order.
   float acc[ACC_LDS ? 1 : VALS];
-  float* my_acc = acc_lds + slot * WIDTH;
-  if constexpr (ACC_LDS) {
 #pragma unroll
-    for (int e = 0; e < VALS; ++e) my_acc[tk::row_column<VEC, RT>(e, lane)] = 0.f;
-  } else {
-#pragma unroll
-    for (int e = 0; e < VALS; ++e) acc[e] = 0.f;
+  for (int e = 0; e < VALS; ++e) {
+    if constexpr (ACC_LDS)
+      fold[tk::row_column<VEC, RT>(e, lane)] = 0.f;
+    else
+      acc[e] = 0.f;
   }
 
+  // Rows are software-pipelined where registers allow (not in 1024-thread
+  // workgroups, capped at 128 registers): the next row's loads are issued before
+  // the current row is reduced, and stay in flight across the LDS-only barriers.
+  constexpr bool PREFETCH = RT < 1024 && (VEC > 1 || VALS <= 16);
+  Row xv, dv, iv;
+  float r = 0.f;
+  if (PREFETCH && slot < group_rows) {
+    const int64_t row = static_cast<int64_t>(group) + static_cast<int64_t>(slot) * group_size;
+    xv.load(x + row * x_stride, cols, lane);
+    dv.load(dy + row * dy_stride, cols, lane);
+    if (incoming != nullptr) iv.load(incoming + row * inc_stride, cols, lane);
+    r = rstd[row];
+  }
   for (int it = 0; it < iters; ++it) {
     const int k = it * SLOTS + slot;
-    // Every thread of a multi-wave group runs the same trip count so the block
-    // barriers inside group_allreduce line up; an idle slot computes on zeros.
-    const bool valid = k < group_rows;
+    // Single-wave slots skip missing rows; the threads of a multi-wave group
+    // (SLOTS == 1) always have a row, so the barriers in group_allreduce line up.
+    if (SLOTS > 1 && k >= group_rows) break;
     const int64_t row = static_cast<int64_t>(group) + static_cast<int64_t>(k) * group_size;
-    Row xv, dv, iv, wv;
-    float r = 0.f;
-    if (valid) {
+    if constexpr (!PREFETCH) {
       xv.load(x + row * x_stride, cols, lane);
       dv.load(dy + row * dy_stride, cols, lane);
       if (incoming != nullptr) iv.load(incoming + row * inc_stride, cols, lane);
       r = rstd[row];
-    } else {
-      xv.load(x, 0, lane);  // all zeros
-      dv.load(dy, 0, lane);
     }
+    const bool more = PREFETCH && k + SLOTS < group_rows;
+    Row xn, dn, in;
+    float rn = 0.f;
+    if (more) {
+      const int64_t next = row + static_cast<int64_t>(SLOTS) * group_size;
+      xn.load(x + next * x_stride, cols, lane);
+      dn.load(dy + next * dy_stride, cols, lane);
+      if (incoming != nullptr) in.load(incoming + next * inc_stride, cols, lane);
+      rn = rstd[next];
+    }
+    Row wv;
     wv.load(weight, cols, lane);  // 2*cols bytes, served from cache
     float dot = 0.f;
 #pragma unroll
     for (int e = 0; e < VALS; ++e) {
       const float x_hat = xv.get(e) * r;
       const float d = dv.get(e);
-      if constexpr (ACC_LDS) {
-        my_acc[tk::row_column<VEC, RT>(e, lane)] += d * x_hat;
-      } else {
+      if constexpr (ACC_LDS)
+        fold[tk::row_column<VEC, RT>(e, lane)] += d * x_hat;
+      else
         acc[e] += d * x_hat;
-      }
       dot += (wv.get(e) * d) * x_hat;
     }
     dot = tk::group_allreduce<RT>(dot, tk::SumOp{}, scratch);
     const float mean = dot / static_cast<float>(cols);
-    if (valid) {
 #pragma unroll
-      for (int e = 0; e < VALS; ++e) {
-        const float x_hat = xv.get(e) * r;
-        const float g = wv.get(e) * dv.get(e);
-        float v = r * (g - x_hat * mean);
-        if (incoming != nullptr) v += iv.get(e);
-        xv.set(e, v);
-      }
-      xv.store(dx + row * dx_stride, cols, lane);
+    for (int e = 0; e < VALS; ++e) {
+      const float x_hat = xv.get(e) * r;
+      const float g = wv.get(e) * dv.get(e);
+      float v = r * (g - x_hat * mean);
+      if (incoming != nullptr) v += iv.get(e);
+      xv.set(e, v);
+    }
+    xv.store(dx + row * dx_stride, cols, lane);
+    if (more) {
+      xv = xn;
+      dv = dn;
+      iv = in;
+      r = rn;
     }
   }
 
   float* out = partial + static_cast<int64_t>(group) * cols;
-  if constexpr (!ACC_LDS) {
+  if constexpr (SLOTS == 1) {
 #pragma unroll
     for (int e = 0; e < VALS; ++e) {
       const int c = tk::row_column<VEC, RT>(e, lane);
-      if (c < cols) out[c] = acc[e];
+      if (c < cols) out[c] = ACC_LDS ? fold[c] : acc[e];
     }
   } else {
-    __syncthreads();
-    // Sum the slots in increasing slot order.
-    for (int c = threadIdx.x; c < cols; c += bwd_block<RT>()) {
-      float t = acc_lds[c];
+    // ((slot 0 + slot 1) + slot 2) + ...: one slot at a time, in slot order.
+    for (int s2 = 0; s2 < SLOTS; ++s2) {
+      if (slot == s2) {
 #pragma unroll
-      for (int s2 = 1; s2 < SLOTS; ++s2) t += acc_lds[s2 * WIDTH + c];
-      out[c] = t;
+        for (int e = 0; e < VALS; ++e) {
+          const int c = tk::row_column<VEC, RT>(e, lane);
+          if (c < cols) fold[c] = s2 == 0 ? acc[e] : fold[c] + acc[e];
+        }
+      }
+      __syncthreads();
     }
+    for (int c = threadIdx.x; c < cols; c += bwd_block<RT>()) out[c] = fold[c];
   }
   if (threadIdx.x == 0) counts[group] = 1;
 }
 
-constexpr int kStage2Waves = 8;
+constexpr int kStage2Cols = 32;    // columns per workgroup: 128-byte row segments
+constexpr int kStage2Slices = 32;  // interleaved partial-row slices per column
+constexpr int kStage2Threads = kStage2Cols * kStage2Slices;
 
-// dw[c] = sum over g of partial[g][c]. Block = 64 columns x 8 waves; wave w
-// sums a contiguous slice of g in increasing order, then the eight slice sums
-// are added in wave order.
+// dw[c] = sum over g of partial[g][c]. Thread (slice s, column c) sums the rows
+// g = s, s + 32, s + 64, ... in increasing order; the 32 slice sums are then added
+// in slice order. Narrow column blocks give cols / 32 workgroups, enough to keep
+// many partial rows in flight.
 template <typename T>
-__global__ __launch_bounds__(64 * kStage2Waves) void rmsnorm_bwd_stage2_kernel(
+__global__ __launch_bounds__(kStage2Threads) void rmsnorm_bwd_stage2_kernel(
     const float* __restrict__ partial, T* __restrict__ dw, int group_count, int cols) {
-  __shared__ float slices[kStage2Waves][64];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int c = blockIdx.x * 64 + lane;
-  const int per = (group_count + kStage2Waves - 1) / kStage2Waves;
-  const int g0 = wave * per;
-  const int g1 = min(group_count, g0 + per);
+  __shared__ float slices[kStage2Slices][kStage2Cols];
+  const int col = threadIdx.x % kStage2Cols;
+  const int slice = threadIdx.x / kStage2Cols;
+  const int c = blockIdx.x * kStage2Cols + col;
   float s = 0.f;
   if (c < cols) {
-    for (int g = g0; g < g1; ++g) s += partial[static_cast<int64_t>(g) * cols + c];
+#pragma unroll 16
+    for (int g = slice; g < group_count; g += kStage2Slices)
+      s += partial[static_cast<int64_t>(g) * cols + c];
   }
-  slices[wave][lane] = s;
+  slices[slice][col] = s;
   __syncthreads();
-  if (wave == 0 && c < cols) {
-    float t = slices[0][lane];
+  if (slice == 0 && c < cols) {
+    float t = slices[0][col];
 #pragma unroll
-    for (int w = 1; w < kStage2Waves; ++w) t += slices[w][lane];
+    for (int i = 1; i < kStage2Slices; ++i) t += slices[i][col];
     dw[c] = tk::from_f32<T>(t);
   }
 }
@@ -264,6 +293,9 @@ extern "C" int tk_rmsnorm_bwd_stage1(int dtype, void* dx, const void* dy, const 
       {x_row_stride, dy_row_stride, incoming_dx ? incoming_dx_row_stride : 0, dx_row_stride});
   tk::RowShape shape;
   if (check_rows("rmsnorm_bwd_stage1", dtype, rows, cols, vector_ok, &shape)) return 1;
+  // Stage 1 holds three row tensors plus the dweight partials per thread: prefer at
+  // most 16 values per thread (more waves per row) so several workgroups fit per CU.
+  tk::pick_row_shape(cols, &shape, 16);
   const dim3 grid(static_cast<unsigned>(group_count));
   hipStream_t s = tk::as_stream(stream);
   int32_t* counts = locks + group_size;
@@ -286,10 +318,10 @@ extern "C" int tk_rmsnorm_bwd_stage2(int dtype, const float* partial_dw, void* d
   if (group_count <= 0 || cols <= 0 || group_count > INT32_MAX || cols > INT32_MAX ||
       group_count * cols > INT32_MAX)
     return tk::fail("rmsnorm_bwd_stage2: bad partial shape");
-  const dim3 grid(static_cast<unsigned>(tk::cdiv(cols, 64)));
+  const dim3 grid(static_cast<unsigned>(tk::cdiv(cols, kStage2Cols)));
   hipStream_t s = tk::as_stream(stream);
   TK_DISPATCH_DTYPE(dtype, T,
-    hipLaunchKernelGGL((rmsnorm_bwd_stage2_kernel<T>), grid, dim3(64 * kStage2Waves), 0, s,
+    hipLaunchKernelGGL((rmsnorm_bwd_stage2_kernel<T>), grid, dim3(kStage2Threads), 0, s,
                        partial_dw, static_cast<T*>(dw), (int)group_count, (int)cols));
   return tk::check_launch("rmsnorm_bwd_stage2");
 }

@@ -110,6 +110,13 @@ __device__ __forceinline__ float wave_allreduce(float v, Op op) {
 // All-reduce over a group of RT threads (RT a multiple of 64). For RT > 64 the
 // per-wave results meet in `scratch` (RT/64 floats of LDS); the call contains
 // two block barriers, so every thread of the block must reach it.
+// Workgroup barrier that orders LDS only: this wave's LDS operations complete,
+// then s_barrier. Unlike __syncthreads() it does not wait for outstanding global
+// loads, so rows prefetched before it stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <int RT, typename Op>
 __device__ __forceinline__ float group_allreduce(float v, Op op, float* scratch) {
   v = wave_allreduce(v, op);
@@ -117,11 +124,11 @@ __device__ __forceinline__ float group_allreduce(float v, Op op, float* scratch)
     constexpr int W = RT / 64;
     const int wave = (threadIdx.x % RT) / 64;
     if ((threadIdx.x & 63) == 0) scratch[wave] = v;
-    __syncthreads();
+    lds_barrier();
     float r = scratch[0];
 #pragma unroll
     for (int w = 1; w < W; ++w) r = op(r, scratch[w]);
-    __syncthreads();
+    lds_barrier();  // every wave has read scratch before it is reused
     v = r;
   }
   return v;

@@ -15,9 +15,10 @@ import math
 MAX_FEATURE_BYTES = 65_536
 EPS = 1e-5
 
-# Groups of the backward dweight reduction: one workgroup per group, and
-# MI355X has 256 compute units.
-DEFAULT_GROUPS = 256
+# Groups of the backward dweight reduction: one workgroup per group. 512 groups
+# keep two 4-wave workgroups per compute unit (256 CUs) streaming rows, while the
+# float32 partial buffer stays at 512 x columns.
+DEFAULT_GROUPS = 512
 
 
 def validate_epsilon(eps: float) -> None:
@@ -61,8 +62,8 @@ def group_size_m(columns: int) -> int:
 
     The reference trades lock contention against stage-two work
     (``_norm_common.py:63-75``). Without locks the only concern is filling the
-    GPU while keeping the float32 partial buffer small, so every width uses one
-    group per compute unit.
+    GPU while keeping the float32 partial buffer small, so every width uses two
+    groups per compute unit.
     """
     del columns
     return DEFAULT_GROUPS
