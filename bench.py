@@ -17,7 +17,10 @@ committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when present.
 ``cpu_baseline`` times the CPU oracle (oracle/tklab_oracle.c) on a bounded
 row sample of the same workload on the host cores.
 ``kernels`` times every other BASELINE configuration (softmax, SwiGLU, RoPE,
-GEMM, attention) per kernel with a 1 GiB cache flush before each launch.
+GEMM, attention) per kernel. Memory-bound rows run back-to-back launches that
+rotate over enough copies of their tensors to touch at least 1 GiB (four times
+the 256 MiB last-level cache), so they measure steady HBM streaming without
+cache reuse; MFMA rows flush 1 GiB before each launch.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu]
 """
@@ -201,8 +204,25 @@ def kernel_table(torch, device) -> list[dict]:
         torch.cuda.synchronize()
         return statistics.median(x.elapsed_time(y) for x, y in times)
 
-    def mem_row(name, config, fn, nbytes, reps=20):
-        ms = timed(fn, reps)
+    def streamed(make, nbytes: int, reps: int) -> float:
+        """Mean ms per launch, back to back, rotating over >= 1 GiB of tensor copies."""
+        copies = max(1, -(-(1 << 30) // nbytes))
+        fns = [make(i) for i in range(copies)]
+        for fn in fns:
+            fn()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for i in range(reps):
+            fns[i % copies]()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    def mem_row(name, config, make, nbytes, reps=30):
+        """`make(i)` returns the launch for tensor copy i (copy 0 may reuse the originals)."""
+        ms = streamed(make, nbytes, reps)
         gbps = nbytes / ms / 1e6
         rows.append({"kernel": name, "config": config, "ms": round(ms, 4), "bytes": nbytes,
                      "GB/s": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4)})
@@ -217,9 +237,14 @@ def kernel_table(torch, device) -> list[dict]:
     bf16 = torch.bfloat16
     # Config 1: softmax float32 [4096, 4096].
     x = torch.randn(4096, 4096, device=device, generator=g)
-    y = torch.empty_like(x)
-    mem_row("tk_softmax_fwd", "f32 4096x4096", lambda: sm._launch((x,), y), 2 * x.numel() * 4)
-    del x, y
+
+    def softmax_copy(i):
+        xi = x if i == 0 else x.clone()
+        yi = torch.empty_like(x)
+        return lambda: sm._launch((xi,), yi)
+
+    mem_row("tk_softmax_fwd", "f32 4096x4096", softmax_copy, 2 * x.numel() * 4)
+    del x
     # Config 3: SwiGLU bf16 [16384, 14336].
     gate = torch.randn(16384, 14336, device=device, dtype=bf16, generator=g)
     up = torch.randn(16384, 14336, device=device, dtype=bf16, generator=g)
@@ -227,9 +252,10 @@ def kernel_table(torch, device) -> list[dict]:
     out = torch.empty_like(gate)
     dv = torch.empty_like(gate)
     n = gate.numel()
-    mem_row("tk_swiglu_fwd", "bf16 16384x14336", lambda: sg._launch_forward(up, gate, out), 3 * n * 2)
+    mem_row("tk_swiglu_fwd", "bf16 16384x14336",
+            lambda i: (lambda: sg._launch_forward(up, gate, out)), 3 * n * 2)
     mem_row("tk_swiglu_bwd", "bf16 16384x14336",
-            lambda: sg._launch_backward_into(dy, up, gate, dv, out), 5 * n * 2)
+            lambda i: (lambda: sg._launch_backward_into(dy, up, gate, dv, out)), 5 * n * 2)
     del gate, up, dy, out, dv
     # Config 3: RoPE on q [4, 32, 4096, 128] viewed [524288, 128], per-row tables.
     q = torch.randn(4 * 32 * 4096, 128, device=device, dtype=bf16, generator=g)
@@ -237,13 +263,19 @@ def kernel_table(torch, device) -> list[dict]:
     ang = torch.arange(4096, device=device, dtype=torch.float32)[:, None] * inv[None, :]
     cos = torch.cos(ang).to(bf16).repeat(128, 1)
     sin = torch.sin(ang).to(bf16).repeat(128, 1)
-    yq = torch.empty_like(q)
-    dq = torch.empty_like(q)
-    mem_row("tk_rope_fwd", "bf16 [4,32,4096,128]", lambda: rp._launch_forward(q, cos, sin, yq),
+
+    def rope_copy(i, backward):
+        qi, ci, si = (q, cos, sin) if i == 0 else (q.clone(), cos.clone(), sin.clone())
+        out = torch.empty_like(q)
+        if backward:
+            return lambda: rp._launch_backward_into(qi, q, ci, si, out, None, None)
+        return lambda: rp._launch_forward(qi, ci, si, out)
+
+    mem_row("tk_rope_fwd", "bf16 [4,32,4096,128]", lambda i: rope_copy(i, False),
             3 * q.numel() * 2)
-    mem_row("tk_rope_bwd", "bf16 [4,32,4096,128] dx only",
-            lambda: rp._launch_backward_into(yq, q, cos, sin, dq, None, None), 3 * q.numel() * 2)
-    del q, cos, sin, yq, dq
+    mem_row("tk_rope_bwd", "bf16 [4,32,4096,128] dx only", lambda i: rope_copy(i, True),
+            3 * q.numel() * 2)
+    del q, cos, sin
     # Config 4: GEMM.
     for dt_name, dt in (("float16", torch.float16), ("bfloat16", bf16)):
         for m, nn, k in ((8192, 8192, 8192), (4096, 4096, 4096), (8191, 8192, 8192)):

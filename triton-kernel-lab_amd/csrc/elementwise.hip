@@ -1,11 +1,12 @@
 // Elementwise kernels: SwiGLU forward/backward and rotate-half RoPE
 // forward/backward.
 //
-// Every thread handles one chunk of VEC contiguous elements per step
-// (VEC = 16/sizeof(T): one 128-bit access per tensor) and walks a grid-stride
-// loop over all chunks of the (rows x chunks_per_row) problem. Row strides are
-// honoured, so row-sliced views need no copy; the row of a chunk comes from a
-// multiply-shift division by chunks_per_row.
+// A chunk is VEC contiguous elements (VEC = 16/sizeof(T): one 128-bit access per
+// tensor). A workgroup pass takes kUnroll * kBlock consecutive chunks; each thread
+// issues the loads of its kUnroll chunks before any arithmetic, so every wave keeps
+// a contiguous 4 KiB run per tensor in flight (one chunk per thread, or chunks far
+// apart, leave HBM well short of its bandwidth). Row strides are honoured, so row-sliced views need no copy; the
+// row of a chunk comes from a multiply-shift division by chunks_per_row.
 //
 // Floating-point contraction is disabled so each product and sum is rounded
 // separately, the same way PyTorch's pointwise ops evaluate these formulas.
@@ -25,16 +26,28 @@ __device__ __forceinline__ float stable_sigmoid(float z) {
   return z >= 0.f ? 1.0f / d : e / d;
 }
 
+constexpr int kUnroll = 4;
+constexpr int64_t kMaxBlocks = 8192;  // 32 workgroups per CU; the loop covers the rest
+
 struct Grid1D {
   unsigned blocks;
 };
 
 inline Grid1D chunk_grid(int64_t chunks) {
-  // Enough blocks to fill 256 CUs many times over; the loop covers the rest.
-  int64_t blocks = tk::cdiv(chunks, kBlock);
-  const int64_t cap = 256 * 64;
-  if (blocks > cap) blocks = cap;
+  int64_t blocks = tk::cdiv(chunks, kBlock * kUnroll);
+  if (blocks > kMaxBlocks) blocks = kMaxBlocks;
   return {static_cast<unsigned>(blocks)};
+}
+
+// Chunk i of a row-major problem: its row and the first element's column.
+struct ChunkPos {
+  int row, col;
+};
+
+template <int VEC>
+__device__ __forceinline__ ChunkPos chunk_pos(int i, const tk::FastDiv& per_row) {
+  const int row = per_row.div(i);
+  return {row, (i - row * static_cast<int>(per_row.d)) * VEC};
 }
 
 // ------------------------------------------------------------------ SwiGLU
@@ -44,15 +57,28 @@ template <typename T, int VEC>
 __global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(
     const T* __restrict__ value, const T* __restrict__ gate, T* __restrict__ y, int chunks,
     tk::FastDiv per_row, int64_t vs, int64_t gs, int64_t ys) {
-  for (int i = blockIdx.x * kBlock + threadIdx.x; i < chunks; i += gridDim.x * kBlock) {
-    const int row = per_row.div(i);
-    const int c = (i - row * static_cast<int>(per_row.d)) * VEC;
-    float v[VEC], g[VEC];
-    tk::load_vec<T, VEC>(value + row * vs + c, v);
-    tk::load_vec<T, VEC>(gate + row * gs + c, g);
+  // A workgroup pass covers kUnroll * kBlock consecutive chunks (one 4 KiB run per
+  // wave and tensor), then the grid strides on.
+  const int stride = gridDim.x * kBlock * kUnroll;
+  for (int i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
+    float v[kUnroll][VEC], g[kUnroll][VEC];
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) v[j] = v[j] * g[j] * stable_sigmoid(g[j]);
-    tk::store_vec<T, VEC>(y + row * ys + c, v);
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = i0 + u * kBlock;
+      if (i >= chunks) break;
+      const ChunkPos p = chunk_pos<VEC>(i, per_row);
+      tk::load_vec<T, VEC>(value + p.row * vs + p.col, v[u]);
+      tk::load_vec<T, VEC>(gate + p.row * gs + p.col, g[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = i0 + u * kBlock;
+      if (i >= chunks) break;
+      const ChunkPos p = chunk_pos<VEC>(i, per_row);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) v[u][j] = v[u][j] * g[u][j] * stable_sigmoid(g[u][j]);
+      tk::store_vec<T, VEC>(y + p.row * ys + p.col, v[u]);
+    }
   }
 }
 
@@ -63,23 +89,37 @@ __global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(
     const T* __restrict__ dy, const T* __restrict__ value, const T* __restrict__ gate,
     T* __restrict__ dvalue, T* __restrict__ dgate, int chunks, tk::FastDiv per_row, int64_t dys,
     int64_t vs, int64_t gs, int64_t dvs, int64_t dgs) {
-  for (int i = blockIdx.x * kBlock + threadIdx.x; i < chunks; i += gridDim.x * kBlock) {
-    const int row = per_row.div(i);
-    const int c = (i - row * static_cast<int>(per_row.d)) * VEC;
-    float d[VEC], v[VEC], g[VEC], dv[VEC], dg[VEC];
-    tk::load_vec<T, VEC>(dy + row * dys + c, d);
-    tk::load_vec<T, VEC>(value + row * vs + c, v);
-    tk::load_vec<T, VEC>(gate + row * gs + c, g);
+  // A workgroup pass covers kUnroll * kBlock consecutive chunks (one 4 KiB run per
+  // wave and tensor), then the grid strides on.
+  const int stride = gridDim.x * kBlock * kUnroll;
+  for (int i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
+    float d[kUnroll][VEC], v[kUnroll][VEC], g[kUnroll][VEC];
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      const float sg = stable_sigmoid(g[j]);
-      const float silu = g[j] * sg;
-      const float dsilu = sg * (1.0f + g[j] * (1.0f - sg));
-      dv[j] = d[j] * silu;
-      dg[j] = d[j] * v[j] * dsilu;
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = i0 + u * kBlock;
+      if (i >= chunks) break;
+      const ChunkPos p = chunk_pos<VEC>(i, per_row);
+      tk::load_vec<T, VEC>(dy + p.row * dys + p.col, d[u]);
+      tk::load_vec<T, VEC>(value + p.row * vs + p.col, v[u]);
+      tk::load_vec<T, VEC>(gate + p.row * gs + p.col, g[u]);
     }
-    tk::store_vec<T, VEC>(dvalue + row * dvs + c, dv);
-    tk::store_vec<T, VEC>(dgate + row * dgs + c, dg);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = i0 + u * kBlock;
+      if (i >= chunks) break;
+      const ChunkPos p = chunk_pos<VEC>(i, per_row);
+      float dv[VEC], dg[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        const float sg = stable_sigmoid(g[u][j]);
+        const float silu = g[u][j] * sg;
+        const float dsilu = sg * (1.0f + g[u][j] * (1.0f - sg));
+        dv[j] = d[u][j] * silu;
+        dg[j] = d[u][j] * v[u][j] * dsilu;
+      }
+      tk::store_vec<T, VEC>(dvalue + p.row * dvs + p.col, dv);
+      tk::store_vec<T, VEC>(dgate + p.row * dgs + p.col, dg);
+    }
   }
 }
 
@@ -91,23 +131,37 @@ __global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ cosv, const T* __restrict__ sinv,
     T* __restrict__ y, int chunks, tk::FastDiv per_row, int half, int64_t xs, int64_t cs,
     int64_t ss, int64_t ys) {
-  for (int i = blockIdx.x * kBlock + threadIdx.x; i < chunks; i += gridDim.x * kBlock) {
-    const int row = per_row.div(i);
-    const int c = (i - row * static_cast<int>(per_row.d)) * VEC;
-    float x1[VEC], x2[VEC], co[VEC], si[VEC], y1[VEC], y2[VEC];
-    const T* xr = x + row * xs;
-    tk::load_vec<T, VEC>(xr + c, x1);
-    tk::load_vec<T, VEC>(xr + half + c, x2);
-    tk::load_vec<T, VEC>(cosv + row * cs + c, co);
-    tk::load_vec<T, VEC>(sinv + row * ss + c, si);
+  // A workgroup pass covers kUnroll * kBlock consecutive chunks (one 4 KiB run per
+  // wave and tensor), then the grid strides on.
+  const int stride = gridDim.x * kBlock * kUnroll;
+  for (int i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
+    float x1[kUnroll][VEC], x2[kUnroll][VEC], co[kUnroll][VEC], si[kUnroll][VEC];
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      y1[j] = x1[j] * co[j] - x2[j] * si[j];
-      y2[j] = x2[j] * co[j] + x1[j] * si[j];
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = i0 + u * kBlock;
+      if (i >= chunks) break;
+      const ChunkPos p = chunk_pos<VEC>(i, per_row);
+      const T* xr = x + p.row * xs;
+      tk::load_vec<T, VEC>(xr + p.col, x1[u]);
+      tk::load_vec<T, VEC>(xr + half + p.col, x2[u]);
+      tk::load_vec<T, VEC>(cosv + p.row * cs + p.col, co[u]);
+      tk::load_vec<T, VEC>(sinv + p.row * ss + p.col, si[u]);
     }
-    T* yr = y + row * ys;
-    tk::store_vec<T, VEC>(yr + c, y1);
-    tk::store_vec<T, VEC>(yr + half + c, y2);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = i0 + u * kBlock;
+      if (i >= chunks) break;
+      const ChunkPos p = chunk_pos<VEC>(i, per_row);
+      float y1[VEC], y2[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        y1[j] = x1[u][j] * co[u][j] - x2[u][j] * si[u][j];
+        y2[j] = x2[u][j] * co[u][j] + x1[u][j] * si[u][j];
+      }
+      T* yr = y + p.row * ys;
+      tk::store_vec<T, VEC>(yr + p.col, y1);
+      tk::store_vec<T, VEC>(yr + half + p.col, y2);
+    }
   }
 }
 
@@ -120,37 +174,51 @@ __global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
     int chunks, tk::FastDiv per_row, int half, int64_t dys, int64_t xs, int64_t cs, int64_t ss,
     int64_t dxs, int64_t dcs, int64_t dss) {
   const bool need_x = dcos != nullptr || dsin != nullptr;
-  for (int i = blockIdx.x * kBlock + threadIdx.x; i < chunks; i += gridDim.x * kBlock) {
-    const int row = per_row.div(i);
-    const int c = (i - row * static_cast<int>(per_row.d)) * VEC;
-    float d1[VEC], d2[VEC], co[VEC], si[VEC], o1[VEC], o2[VEC];
-    const T* dyr = dy + row * dys;
-    tk::load_vec<T, VEC>(dyr + c, d1);
-    tk::load_vec<T, VEC>(dyr + half + c, d2);
-    tk::load_vec<T, VEC>(cosv + row * cs + c, co);
-    tk::load_vec<T, VEC>(sinv + row * ss + c, si);
+  // A workgroup pass covers kUnroll * kBlock consecutive chunks (one 4 KiB run per
+  // wave and tensor), then the grid strides on.
+  const int stride = gridDim.x * kBlock * kUnroll;
+  for (int i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
+    float d1[kUnroll][VEC], d2[kUnroll][VEC], co[kUnroll][VEC], si[kUnroll][VEC];
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      o1[j] = d1[j] * co[j] + d2[j] * si[j];
-      o2[j] = d2[j] * co[j] - d1[j] * si[j];
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = i0 + u * kBlock;
+      if (i >= chunks) break;
+      const ChunkPos p = chunk_pos<VEC>(i, per_row);
+      const T* dyr = dy + p.row * dys;
+      tk::load_vec<T, VEC>(dyr + p.col, d1[u]);
+      tk::load_vec<T, VEC>(dyr + half + p.col, d2[u]);
+      tk::load_vec<T, VEC>(cosv + p.row * cs + p.col, co[u]);
+      tk::load_vec<T, VEC>(sinv + p.row * ss + p.col, si[u]);
     }
-    T* dxr = dx + row * dxs;
-    tk::store_vec<T, VEC>(dxr + c, o1);
-    tk::store_vec<T, VEC>(dxr + half + c, o2);
-    if (need_x) {
-      float x1[VEC], x2[VEC];
-      const T* xr = x + row * xs;
-      tk::load_vec<T, VEC>(xr + c, x1);
-      tk::load_vec<T, VEC>(xr + half + c, x2);
-      if (dcos != nullptr) {
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) o1[j] = d1[j] * x1[j] + d2[j] * x2[j];
-        tk::store_vec<T, VEC>(dcos + row * dcs + c, o1);
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = i0 + u * kBlock;
+      if (i >= chunks) break;
+      const ChunkPos p = chunk_pos<VEC>(i, per_row);
+      float o1[VEC], o2[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        o1[j] = d1[u][j] * co[u][j] + d2[u][j] * si[u][j];
+        o2[j] = d2[u][j] * co[u][j] - d1[u][j] * si[u][j];
       }
-      if (dsin != nullptr) {
+      T* dxr = dx + p.row * dxs;
+      tk::store_vec<T, VEC>(dxr + p.col, o1);
+      tk::store_vec<T, VEC>(dxr + half + p.col, o2);
+      if (need_x) {
+        float x1[VEC], x2[VEC];
+        const T* xr = x + p.row * xs;
+        tk::load_vec<T, VEC>(xr + p.col, x1);
+        tk::load_vec<T, VEC>(xr + half + p.col, x2);
+        if (dcos != nullptr) {
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) o2[j] = -d1[j] * x2[j] + d2[j] * x1[j];
-        tk::store_vec<T, VEC>(dsin + row * dss + c, o2);
+          for (int j = 0; j < VEC; ++j) o1[j] = d1[u][j] * x1[j] + d2[u][j] * x2[j];
+          tk::store_vec<T, VEC>(dcos + p.row * dcs + p.col, o1);
+        }
+        if (dsin != nullptr) {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) o2[j] = -d1[u][j] * x2[j] + d2[u][j] * x1[j];
+          tk::store_vec<T, VEC>(dsin + p.row * dss + p.col, o2);
+        }
       }
     }
   }
@@ -173,7 +241,9 @@ int check_problem(const char* what, int dtype, int64_t rows, int64_t width, int 
   if (rows <= 0 || width <= 0) return tk::fail("%s: empty problem", what);
   *chunks_per_row = width / vec;
   *chunks = rows * *chunks_per_row;
-  if (*chunks > INT32_MAX - 64 * kBlock * 256) return tk::fail("%s: problem too large", what);
+  // Chunk indices run to chunks + (grid stride) in 32-bit arithmetic.
+  if (*chunks > INT32_MAX - kUnroll * kMaxBlocks * kBlock)
+    return tk::fail("%s: problem too large", what);
   return 0;
 }
 
