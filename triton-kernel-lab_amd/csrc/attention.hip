@@ -836,6 +836,11 @@ extern "C" int tk_attn_bwd_dkdv(int dtype, const void* q, const void* k, const v
   if (bwd_shape("attn_bwd_dkdv", dtype, ptrs, 8, batch, heads, seq, head_dim, strides, sm_scale,
                 128, &s))
     return 1;
+  if (tk::attn_bwd_dma_applies(seq, head_dim, strides)) {
+    tk::attn_bwd_dkdv_dma_launch(dtype, q, k, v, dout, dk, dv, lse, delta, batch, heads, seq,
+                                 head_dim, strides, sm_scale, causal != 0, tk::as_stream(stream));
+    return tk::check_launch("attn_bwd_dkdv");
+  }
   const dim3 grid(static_cast<unsigned>(s.tiles));
   TK_ATTN_DISPATCH(dtype, head_dim, causal, attn_bwd_dkdv_kernel, grid, (const T*)q, (const T*)k,
                    (const T*)v, (const T*)dout, (T*)dk, (T*)dv, lse, delta, s);
@@ -851,6 +856,11 @@ extern "C" int tk_attn_bwd_dq(int dtype, const void* q, const void* k, const voi
   if (bwd_shape("attn_bwd_dq", dtype, ptrs, 7, batch, heads, seq, head_dim, strides, sm_scale, 128,
                 &s))
     return 1;
+  if (tk::attn_bwd_dma_applies(seq, head_dim, strides)) {
+    tk::attn_bwd_dq_dma_launch(dtype, q, k, v, dout, dq, lse, delta, batch, heads, seq, head_dim,
+                               strides, sm_scale, causal != 0, tk::as_stream(stream));
+    return tk::check_launch("attn_bwd_dq");
+  }
   const dim3 grid(static_cast<unsigned>(s.tiles));
   TK_ATTN_DISPATCH(dtype, head_dim, causal, attn_bwd_dq_kernel, grid, (const T*)q, (const T*)k,
                    (const T*)v, (const T*)dout, (T*)dq, lse, delta, s);

@@ -1,5 +1,5 @@
 // Internal interface between the attention entry points (attention.hip) and the
-// buffer->LDS DMA forward kernel (attention_fwd.hip).
+// buffer->LDS DMA kernels (attention_fwd.hip, attention_bwd.hip).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <cstdint>
@@ -16,5 +16,21 @@ void attn_fwd_dma_launch(int dtype, const void* q, const void* k, const void* v,
                          const int64_t* q_strides, const int64_t* k_strides,
                          const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
                          bool causal, hipStream_t stream);
+
+// True when one head's rows (shared layout of q, k, v, dO, dQ, dK, dV) span less than
+// 2 GiB. The caller has already checked dtype, head_dim and 16-byte row alignment.
+bool attn_bwd_dma_applies(int64_t seq, int64_t head_dim, const int64_t* strides);
+
+void attn_bwd_dkdv_dma_launch(int dtype, const void* q, const void* k, const void* v,
+                              const void* dout, void* dk, void* dv, const float* lse,
+                              const float* delta, int64_t batch, int64_t heads, int64_t seq,
+                              int64_t head_dim, const int64_t* strides, float sm_scale,
+                              bool causal, hipStream_t stream);
+
+void attn_bwd_dq_dma_launch(int dtype, const void* q, const void* k, const void* v,
+                            const void* dout, void* dq, const float* lse, const float* delta,
+                            int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                            const int64_t* strides, float sm_scale, bool causal,
+                            hipStream_t stream);
 
 }  // namespace tk

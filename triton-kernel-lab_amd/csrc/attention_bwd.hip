@@ -1,0 +1,656 @@
+// Flash attention recompute backward for head_dim 64/128 (f16/bf16) on CDNA4 MFMA: the
+// dK/dV and dQ passes behind tk_attn_bwd_dkdv / tk_attn_bwd_dq
+// (src/tklab/kernels/flash_attention.py:383-533: P = exp2(S * scale * log2(e) - lse),
+// dS = P (dP - delta), dV = P^T dO, dK = scale dS^T Q, dQ = scale dS K; each output is
+// written by exactly one workgroup, so both passes are deterministic).
+//
+// dK/dV pass: a workgroup owns 128 keys (4 wave64s x 32, one wave per SIMD) and walks the
+// query blocks of 64. K and V fragments stay in registers. Per query block each wave
+// computes S = Q K^T and dP = dO V^T (accumulator lane = one key, so P and dS feed the
+// next MFMAs as B operands straight from registers), then dV^T += dO^T P and
+// dK^T += Q^T dS with dO^T / Q^T read transposed (ds_read_b64_tr_b16) from the same
+// row-major tiles that S and dP read with ds_read_b128.
+//
+// dQ pass: a workgroup owns 128 queries (4 waves x 32) and walks the key blocks of 64,
+// like the forward: S^T = K Q^T and dP^T = V dO^T (lane = one query, so lse and delta
+// are one value per lane), dQ^T += K^T dS^T with K^T read transposed.
+//
+// Tiles reach LDS by buffer->LDS DMA into 3-stage rings, two blocks ahead, one barrier
+// per block. Tiles read both ways (Q, dO in the dK/dV pass; K in the dQ pass) store the
+// 16-byte chunk c of row r at slot c ^ dual_swz(r), which keeps both the 16-row
+// ds_read_b128 phases and the 4-row x 64-byte transposed phases on 64 distinct banks.
+#include "attention.hpp"
+#include "attention_dma.hpp"
+
+namespace {
+
+using namespace tk_attn;
+
+constexpr int kThreads = 256;  // 4 waves, one per SIMD
+
+template <int N>
+__device__ __forceinline__ void wait_lgkm_n() {
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
+}
+
+struct BwdShape {
+  int heads, seq;
+  int64_t st[3];  // batch, head, sequence strides shared by q, k, v, dO, dQ, dK, dV
+  float scale, scale_log2;
+  int blocks_per_head, tiles;
+  uint32_t head_bytes;  // extent of one head's rows
+};
+
+template <int D>
+struct BwdGeo {
+  static constexpr int WAVES = 4, LW = 32;     // rows (keys or queries) per wave
+  static constexpr int BW = WAVES * LW;        // rows per workgroup: 128
+  static constexpr int BB = 64;                // rows per streamed block
+  static constexpr int KS = D / 16, DT = D / 32;
+  static constexpr int RB = D * 2;             // bytes per row
+  static constexpr int TILE = BB * RB;         // bytes per streamed tile
+  static constexpr int STAGES = 3;
+  static constexpr int ROWS_PER_DMA = 1024 / RB;
+  static constexpr int DMA_PER_TILE = TILE / 1024 / WAVES;  // per wave
+  static constexpr int SLOTS = RB / 16;        // 16-byte slots per row
+  // Layout for tiles read only with ds_read_b128 (16 rows, one chunk per phase).
+  static __device__ __forceinline__ int row_swz(int r) {
+    return D == 128 ? (r & 15) : ((r >> 1) & 7);
+  }
+  // Layout for tiles also read with ds_read_b64_tr_b16 (4 rows x 4 chunks per phase).
+  static __device__ __forceinline__ int dual_swz(int r) {
+    return D == 128 ? (((r & 3) << 2) | ((r >> 2) & 3))
+                    : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
+  }
+};
+
+// Source offset (bytes, tile-relative row) of DMA `x` of this wave for a [64][D] tile
+// stored with swizzle `swz`.
+template <int D, bool DUAL>
+__device__ __forceinline__ uint32_t tile_src(int wave, int x, int lane, int64_t row_stride) {
+  using G = BwdGeo<D>;
+  const int id = wave * G::DMA_PER_TILE + x;
+  const int row = id * G::ROWS_PER_DMA + lane / G::SLOTS;
+  const int slot = lane % G::SLOTS;
+  const int chunk = slot ^ (DUAL ? G::dual_swz(row) : G::row_swz(row));
+  return uint32_t(row * row_stride + chunk * 8) * 2u;
+}
+
+// Lane address (bytes, inside a tile) of the A-operand fragment for a 32-row tile read
+// with ds_read_b128: row lane % 32, chunk 2 kk + lane / 32.
+template <int D, bool DUAL>
+__device__ __forceinline__ uint32_t frag_addr(int lane, int kk) {
+  using G = BwdGeo<D>;
+  const int row = lane & 31;
+  const int swz = DUAL ? G::dual_swz(row) : G::row_swz(row);
+  return row * G::RB + (((2 * kk + (lane >> 5)) ^ swz) * 16);
+}
+
+// Lane address of a transposed read (ds_read_b64_tr_b16) of feature tile dt: rows
+// 4 hi + j + half8 (k-index 0..3 for half8 = 0, 4..7 for half8 = 8; +16 per 16-row
+// step), features 32 dt + 16 g + 4 q. The dual swizzle uses row bits 0..3, so the
+// two row groups get their own addresses; only the step (row bits 4..5) is folded
+// into the instruction's immediate offset.
+template <int D>
+__device__ __forceinline__ uint32_t tr_addr(int lane, int dt, int half8) {
+  using G = BwdGeo<D>;
+  const int g = (lane >> 4) & 1, j = (lane & 15) >> 2, q = lane & 3, hi = lane >> 5;
+  const int row = 4 * hi + j + half8;
+  const int chunk = 2 * (2 * dt + g) + (q >> 1);
+  return row * G::RB + ((chunk ^ G::dual_swz(row)) * 16) + (q & 1) * 8;
+}
+
+// Transposed fragment of the 16 rows starting at ROW0 (a multiple of 16).
+template <int ROW0, int RB>
+__device__ __forceinline__ i32x4 read_tr(uint32_t addr0, uint32_t addr8) {
+  const i32x2 a = lds_read_tr16<ROW0 * RB>(addr0);
+  const i32x2 b = lds_read_tr16<ROW0 * RB>(addr8);
+  return i32x4{a[0], a[1], b[0], b[1]};
+}
+
+template <int RB>
+__device__ __forceinline__ i32x4 read_tr_step(int step, uint32_t addr0, uint32_t addr8) {
+  switch (step) {
+    case 0: return read_tr<0, RB>(addr0, addr8);
+    case 1: return read_tr<16, RB>(addr0, addr8);
+    case 2: return read_tr<32, RB>(addr0, addr8);
+    default: return read_tr<48, RB>(addr0, addr8);
+  }
+}
+
+// Row fragment (ds_read_b128) of row tile `mt` (32 rows = 32 * RB bytes).
+template <int RB>
+__device__ __forceinline__ i32x4 read_row(int mt, uint32_t addr) {
+  return mt == 0 ? lds_read_b128<0>(addr) : lds_read_b128<32 * RB>(addr);
+}
+
+
+// DMA of one [64][D] tile of each of two tensors (rsrc a -> stage, rsrc b -> stage + TILE):
+// this wave's DMA_PER_TILE loads of each, `blk_off` bytes into the head.
+template <int D>
+__device__ __forceinline__ void dma_tiles(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
+                                          char* stage, const uint32_t* a_src,
+                                          const uint32_t* b_src, uint32_t blk_off, int wave) {
+  using G = BwdGeo<D>;
+#pragma unroll
+  for (int x = 0; x < G::DMA_PER_TILE; ++x) {
+    const int id = wave * G::DMA_PER_TILE + x;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(stage + id * 1024), 16, a_src[x],
+                                             blk_off, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(stage + G::TILE + id * 1024), 16,
+                                             b_src[x], blk_off, 0, 0);
+  }
+}
+
+// DMA of 32 statistics floats (lanes 0..31, 4 bytes each) to `dst`.
+__device__ __forceinline__ void dma_stats(__amdgpu_buffer_rsrc_t rs, char* dst, uint32_t src,
+                                          uint32_t blk_off, int lane) {
+  if (lane < 32) __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)dst, 4, src, blk_off, 0, 0);
+}
+
+__device__ __forceinline__ int acc_row(int r, int hi) { return ((r >> 2) << 3) + (hi << 2) + (r & 3); }
+
+// ---------------------------------------------------------------- dK / dV
+
+template <typename T, int D, bool CAUSAL>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(1, 1))) void
+attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
+                         const T* __restrict__ V, const T* __restrict__ dO, T* __restrict__ dK,
+                         T* __restrict__ dV, const float* __restrict__ lse,
+                         const float* __restrict__ delta, BwdShape s) {
+  using G = BwdGeo<D>;
+  constexpr int BB = G::BB, KS = G::KS, DT = G::DT, RB = G::RB, TILE = G::TILE;
+  constexpr int STAT = 2 * BB * 4;             // lse[64] then delta[64]
+  constexpr int STB = 2 * TILE + STAT;          // stage: Q, dO, statistics
+  constexpr int NDMA = 2 * G::DMA_PER_TILE + 1; // per wave per block
+  __shared__ __attribute__((aligned(1024))) char lds[G::STAGES * STB];
+
+  int w = blockIdx.x;
+  if (s.tiles % 8 == 0) w = (w % 8) * (s.tiles / 8) + w / 8;
+  const int bh = w / s.blocks_per_head;
+  const int kblk = w % s.blocks_per_head;
+  const int b = bh / s.heads, h = bh % s.heads;
+  const int64_t base = b * s.st[0] + h * s.st[1];
+  const int N = s.seq;
+  const int64_t sn = s.st[2];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int kb0 = kblk * G::BW;
+  const int wk0 = kb0 + wave * G::LW;
+  const int key = wk0 + l32;  // this lane's key (column of S and dP)
+
+  // K and V fragments of this wave's keys (B operands of S = Q K^T and dP = dO V^T).
+  i32x4 kf[KS], vf[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    const int64_t off = base + int64_t(key) * sn + kk * 16 + hi * 8;
+    kf[kk] = key < N ? *reinterpret_cast<const i32x4*>(K + off) : i32x4{0, 0, 0, 0};
+    vf[kk] = key < N ? *reinterpret_cast<const i32x4*>(V + off) : i32x4{0, 0, 0, 0};
+  }
+
+  const __amdgpu_buffer_rsrc_t rq =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(Q + base), (short)0, s.head_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rdo =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(dO + base), (short)0, s.head_bytes, 0x00020000);
+  const float* stat_src = (wave < 2 ? lse : delta) + int64_t(bh) * N;
+  const __amdgpu_buffer_rsrc_t rst =
+      __builtin_amdgcn_make_buffer_rsrc((void*)stat_src, (short)0, uint32_t(N) * 4u, 0x00020000);
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
+
+  uint32_t q_src[G::DMA_PER_TILE];
+#pragma unroll
+  for (int x = 0; x < G::DMA_PER_TILE; ++x) q_src[x] = tile_src<D, true>(wave, x, lane, sn);
+  const uint32_t st_src = uint32_t((wave & 1) * 32 + l32) * 4u;
+  const uint32_t blk_bytes = uint32_t(BB * sn) * 2u;
+
+  const int first = CAUSAL ? kb0 / BB : 0;  // first query block with a query >= kb0
+  const int nblk = (N + BB - 1) / BB - first;
+
+  // DMA of relative block J into stage ST (clamped: past-the-end blocks reload the last).
+#define TK_BWD_DKDV_DMA(J, ST)                                                              \
+  {                                                                                         \
+    const int qb_ = first + min((J), nblk - 1);                                             \
+    dma_tiles<D>(rq, rdo, lds + (ST) * STB, q_src, q_src, qb_ * blk_bytes, wave);           \
+    dma_stats(rst, lds + (ST) * STB + 2 * TILE + wave * 128, st_src, qb_ * BB * 4, lane);   \
+  }
+
+  f32x16 acc_dv[DT], acc_dk[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_dv[dt][r] = acc_dk[dt][r] = 0.f;
+
+  uint32_t qa[KS], ta0[DT], ta8[DT];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) qa[kk] = frag_addr<D, true>(lane, kk);
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    ta0[dt] = tr_addr<D>(lane, dt, 0);
+    ta8[dt] = tr_addr<D>(lane, dt, 8);
+  }
+  const uint32_t sa = (hi * 4) * 4;  // statistics: query offset 4 hi within each group of 8
+  const float sl2 = s.scale_log2;
+
+  TK_BWD_DKDV_DMA(0, 0)
+  TK_BWD_DKDV_DMA(1, 1)
+  int stage = 0, fill = 2;
+  // Causal: this wave's blocks start at the first one holding a query >= its first key.
+  const int wave_first = CAUSAL ? min(nblk, (wk0 / BB) - first) : 0;
+  int j = 0;
+  for (; j < wave_first; ++j) {
+    wait_vmcnt<NDMA>();
+    barrier_no_fence();
+    TK_BWD_DKDV_DMA(j + 2, fill)
+    stage = stage + 1 == G::STAGES ? 0 : stage + 1;
+    fill = fill + 1 == G::STAGES ? 0 : fill + 1;
+  }
+  for (; j < nblk; ++j) {
+    wait_vmcnt<NDMA>();
+    barrier_no_fence();
+    TK_BWD_DKDV_DMA(j + 2, fill)
+    const int q0 = (first + j) * BB;
+    const uint32_t qbase = lds_base + stage * STB;
+    const uint32_t dobase = qbase + TILE;
+    const uint32_t sbase = qbase + 2 * TILE;
+
+    // S = Q K^T, dP = dO V^T: 2 query tiles of 32.
+    f32x16 sc[2], dp[2];
+    {
+      i32x4 fq[2][KS];
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        fq[0][kk] = read_row<RB>(0, qbase + qa[kk]);
+        fq[1][kk] = read_row<RB>(1, qbase + qa[kk]);
+      }
+      wait_lgkm_n<0>();
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        pin(fq[0][kk]);
+        pin(fq[1][kk]);
+      }
+      const f32x16 z = {};
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        sc[0] = Mma<T>::run(fq[0][kk], kf[kk], kk == 0 ? z : sc[0]);
+        sc[1] = Mma<T>::run(fq[1][kk], kf[kk], kk == 0 ? z : sc[1]);
+      }
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        fq[0][kk] = read_row<RB>(0, dobase + qa[kk]);
+        fq[1][kk] = read_row<RB>(1, dobase + qa[kk]);
+      }
+      wait_lgkm_n<0>();
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        pin(fq[0][kk]);
+        pin(fq[1][kk]);
+      }
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        dp[0] = Mma<T>::run(fq[0][kk], vf[kk], kk == 0 ? z : dp[0]);
+        dp[1] = Mma<T>::run(fq[1][kk], vf[kk], kk == 0 ? z : dp[1]);
+      }
+    }
+
+    // P = exp2(S c - lse), dS = P (dP - delta). Register r of query tile mt holds query
+    // q0 + 32 mt + 8 (r / 4) + 4 hi + r % 4; its statistics are 4 consecutive floats.
+    i32x4 lst[2][4], dst[2][4];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        // group g of tile mt starts at query offset 32 mt + 8 g
+        switch (mt * 4 + g) {
+          case 0: lst[0][0] = lds_read_b128<0 * 32>(sbase + sa); dst[0][0] = lds_read_b128<256 + 0 * 32>(sbase + sa); break;
+          case 1: lst[0][1] = lds_read_b128<1 * 32>(sbase + sa); dst[0][1] = lds_read_b128<256 + 1 * 32>(sbase + sa); break;
+          case 2: lst[0][2] = lds_read_b128<2 * 32>(sbase + sa); dst[0][2] = lds_read_b128<256 + 2 * 32>(sbase + sa); break;
+          case 3: lst[0][3] = lds_read_b128<3 * 32>(sbase + sa); dst[0][3] = lds_read_b128<256 + 3 * 32>(sbase + sa); break;
+          case 4: lst[1][0] = lds_read_b128<4 * 32>(sbase + sa); dst[1][0] = lds_read_b128<256 + 4 * 32>(sbase + sa); break;
+          case 5: lst[1][1] = lds_read_b128<5 * 32>(sbase + sa); dst[1][1] = lds_read_b128<256 + 5 * 32>(sbase + sa); break;
+          case 6: lst[1][2] = lds_read_b128<6 * 32>(sbase + sa); dst[1][2] = lds_read_b128<256 + 6 * 32>(sbase + sa); break;
+          default: lst[1][3] = lds_read_b128<7 * 32>(sbase + sa); dst[1][3] = lds_read_b128<256 + 7 * 32>(sbase + sa); break;
+        }
+      }
+    wait_lgkm_n<0>();
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        pin(lst[mt][g]);
+        pin(dst[mt][g]);
+      }
+    const bool need_mask = CAUSAL && q0 < wk0 + G::LW - 1;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float l = __int_as_float(lst[mt][r >> 2][r & 3]);
+        const float dl = __int_as_float(dst[mt][r >> 2][r & 3]);
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[mt][r], sl2, -l));
+        if (need_mask && key > q0 + mt * 32 + acc_row(r, hi)) p = 0.f;
+        sc[mt][r] = p;
+        dp[mt][r] = p * (dp[mt][r] - dl);
+      }
+    const i32x4 pf[4] = {acc_frag<T>(sc[0], 0), acc_frag<T>(sc[0], 1), acc_frag<T>(sc[1], 0),
+                         acc_frag<T>(sc[1], 1)};
+    const i32x4 df[4] = {acc_frag<T>(dp[0], 0), acc_frag<T>(dp[0], 1), acc_frag<T>(dp[1], 0),
+                         acc_frag<T>(dp[1], 1)};
+
+    // dV^T += dO^T P and dK^T += Q^T dS over 4 steps of 16 queries.
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      i32x4 to[2][DT], tq[2][DT];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          to[i][dt] = read_tr_step<RB>(2 * half + i, dobase + ta0[dt], dobase + ta8[dt]);
+          tq[i][dt] = read_tr_step<RB>(2 * half + i, qbase + ta0[dt], qbase + ta8[dt]);
+        }
+      wait_lgkm_n<0>();
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          pin(to[i][dt]);
+          pin(tq[i][dt]);
+        }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          acc_dv[dt] = Mma<T>::run(to[i][dt], pf[2 * half + i], acc_dv[dt]);
+          acc_dk[dt] = Mma<T>::run(tq[i][dt], df[2 * half + i], acc_dk[dt]);
+        }
+    }
+    stage = stage + 1 == G::STAGES ? 0 : stage + 1;
+    fill = fill + 1 == G::STAGES ? 0 : fill + 1;
+  }
+#undef TK_BWD_DKDV_DMA
+  wait_vmcnt<0>();
+
+  // dK = scale (dK^T)^T, dV = (dV^T)^T: register r of tile dt is feature
+  // 32 dt + 8 (r / 4) + 4 hi + r % 4 of this lane's key.
+  if (key < N) {
+    T* dkr = dK + base + int64_t(key) * sn;
+    T* dvr = dV + base + int64_t(key) * sn;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = dt * 32 + g4 * 8 + hi * 4;
+        uint2 u;
+        u.x = pack2<T>(acc_dk[dt][g4 * 4 + 0] * s.scale, acc_dk[dt][g4 * 4 + 1] * s.scale);
+        u.y = pack2<T>(acc_dk[dt][g4 * 4 + 2] * s.scale, acc_dk[dt][g4 * 4 + 3] * s.scale);
+        *reinterpret_cast<uint2*>(dkr + d) = u;
+        u.x = pack2<T>(acc_dv[dt][g4 * 4 + 0], acc_dv[dt][g4 * 4 + 1]);
+        u.y = pack2<T>(acc_dv[dt][g4 * 4 + 2], acc_dv[dt][g4 * 4 + 3]);
+        *reinterpret_cast<uint2*>(dvr + d) = u;
+      }
+  }
+}
+
+// ---------------------------------------------------------------- dQ
+
+template <typename T, int D, bool CAUSAL>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(1, 1))) void
+attn_bwd_dq_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
+                       const T* __restrict__ V, const T* __restrict__ dO, T* __restrict__ dQ,
+                       const float* __restrict__ lse, const float* __restrict__ delta,
+                       BwdShape s) {
+  using G = BwdGeo<D>;
+  constexpr int BB = G::BB, KS = G::KS, DT = G::DT, RB = G::RB, TILE = G::TILE;
+  constexpr int STB = 2 * TILE;                // stage: K, V
+  constexpr int NDMA = 2 * G::DMA_PER_TILE;
+  __shared__ __attribute__((aligned(1024))) char lds[G::STAGES * STB];
+
+  int w = blockIdx.x;
+  if (s.tiles % 8 == 0) w = (w % 8) * (s.tiles / 8) + w / 8;
+  const int bh = w / s.blocks_per_head;
+  const int qblk = CAUSAL ? s.blocks_per_head - 1 - w % s.blocks_per_head : w % s.blocks_per_head;
+  const int b = bh / s.heads, h = bh % s.heads;
+  const int64_t base = b * s.st[0] + h * s.st[1];
+  const int N = s.seq;
+  const int64_t sn = s.st[2];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int q0 = qblk * G::BW;
+  const int wq0 = q0 + wave * G::LW;
+  const int query = wq0 + l32;
+
+  // Q and dO fragments of this wave's queries (B operands of S^T and dP^T).
+  i32x4 qf[KS], of[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    const int64_t off = base + int64_t(query) * sn + kk * 16 + hi * 8;
+    qf[kk] = query < N ? *reinterpret_cast<const i32x4*>(Q + off) : i32x4{0, 0, 0, 0};
+    of[kk] = query < N ? *reinterpret_cast<const i32x4*>(dO + off) : i32x4{0, 0, 0, 0};
+  }
+  const float lse_q = query < N ? lse[int64_t(bh) * N + query] : 0.f;
+  const float delta_q = query < N ? delta[int64_t(bh) * N + query] : 0.f;
+
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(K + base), (short)0, s.head_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(V + base), (short)0, s.head_bytes, 0x00020000);
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
+  uint32_t k_src[G::DMA_PER_TILE], v_src[G::DMA_PER_TILE];
+#pragma unroll
+  for (int x = 0; x < G::DMA_PER_TILE; ++x) {
+    k_src[x] = tile_src<D, true>(wave, x, lane, sn);
+    v_src[x] = tile_src<D, false>(wave, x, lane, sn);
+  }
+  const uint32_t blk_bytes = uint32_t(BB * sn) * 2u;
+  const int kv_end = CAUSAL ? min(N, q0 + G::BW) : N;
+  const int nblk = (kv_end + BB - 1) / BB;
+
+#define TK_BWD_DQ_DMA(J, ST) \
+  dma_tiles<D>(rk, rv, lds + (ST) * STB, k_src, v_src, min((J), nblk - 1) * blk_bytes, wave);
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
+
+  uint32_t ka[KS], va[KS], ta0[DT], ta8[DT];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    ka[kk] = frag_addr<D, true>(lane, kk);
+    va[kk] = frag_addr<D, false>(lane, kk);
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    ta0[dt] = tr_addr<D>(lane, dt, 0);
+    ta8[dt] = tr_addr<D>(lane, dt, 8);
+  }
+  const float sl2 = s.scale_log2;
+
+  TK_BWD_DQ_DMA(0, 0)
+  TK_BWD_DQ_DMA(1, 1)
+  int stage = 0, fill = 2;
+  const int wave_blocks = CAUSAL ? min(nblk, (wq0 + G::LW - 1) / BB + 1) : nblk;
+  int j = 0;
+  for (; j < wave_blocks; ++j) {
+    wait_vmcnt<NDMA>();
+    barrier_no_fence();
+    TK_BWD_DQ_DMA(j + 2, fill)
+    const int n0 = j * BB;
+    const uint32_t kbase = lds_base + stage * STB;
+    const uint32_t vbase = kbase + TILE;
+
+    // S^T = K Q^T and dP^T = V dO^T: 2 key tiles of 32.
+    f32x16 sc[2], dp[2];
+    {
+      i32x4 fk[2][KS];
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        fk[0][kk] = read_row<RB>(0, kbase + ka[kk]);
+        fk[1][kk] = read_row<RB>(1, kbase + ka[kk]);
+      }
+      wait_lgkm_n<0>();
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        pin(fk[0][kk]);
+        pin(fk[1][kk]);
+      }
+      const f32x16 z = {};
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        sc[0] = Mma<T>::run(fk[0][kk], qf[kk], kk == 0 ? z : sc[0]);
+        sc[1] = Mma<T>::run(fk[1][kk], qf[kk], kk == 0 ? z : sc[1]);
+      }
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        fk[0][kk] = read_row<RB>(0, vbase + va[kk]);
+        fk[1][kk] = read_row<RB>(1, vbase + va[kk]);
+      }
+      wait_lgkm_n<0>();
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        pin(fk[0][kk]);
+        pin(fk[1][kk]);
+      }
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        dp[0] = Mma<T>::run(fk[0][kk], of[kk], kk == 0 ? z : dp[0]);
+        dp[1] = Mma<T>::run(fk[1][kk], of[kk], kk == 0 ? z : dp[1]);
+      }
+    }
+
+    // P^T = exp2(S^T c - lse), dS^T = P^T (dP^T - delta); register r of key tile nt
+    // holds key n0 + 32 nt + 8 (r / 4) + 4 hi + r % 4.
+    const bool need_mask = n0 + BB > N || (CAUSAL && n0 + BB - 1 > wq0);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[nt][r], sl2, -lse_q));
+        if (need_mask) {
+          const int k = n0 + nt * 32 + acc_row(r, hi);
+          if (k >= N || (CAUSAL && k > query)) p = 0.f;
+        }
+        dp[nt][r] = p * (dp[nt][r] - delta_q);
+      }
+    const i32x4 df[4] = {acc_frag<T>(dp[0], 0), acc_frag<T>(dp[0], 1), acc_frag<T>(dp[1], 0),
+                         acc_frag<T>(dp[1], 1)};
+
+    // dQ^T += K^T dS^T over 4 steps of 16 keys.
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      i32x4 tk[2][DT];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          tk[i][dt] = read_tr_step<RB>(2 * half + i, kbase + ta0[dt], kbase + ta8[dt]);
+      wait_lgkm_n<0>();
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) pin(tk[i][dt]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = Mma<T>::run(tk[i][dt], df[2 * half + i], acc[dt]);
+    }
+    stage = stage + 1 == G::STAGES ? 0 : stage + 1;
+    fill = fill + 1 == G::STAGES ? 0 : fill + 1;
+  }
+  for (; j < nblk; ++j) {
+    wait_vmcnt<NDMA>();
+    barrier_no_fence();
+    TK_BWD_DQ_DMA(j + 2, fill)
+    fill = fill + 1 == G::STAGES ? 0 : fill + 1;
+  }
+#undef TK_BWD_DQ_DMA
+  wait_vmcnt<0>();
+
+  if (query < N) {
+    T* row = dQ + base + int64_t(query) * sn;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = dt * 32 + g4 * 8 + hi * 4;
+        uint2 u;
+        u.x = pack2<T>(acc[dt][g4 * 4 + 0] * s.scale, acc[dt][g4 * 4 + 1] * s.scale);
+        u.y = pack2<T>(acc[dt][g4 * 4 + 2] * s.scale, acc[dt][g4 * 4 + 3] * s.scale);
+        *reinterpret_cast<uint2*>(row + d) = u;
+      }
+  }
+}
+
+BwdShape make_shape(int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                    const int64_t* strides, float sm_scale) {
+  BwdShape s{};
+  s.heads = (int)heads;
+  s.seq = (int)seq;
+  for (int i = 0; i < 3; ++i) s.st[i] = strides[i];
+  s.scale = sm_scale;
+  s.scale_log2 = sm_scale * 1.4426950408889634f;
+  s.blocks_per_head = (int)tk::cdiv(seq, 128);
+  s.tiles = (int)(s.blocks_per_head * batch * heads);
+  s.head_bytes = (uint32_t)(((seq - 1) * strides[2] + head_dim) * 2);
+  return s;
+}
+
+#define TK_BWD_LAUNCH(KERNEL, ...)                                                          \
+  do {                                                                                      \
+    const dim3 grid(static_cast<unsigned>(s.tiles));                                       \
+    if (dtype == TK_DTYPE_F16) {                                                            \
+      using T = _Float16;                                                                   \
+      if (head_dim == 64) {                                                                 \
+        if (causal) hipLaunchKernelGGL((KERNEL<T, 64, true>), grid, dim3(kThreads), 0, stream, __VA_ARGS__); \
+        else hipLaunchKernelGGL((KERNEL<T, 64, false>), grid, dim3(kThreads), 0, stream, __VA_ARGS__);      \
+      } else {                                                                              \
+        if (causal) hipLaunchKernelGGL((KERNEL<T, 128, true>), grid, dim3(kThreads), 0, stream, __VA_ARGS__); \
+        else hipLaunchKernelGGL((KERNEL<T, 128, false>), grid, dim3(kThreads), 0, stream, __VA_ARGS__);      \
+      }                                                                                     \
+    } else {                                                                                \
+      using T = __bf16;                                                                     \
+      if (head_dim == 64) {                                                                 \
+        if (causal) hipLaunchKernelGGL((KERNEL<T, 64, true>), grid, dim3(kThreads), 0, stream, __VA_ARGS__); \
+        else hipLaunchKernelGGL((KERNEL<T, 64, false>), grid, dim3(kThreads), 0, stream, __VA_ARGS__);      \
+      } else {                                                                              \
+        if (causal) hipLaunchKernelGGL((KERNEL<T, 128, true>), grid, dim3(kThreads), 0, stream, __VA_ARGS__); \
+        else hipLaunchKernelGGL((KERNEL<T, 128, false>), grid, dim3(kThreads), 0, stream, __VA_ARGS__);      \
+      }                                                                                     \
+    }                                                                                       \
+  } while (0)
+
+}  // namespace
+
+namespace tk {
+
+bool attn_bwd_dma_applies(int64_t seq, int64_t head_dim, const int64_t* strides) {
+  return ((seq - 1) * strides[2] + head_dim) * 2 < (int64_t(1) << 31);
+}
+
+void attn_bwd_dkdv_dma_launch(int dtype, const void* q, const void* k, const void* v,
+                              const void* dout, void* dk, void* dv, const float* lse,
+                              const float* delta, int64_t batch, int64_t heads, int64_t seq,
+                              int64_t head_dim, const int64_t* strides, float sm_scale,
+                              bool causal, hipStream_t stream) {
+  const BwdShape s = make_shape(batch, heads, seq, head_dim, strides, sm_scale);
+  TK_BWD_LAUNCH(attn_bwd_dkdv_dma_kernel, (const T*)q, (const T*)k, (const T*)v,
+                (const T*)dout, (T*)dk, (T*)dv, lse, delta, s);
+}
+
+void attn_bwd_dq_dma_launch(int dtype, const void* q, const void* k, const void* v,
+                            const void* dout, void* dq, const float* lse, const float* delta,
+                            int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                            const int64_t* strides, float sm_scale, bool causal,
+                            hipStream_t stream) {
+  const BwdShape s = make_shape(batch, heads, seq, head_dim, strides, sm_scale);
+  TK_BWD_LAUNCH(attn_bwd_dq_dma_kernel, (const T*)q, (const T*)k, (const T*)v, (const T*)dout,
+                (T*)dq, lse, delta, s);
+}
+
+}  // namespace tk
