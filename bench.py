@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X tklab kernels; prints one JSON line.
 
-Step (the timed unit): BASELINE config 2 — residual RMSNorm forward + backward
+Step (the timed unit): benchmark config 2 — residual RMSNorm forward + backward
 on bfloat16 x, residual [16384, 4096] (weight ~ N(1, 0.02), eps 1e-6, both
 upstream gradients ~ N(0, 1)), i.e. three launches into preallocated buffers:
 tk_rmsnorm_fwd (with residual), tk_rmsnorm_bwd_stage1 (with the incoming sum
@@ -16,7 +16,7 @@ on the launch stream inside the timed region. ``traffic`` comes from the
 committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when present.
 ``cpu_baseline`` times the CPU oracle (oracle/tklab_oracle.c) on a bounded
 row sample of the same workload on the host cores.
-``kernels`` times every other BASELINE configuration (softmax, SwiGLU, RoPE,
+``kernels`` times every other benchmark configuration (softmax, SwiGLU, RoPE,
 GEMM, attention) per kernel. Memory-bound rows run back-to-back launches that
 rotate over enough copies of their tensors to touch at least 1 GiB (four times
 the 256 MiB last-level cache), so they measure steady HBM streaming without
@@ -180,7 +180,7 @@ def cpu_baseline(seconds: float) -> dict:
 
 
 def kernel_table(torch, device) -> list[dict]:
-    """Per-kernel timings of every BASELINE configuration (flushed, event-timed)."""
+    """Per-kernel timings of every benchmark configuration (see the module docstring)."""
     from tklab.kernels import flash_attention as fa
     from tklab.kernels import fused_softmax as sm
     from tklab.kernels import matmul as mm
@@ -366,7 +366,7 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded torch.randn on device)",
         "config": {
-            "workload": "residual_rms_norm forward+backward (BASELINE config 2)",
+            "workload": "residual_rms_norm forward+backward (benchmark config 2)",
             "rows": ROWS,
             "cols": COLS,
             "eps": EPS,

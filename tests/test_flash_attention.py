@@ -5,7 +5,7 @@ agreement within relative Frobenius 2e-2 for (1, 16, N, 64) float16 at
 N = 128 and 1000, seeds 23 + N + causal; the saved statistic equals
 logsumexp(scores) * log2(e) within 1e-3, seeds 91 + causal. References are
 evaluated on float32 upcasts. This build adds the CPU oracle across dtypes and
-head dims, and a per-head float32 check at the BASELINE shape.
+head dims, and a per-head float32 check at the benchmark shape.
 """
 
 from __future__ import annotations
@@ -109,7 +109,7 @@ def test_single_key_and_constant_keys_closed_forms() -> None:
     ("causal", "n", "d"), [(True, 8192, 128), (False, 4096, 128), (True, 8192, 64), (False, 4096, 64)]
 )
 def test_config_shapes_per_head(causal, n, d) -> None:
-    """BASELINE config 5 shapes (B4 H32 bf16); one head checked against float32 torch math."""
+    """benchmark config 5 shapes (B4 H32 bf16); one head checked against float32 torch math."""
     torch.manual_seed(0)
     shape = (4, 32, n, d)
     q, k, v = (torch.randn(shape, device="cuda", dtype=torch.bfloat16) for _ in range(3))

@@ -5,7 +5,7 @@ gradients vs SDPA autograd within relative Frobenius 3e-2 for (1, 16, N, 64)
 float16 at N = 128 and 1000 (seeds 41 + N + causal), and vs the float32
 gradient algebra within 1e-3 at N = 128 (seeds 79 + causal). References run
 on float32 upcasts. This build adds the CPU oracle and a per-head float32
-check at a BASELINE-sized head.
+check at a benchmark-sized head.
 """
 
 from __future__ import annotations
@@ -108,7 +108,7 @@ def test_backward_is_bitwise_reproducible() -> None:
 
 @pytest.mark.parametrize("causal", [True, False])
 def test_config_sized_head_matches_float32_algebra(causal) -> None:
-    """BASELINE config 5 per-head size (N 8192 causal / 4096 non-causal, D 128, bf16), 2 heads."""
+    """benchmark config 5 per-head size (N 8192 causal / 4096 non-causal, D 128, bf16), 2 heads."""
     torch.manual_seed(0)
     n = 8192 if causal else 4096
     q, k, v, do = _leaves((1, 2, n, 128), dtype=torch.bfloat16)

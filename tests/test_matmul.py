@@ -3,7 +3,7 @@
 Reference checks: relative Frobenius < 1e-2 against torch.matmul on float32
 upcasts (reference matmul.py:282-284) on square, tail and strided problems.
 This build adds the CPU oracle (double accumulation) on sampled rows at the
-BASELINE shapes and elementwise agreement at the storage dtype's tolerance.
+benchmark shapes and elementwise agreement at the storage dtype's tolerance.
 """
 
 from __future__ import annotations
@@ -74,7 +74,7 @@ def test_transposed_views_take_the_general_path() -> None:
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize(("m", "n", "k"), [(4096, 4096, 4096), (8191, 8192, 8192), (8192, 8192, 8192)])
 def test_config_shapes(dtype: torch.dtype, m: int, n: int, k: int) -> None:
-    """8192^3 (and 4096^3, ragged M=8191), N(0, 1/sqrt(K)) inputs."""
+    """benchmark config 4: 8192^3 (and 4096^3, ragged M=8191), N(0, 1/sqrt(K)) inputs."""
     torch.manual_seed(0)
     a, b = _inputs(m, n, k, dtype)
     c = matmul_fp32acc(a, b)

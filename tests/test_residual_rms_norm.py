@@ -113,7 +113,7 @@ def test_single_group_adds_incoming_gradient() -> None:
 
 
 def test_config_shape_bf16_16384x4096_matches_the_oracle() -> None:
-    """x, residual ~N(0,1), weight ~N(1, 0.02), eps 1e-6, both grads."""
+    """benchmark config 2: x, residual ~N(0,1), weight ~N(1, 0.02), eps 1e-6, both grads."""
     torch.manual_seed(0)
     rows, cols = 16384, 4096
     x = torch.randn(rows, cols, device="cuda", dtype=torch.bfloat16, requires_grad=True)

@@ -94,7 +94,7 @@ def test_bitwise_against_the_oracle(dtype: torch.dtype, cols: int) -> None:
 
 
 def test_config_shape_bf16_q_4x32x4096x128() -> None:
-    """BASELINE config 3 RoPE: q [4,32,4096,128] bf16 as [524288, 128], base 1e4, positions 0..4095."""
+    """benchmark config 3 RoPE: q [4,32,4096,128] bf16 as [524288, 128], base 1e4, positions 0..4095."""
     torch.manual_seed(0)
     b, h, s, d = 4, 32, 4096, 128
     q = torch.randn(b, h, s, d, device="cuda", dtype=torch.bfloat16)

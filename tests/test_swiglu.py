@@ -81,7 +81,7 @@ def test_matches_the_oracle(dtype: torch.dtype, cols: int) -> None:
 
 
 def test_config_shape_bf16_16384x14336() -> None:
-    """BASELINE config 3 SwiGLU: gate, up ~N(0,1) [16384, 14336] bf16; every 97th row checked."""
+    """benchmark config 3 SwiGLU: gate, up ~N(0,1) [16384, 14336] bf16; every 97th row checked."""
     torch.manual_seed(0)
     gate = torch.randn(16384, 14336, device="cuda", dtype=torch.bfloat16)
     up = torch.randn(16384, 14336, device="cuda", dtype=torch.bfloat16)
