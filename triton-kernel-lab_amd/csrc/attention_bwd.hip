@@ -100,28 +100,30 @@ __device__ __forceinline__ uint32_t tr_addr(int lane, int dt, int half8) {
   return row * G::RB + ((chunk ^ G::dual_swz(row)) * 16) + (q & 1) * 8;
 }
 
-// Transposed fragment of the 16 rows starting at ROW0 (a multiple of 16).
-template <int ROW0, int RB>
+// Transposed fragment of the 16 rows starting at ROW0 (a multiple of 16) of the tile
+// OFF bytes past the lane addresses.
+template <int ROW0, int RB, int OFF>
 __device__ __forceinline__ i32x4 read_tr(uint32_t addr0, uint32_t addr8) {
-  const i32x2 a = lds_read_tr16<ROW0 * RB>(addr0);
-  const i32x2 b = lds_read_tr16<ROW0 * RB>(addr8);
+  const i32x2 a = lds_read_tr16<OFF + ROW0 * RB>(addr0);
+  const i32x2 b = lds_read_tr16<OFF + ROW0 * RB>(addr8);
   return i32x4{a[0], a[1], b[0], b[1]};
 }
 
-template <int RB>
+template <int RB, int OFF = 0>
 __device__ __forceinline__ i32x4 read_tr_step(int step, uint32_t addr0, uint32_t addr8) {
   switch (step) {
-    case 0: return read_tr<0, RB>(addr0, addr8);
-    case 1: return read_tr<16, RB>(addr0, addr8);
-    case 2: return read_tr<32, RB>(addr0, addr8);
-    default: return read_tr<48, RB>(addr0, addr8);
+    case 0: return read_tr<0, RB, OFF>(addr0, addr8);
+    case 1: return read_tr<16, RB, OFF>(addr0, addr8);
+    case 2: return read_tr<32, RB, OFF>(addr0, addr8);
+    default: return read_tr<48, RB, OFF>(addr0, addr8);
   }
 }
 
-// Row fragment (ds_read_b128) of row tile `mt` (32 rows = 32 * RB bytes).
-template <int RB>
+// Row fragment (ds_read_b128) of row tile `mt` (32 rows = 32 * RB bytes) of the tile
+// OFF bytes past the lane address.
+template <int RB, int OFF = 0>
 __device__ __forceinline__ i32x4 read_row(int mt, uint32_t addr) {
-  return mt == 0 ? lds_read_b128<0>(addr) : lds_read_b128<32 * RB>(addr);
+  return mt == 0 ? lds_read_b128<OFF>(addr) : lds_read_b128<OFF + 32 * RB>(addr);
 }
 
 
@@ -149,6 +151,55 @@ __device__ __forceinline__ void dma_stats(__amdgpu_buffer_rsrc_t rs, char* dst, 
 }
 
 __device__ __forceinline__ int acc_row(int r, int hi) { return ((r >> 2) << 3) + (hi << 2) + (r & 3); }
+
+
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Row operands of one 32-query sub-block of the dK/dV pass: Q and dO fragments
+// (ds_read_b128, features 16 kk + 8 hi .. +7 of query lane % 32) and the lse / delta of
+// the 16 queries this lane's accumulator registers hold (4 groups of 4 consecutive).
+struct SubRows {
+  i32x4 q[8], o[8];
+  i32x4 lse[4], dlt[4];
+};
+
+template <int D>
+__device__ __forceinline__ void read_sub_rows(SubRows& r, int mt, const uint32_t* qa,
+                                              uint32_t sa) {
+  constexpr int KS = D / 16, RB = D * 2, TILE = 64 * RB;
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    r.q[kk] = read_row<RB>(mt, qa[kk]);
+    r.o[kk] = read_row<RB, TILE>(mt, qa[kk]);
+  }
+  // Statistics of query group g of tile mt start at float 32 mt + 8 g (+ 4 hi, in sa, which
+  // already points at the stage's statistics); delta follows lse after 64 floats.
+  if (mt == 0) {
+    r.lse[0] = lds_read_b128<0>(sa);   r.dlt[0] = lds_read_b128<256>(sa);
+    r.lse[1] = lds_read_b128<32>(sa);  r.dlt[1] = lds_read_b128<288>(sa);
+    r.lse[2] = lds_read_b128<64>(sa);  r.dlt[2] = lds_read_b128<320>(sa);
+    r.lse[3] = lds_read_b128<96>(sa);  r.dlt[3] = lds_read_b128<352>(sa);
+  } else {
+    r.lse[0] = lds_read_b128<128>(sa); r.dlt[0] = lds_read_b128<384>(sa);
+    r.lse[1] = lds_read_b128<160>(sa); r.dlt[1] = lds_read_b128<416>(sa);
+    r.lse[2] = lds_read_b128<192>(sa); r.dlt[2] = lds_read_b128<448>(sa);
+    r.lse[3] = lds_read_b128<224>(sa); r.dlt[3] = lds_read_b128<480>(sa);
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void pin_sub_rows(SubRows& r) {
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk) {
+    pin(r.q[kk]);
+    pin(r.o[kk]);
+  }
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    pin(r.lse[g]);
+    pin(r.dlt[g]);
+  }
+}
 
 // ---------------------------------------------------------------- dK / dV
 
@@ -252,104 +303,64 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
     barrier_no_fence();
     TK_BWD_DKDV_DMA(j + 2, fill)
     const int q0 = (first + j) * BB;
-    const uint32_t qbase = lds_base + stage * STB;
-    const uint32_t dobase = qbase + TILE;
-    const uint32_t sbase = qbase + 2 * TILE;
-
-    // S = Q K^T, dP = dO V^T: 2 query tiles of 32.
-    f32x16 sc[2], dp[2];
-    {
-      i32x4 fq[2][KS];
+    // Lane addresses for this stage; the dO tile and the 16-row steps are immediates.
+    const uint32_t sbase = lds_base + stage * STB;
+    uint32_t qs_a[KS], t0[DT], t8[DT];
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        fq[0][kk] = read_row<RB>(0, qbase + qa[kk]);
-        fq[1][kk] = read_row<RB>(1, qbase + qa[kk]);
-      }
-      wait_lgkm_n<0>();
+    for (int kk = 0; kk < KS; ++kk) qs_a[kk] = sbase + qa[kk];
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        pin(fq[0][kk]);
-        pin(fq[1][kk]);
-      }
-      const f32x16 z = {};
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        sc[0] = Mma<T>::run(fq[0][kk], kf[kk], kk == 0 ? z : sc[0]);
-        sc[1] = Mma<T>::run(fq[1][kk], kf[kk], kk == 0 ? z : sc[1]);
-      }
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        fq[0][kk] = read_row<RB>(0, dobase + qa[kk]);
-        fq[1][kk] = read_row<RB>(1, dobase + qa[kk]);
-      }
-      wait_lgkm_n<0>();
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        pin(fq[0][kk]);
-        pin(fq[1][kk]);
-      }
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        dp[0] = Mma<T>::run(fq[0][kk], vf[kk], kk == 0 ? z : dp[0]);
-        dp[1] = Mma<T>::run(fq[1][kk], vf[kk], kk == 0 ? z : dp[1]);
-      }
+    for (int dt = 0; dt < DT; ++dt) {
+      t0[dt] = sbase + ta0[dt];
+      t8[dt] = sbase + ta8[dt];
     }
+    const uint32_t st_a = sbase + 2 * TILE + sa;
+    const bool need_mask = CAUSAL && q0 < wk0 + G::LW - 1;
 
-    // P = exp2(S c - lse), dS = P (dP - delta). Register r of query tile mt holds query
-    // q0 + 32 mt + 8 (r / 4) + 4 hi + r % 4; its statistics are 4 consecutive floats.
-    i32x4 lst[2][4], dst[2][4];
+    // Two sub-blocks of 32 queries (query tile mt); each sub-block's transposed reads are
+    // issued before its softmax arithmetic.
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt) {
+      SubRows rows;
+      read_sub_rows<D>(rows, mt, qs_a, st_a);
+      wait_lgkm_n<0>();
+      pin_sub_rows<D>(rows);
+      // S = Q K^T and dP = dO V^T for 32 queries x this wave's 32 keys.
+      f32x16 sc, dp;
+      {
+        const f32x16 z = {};
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        // group g of tile mt starts at query offset 32 mt + 8 g
-        switch (mt * 4 + g) {
-          case 0: lst[0][0] = lds_read_b128<0 * 32>(sbase + sa); dst[0][0] = lds_read_b128<256 + 0 * 32>(sbase + sa); break;
-          case 1: lst[0][1] = lds_read_b128<1 * 32>(sbase + sa); dst[0][1] = lds_read_b128<256 + 1 * 32>(sbase + sa); break;
-          case 2: lst[0][2] = lds_read_b128<2 * 32>(sbase + sa); dst[0][2] = lds_read_b128<256 + 2 * 32>(sbase + sa); break;
-          case 3: lst[0][3] = lds_read_b128<3 * 32>(sbase + sa); dst[0][3] = lds_read_b128<256 + 3 * 32>(sbase + sa); break;
-          case 4: lst[1][0] = lds_read_b128<4 * 32>(sbase + sa); dst[1][0] = lds_read_b128<256 + 4 * 32>(sbase + sa); break;
-          case 5: lst[1][1] = lds_read_b128<5 * 32>(sbase + sa); dst[1][1] = lds_read_b128<256 + 5 * 32>(sbase + sa); break;
-          case 6: lst[1][2] = lds_read_b128<6 * 32>(sbase + sa); dst[1][2] = lds_read_b128<256 + 6 * 32>(sbase + sa); break;
-          default: lst[1][3] = lds_read_b128<7 * 32>(sbase + sa); dst[1][3] = lds_read_b128<256 + 7 * 32>(sbase + sa); break;
+        for (int kk = 0; kk < KS; ++kk) {
+          sc = Mma<T>::run(rows.q[kk], kf[kk], kk == 0 ? z : sc);
+          dp = Mma<T>::run(rows.o[kk], vf[kk], kk == 0 ? z : dp);
         }
       }
-    wait_lgkm_n<0>();
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        pin(lst[mt][g]);
-        pin(dst[mt][g]);
-      }
-    const bool need_mask = CAUSAL && q0 < wk0 + G::LW - 1;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float l = __int_as_float(lst[mt][r >> 2][r & 3]);
-        const float dl = __int_as_float(dst[mt][r >> 2][r & 3]);
-        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[mt][r], sl2, -l));
-        if (need_mask && key > q0 + mt * 32 + acc_row(r, hi)) p = 0.f;
-        sc[mt][r] = p;
-        dp[mt][r] = p * (dp[mt][r] - dl);
-      }
-    const i32x4 pf[4] = {acc_frag<T>(sc[0], 0), acc_frag<T>(sc[0], 1), acc_frag<T>(sc[1], 0),
-                         acc_frag<T>(sc[1], 1)};
-    const i32x4 df[4] = {acc_frag<T>(dp[0], 0), acc_frag<T>(dp[0], 1), acc_frag<T>(dp[1], 0),
-                         acc_frag<T>(dp[1], 1)};
-
-    // dV^T += dO^T P and dK^T += Q^T dS over 4 steps of 16 queries.
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
       i32x4 to[2][DT], tq[2][DT];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          to[i][dt] = read_tr_step<RB>(2 * half + i, dobase + ta0[dt], dobase + ta8[dt]);
-          tq[i][dt] = read_tr_step<RB>(2 * half + i, qbase + ta0[dt], qbase + ta8[dt]);
+          to[i][dt] = read_tr_step<RB, TILE>(2 * mt + i, t0[dt], t8[dt]);
+          tq[i][dt] = read_tr_step<RB>(2 * mt + i, t0[dt], t8[dt]);
         }
+      // Causal: keys after a query get S = -inf (exp2 -> 0); only diagonal blocks.
+      if (__builtin_expect(need_mask, 0)) {
+        const int lim = q0 + mt * 32 + 4 * hi - key;  // key <= query  <=>  offset >= -lim
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (acc_row(r, 0) + lim < 0) sc[r] = kNegInf;
+      }
+      // P = exp2(S c - lse), dS = P (dP - delta); register r holds query
+      // q0 + 32 mt + 8 (r / 4) + 4 hi + r % 4.
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float l = __int_as_float(rows.lse[r >> 2][r & 3]);
+        const float dl = __int_as_float(rows.dlt[r >> 2][r & 3]);
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], sl2, -l));
+        sc[r] = pv;
+        dp[r] = pv * (dp[r] - dl);
+      }
+      const i32x4 pf[2] = {acc_frag<T>(sc, 0), acc_frag<T>(sc, 1)};
+      const i32x4 df[2] = {acc_frag<T>(dp, 0), acc_frag<T>(dp, 1)};
       wait_lgkm_n<0>();
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -358,12 +369,13 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
           pin(to[i][dt]);
           pin(tq[i][dt]);
         }
+      // dV^T += dO^T P and dK^T += Q^T dS.
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          acc_dv[dt] = Mma<T>::run(to[i][dt], pf[2 * half + i], acc_dv[dt]);
-          acc_dk[dt] = Mma<T>::run(tq[i][dt], df[2 * half + i], acc_dk[dt]);
+          acc_dv[dt] = Mma<T>::run(to[i][dt], pf[i], acc_dv[dt]);
+          acc_dk[dt] = Mma<T>::run(tq[i][dt], df[i], acc_dk[dt]);
         }
     }
     stage = stage + 1 == G::STAGES ? 0 : stage + 1;
@@ -482,8 +494,19 @@ attn_bwd_dq_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
     barrier_no_fence();
     TK_BWD_DQ_DMA(j + 2, fill)
     const int n0 = j * BB;
+    // Lane addresses for this stage; the V tile and the 16-row steps are immediates.
     const uint32_t kbase = lds_base + stage * STB;
-    const uint32_t vbase = kbase + TILE;
+    uint32_t k_a[KS], v_a[KS], t0[DT], t8[DT];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      k_a[kk] = kbase + ka[kk];
+      v_a[kk] = kbase + va[kk];
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      t0[dt] = kbase + ta0[dt];
+      t8[dt] = kbase + ta8[dt];
+    }
 
     // S^T = K Q^T and dP^T = V dO^T: 2 key tiles of 32.
     f32x16 sc[2], dp[2];
@@ -491,8 +514,8 @@ attn_bwd_dq_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
       i32x4 fk[2][KS];
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
-        fk[0][kk] = read_row<RB>(0, kbase + ka[kk]);
-        fk[1][kk] = read_row<RB>(1, kbase + ka[kk]);
+        fk[0][kk] = read_row<RB>(0, k_a[kk]);
+        fk[1][kk] = read_row<RB>(1, k_a[kk]);
       }
       wait_lgkm_n<0>();
 #pragma unroll
@@ -508,8 +531,8 @@ attn_bwd_dq_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
       }
 #pragma unroll
       for (int kk = 0; kk < KS; ++kk) {
-        fk[0][kk] = read_row<RB>(0, vbase + va[kk]);
-        fk[1][kk] = read_row<RB>(1, vbase + va[kk]);
+        fk[0][kk] = read_row<RB, TILE>(0, v_a[kk]);
+        fk[1][kk] = read_row<RB, TILE>(1, v_a[kk]);
       }
       wait_lgkm_n<0>();
 #pragma unroll
@@ -524,19 +547,27 @@ attn_bwd_dq_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
       }
     }
 
-    // P^T = exp2(S^T c - lse), dS^T = P^T (dP^T - delta); register r of key tile nt
-    // holds key n0 + 32 nt + 8 (r / 4) + 4 hi + r % 4.
+    // Masked keys (past the sequence end, or after this lane's query) get S^T = -inf;
+    // only ragged and diagonal blocks. Register r of key tile nt holds key
+    // n0 + 32 nt + 8 (r / 4) + 4 hi + r % 4.
     const bool need_mask = n0 + BB > N || (CAUSAL && n0 + BB - 1 > wq0);
+    if (__builtin_expect(need_mask, 0)) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        int lim = N - 1 - (n0 + nt * 32 + 4 * hi);  // last valid offset from the lane's first key
+        if (CAUSAL) lim = min(lim, query - (n0 + nt * 32 + 4 * hi));
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (acc_row(r, 0) > lim) sc[nt][r] = kNegInf;
+      }
+    }
+    // P^T = exp2(S^T c - lse), dS^T = P^T (dP^T - delta).
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[nt][r], sl2, -lse_q));
-        if (need_mask) {
-          const int k = n0 + nt * 32 + acc_row(r, hi);
-          if (k >= N || (CAUSAL && k > query)) p = 0.f;
-        }
-        dp[nt][r] = p * (dp[nt][r] - delta_q);
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[nt][r], sl2, -lse_q));
+        dp[nt][r] = pv * (dp[nt][r] - delta_q);
       }
     const i32x4 df[4] = {acc_frag<T>(dp[0], 0), acc_frag<T>(dp[0], 1), acc_frag<T>(dp[1], 0),
                          acc_frag<T>(dp[1], 1)};
@@ -548,8 +579,7 @@ attn_bwd_dq_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-          tk[i][dt] = read_tr_step<RB>(2 * half + i, kbase + ta0[dt], kbase + ta8[dt]);
+        for (int dt = 0; dt < DT; ++dt) tk[i][dt] = read_tr_step<RB>(2 * half + i, t0[dt], t8[dt]);
       wait_lgkm_n<0>();
 #pragma unroll
       for (int i = 0; i < 2; ++i)
