@@ -2,9 +2,10 @@
 // float32 accumulation: the fast path behind tk_gemm (src/tklab/kernels/matmul.py:72-164
 // computes the same product with a Triton tile loop).
 //
-// Block tile 256 x 256, K step 32, 256 threads = 4 wave64s in a 2 x 2 grid; each wave
-// owns 128 x 128 of C as 4 x 4 tiles of v_mfma_f32_32x32x16 (256 AGPR accumulators,
-// one wave per SIMD).
+// Block tile 256 x 256, K step 32, 512 threads = 8 wave64s in a 2 (M) x 4 (N) grid, two
+// waves per SIMD; each wave owns 128 x 64 of C as 4 x 2 tiles of v_mfma_f32_32x32x16
+// (128 accumulators). With two waves per SIMD, one wave's LDS reads, DMA issue and
+// barrier waits are covered by the other wave's MFMAs.
 //
 // Operands reach LDS by buffer->LDS DMA (buffer_load_dwordx4 ... lds): no VGPR staging.
 // LDS is a ring of kStages stages of 32 KiB (A tile then B tile); K tile t+kAhead is
@@ -25,7 +26,7 @@
 // The compiler inserts vmcnt(0) before any LDS read that may alias an LDS DMA, which
 // would drain the prefetch ring every step; fragment reads are therefore inline asm
 // ordered by explicit s_waitcnt, with the MFMA/LDS/DMA interleave pinned by
-// sched_barrier so the matrix pipe never waits for address or issue work.
+// sched_barrier.
 //
 // Tile order: workgroup w runs on XCD w % 8; tiles are renumbered so each XCD walks a
 // contiguous range in groups of 4 M-tiles, sharing A and B panels in that XCD's L2.
@@ -35,7 +36,7 @@
 namespace {
 
 constexpr int BM = 256, BN = 256, BK = 32;
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;  // 8 waves
 constexpr int kStages = 5;
 constexpr int kAhead = kStages - 2;
 constexpr int kGroupM = 4;
@@ -124,7 +125,7 @@ __device__ __forceinline__ i32x4 read_b(uint32_t addr) {
 }
 
 struct Frags {
-  i32x4 a[4], b[4];
+  i32x4 a[4], b[2];
 };
 
 // Waits for this wave's LDS reads; the fragments are in/out operands so no use of them
@@ -132,12 +133,12 @@ struct Frags {
 __device__ __forceinline__ void wait_lgkm(Frags& f) {
   asm volatile("s_waitcnt lgkmcnt(0)"
                : "+v"(f.a[0]), "+v"(f.a[1]), "+v"(f.a[2]), "+v"(f.a[3]), "+v"(f.b[0]),
-                 "+v"(f.b[1]), "+v"(f.b[2]), "+v"(f.b[3]));
+                 "+v"(f.b[1]));
 }
 
 template <typename T>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(1, 1))) void
+                          amdgpu_waves_per_eu(2, 2))) void
 gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restrict__ C,
                 Problem p) {
   __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
@@ -154,7 +155,7 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restrict_
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+  const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
   const int lrow = lane & 31;
   const int lhalf = lane >> 5;
   const __amdgpu_buffer_rsrc_t ra =
@@ -163,73 +164,73 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restrict_
       __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, p.b_bytes, 0x00020000);
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
 
-  // DMA sources for K tile 0 (bytes). Wave w fills A rows 64w .. 64w+63 (4 loads of 16
-  // rows) and B k-rows 8w .. 8w+7 (4 loads of 2 k-rows). Rows past M and columns past N
+  // DMA sources for K tile 0 (bytes). Wave w fills A rows 32w .. 32w+31 (2 loads of 16
+  // rows) and B k-rows 4w .. 4w+3 (2 loads of 2 k-rows). Rows past M and columns past N
   // read as zero; K is a multiple of BK on this path.
-  uint32_t a_src[4], b_src[4];
+  uint32_t a_src[2], b_src[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = (wave * 4 + i) * 16 + (lane >> 2);
+  for (int i = 0; i < 2; ++i) {
+    const int r = (wave * 2 + i) * 16 + (lane >> 2);
     const int c = (lane & 3) ^ ((r >> 2) & 3);
     a_src[i] = (m0 + r < p.m) ? uint32_t((m0 + r) * p.lda + c * 8) * 2u : kOob;
-    const int kr = (wave * 4 + i) * 2 + (lane >> 5);
-    const int slot = lane & 31;  // 16-byte slot in the 512-byte k-row
+    const int kr = (wave * 2 + i) * 2 + (lane >> 5);
+    const int slot = lane & 31;
     const int chunk = (((slot >> 1) ^ (2 * (kr & 3))) << 1) | (slot & 1);
     b_src[i] = (n0 + chunk * 8 < p.n) ? uint32_t(kr * p.ldb + n0 + chunk * 8) * 2u : kOob;
   }
   const uint32_t b_tile_bytes = uint32_t(BK * p.ldb) * 2u;
   const int kt = p.k / BK;
 
-  // DMA x (0..7) of K tile `tile` into ring slot `slot`. Tiles past the end reload the
+  // DMA x (0..3: two A loads, two B loads) of K tile `tile` into ring slot `slot`. Tiles past the end reload the
   // last tile into a slot that is never read again, so every step issues the same number
   // of loads and the vmcnt arithmetic stays constant.
   auto dma = [&](int x, int tile, int slot) {
     tile = min(tile, kt - 1);
     char* stage = lds + slot * kStageBytes;
-    if (x < 4)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(stage + (wave * 4 + x) * 1024), 16,
+    if (x < 2)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(stage + (wave * 2 + x) * 1024), 16,
                                                a_src[x], tile * (BK * 2), 0, 0);
     else
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rb, (lds_void*)(stage + kOperandBytes + (wave * 4 + x - 4) * 1024), 16, b_src[x - 4],
+          rb, (lds_void*)(stage + kOperandBytes + (wave * 2 + x - 2) * 1024), 16, b_src[x - 2],
           tile * b_tile_bytes, 0, 0);
   };
 
   // Lane read addresses inside a stage: A row wm + lrow, chunk (2*kk + lhalf) swizzled;
   // B k-row 8*(g>>1) + jj (+16*kk, +4), columns wn + 32j + 16*(g&1) + 4q.
-  uint32_t a_addr[2], b_addr[4];
+  uint32_t a_addr[2], b_addr[2];
   {
     const int sa = (lrow >> 2) & 3;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) a_addr[kk] = (wm + lrow) * 64 + (((kk * 2 + lhalf) ^ sa) * 16);
     const int g = lane >> 4, jj = (lane & 15) >> 2, q = lane & 3;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       const int n = wn + j * 32 + (g & 1) * 16 + 4 * q;
       b_addr[j] = (((g >> 1) * 8 + jj) * 256 + (((n >> 4) ^ (2 * jj)) * 16) + (n & 15)) * 2;
     }
   }
 
-  f32x16 acc[4][4];
+  f32x16 acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
 #pragma unroll
   for (int t = 0; t < kAhead; ++t)
 #pragma unroll
-    for (int x = 0; x < 8; ++x) dma(x, t, t);
-  wait_vmcnt<(kAhead - 1) * 8>();
+    for (int x = 0; x < 4; ++x) dma(x, t, t);
+  wait_vmcnt<(kAhead - 1) * 4>();
   barrier_no_fence();
 
   Frags f0, f1;
 #pragma unroll
   for (int i = 0; i < 4; ++i) f0.a[i] = read_a(i, lds_base + a_addr[0]);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) f0.b[j] = read_b<0>(lds_base + b_addr[j]);
+  for (int j = 0; j < 2; ++j) f0.b[j] = read_b<0>(lds_base + b_addr[j]);
 
   int stage = 0, fill = kAhead;
   for (int t = 0; t < kt; ++t) {
@@ -241,45 +242,36 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restrict_
     wait_lgkm(f0);
     sched_fence();
 #pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      acc[x >> 2][x & 3] = Mfma<T>::run(f0.a[x >> 2], f0.b[x & 3], acc[x >> 2][x & 3]);
+    for (int x = 0; x < 8; ++x) {
+      acc[x >> 1][x & 1] = Mfma<T>::run(f0.a[x >> 1], f0.b[x & 1], acc[x >> 1][x & 1]);
       sched_fence();
       if (x < 4) {
         f1.a[x] = read_a(x, base + a_addr[1]);
-      } else if (x < 8) {
-        switch (x - 4) {
-          case 0: f1.b[0] = read_b<1>(base + b_addr[0]); break;
-          case 1: f1.b[1] = read_b<1>(base + b_addr[1]); break;
-          case 2: f1.b[2] = read_b<1>(base + b_addr[2]); break;
-          default: f1.b[3] = read_b<1>(base + b_addr[3]); break;
-        }
-      } else {
-        dma(x - 8, t + kAhead, fill);
+      } else if (x < 6) {
+        if (x == 4) f1.b[0] = read_b<1>(base + b_addr[0]);
+        else f1.b[1] = read_b<1>(base + b_addr[1]);
       }
+      if (x >= 4) dma(x - 4, t + kAhead, fill);
       sched_fence();
     }
 
     // Tile t+1 has landed for this wave once only the later tiles' loads are pending;
     // the barrier makes every wave's share visible (and retires all reads of tile t-1).
-    wait_vmcnt<(kAhead - 1) * 8>();
+    wait_vmcnt<(kAhead - 1) * 4>();
     barrier_no_fence();
 
     // Second k half of tile t; meanwhile read the first half of tile t+1.
     wait_lgkm(f1);
     sched_fence();
 #pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      acc[x >> 2][x & 3] = Mfma<T>::run(f1.a[x >> 2], f1.b[x & 3], acc[x >> 2][x & 3]);
+    for (int x = 0; x < 8; ++x) {
+      acc[x >> 1][x & 1] = Mfma<T>::run(f1.a[x >> 1], f1.b[x & 1], acc[x >> 1][x & 1]);
       sched_fence();
       if (x < 4) {
         f0.a[x] = read_a(x, next_base + a_addr[0]);
-      } else if (x < 8) {
-        switch (x - 4) {
-          case 0: f0.b[0] = read_b<0>(next_base + b_addr[0]); break;
-          case 1: f0.b[1] = read_b<0>(next_base + b_addr[1]); break;
-          case 2: f0.b[2] = read_b<0>(next_base + b_addr[2]); break;
-          default: f0.b[3] = read_b<0>(next_base + b_addr[3]); break;
-        }
+      } else if (x < 6) {
+        if (x == 4) f0.b[0] = read_b<0>(next_base + b_addr[0]);
+        else f0.b[1] = read_b<0>(next_base + b_addr[1]);
       }
       sched_fence();
     }
@@ -293,7 +285,7 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restrict_
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       const int n = n0 + wn + j * 32 + lrow;
       if (n >= p.n) continue;
 #pragma unroll
