@@ -118,6 +118,27 @@ def test_forward_and_backward_match_the_oracle(dtype: torch.dtype, cols: int) ->
         assert_relative_frobenius(buffers.dw, dev(dw_ref, buffers.dw), max_relative_error=1e-5)
 
 
+@pytest.mark.parametrize("rows", [1, 300, 1030, 1537])
+@pytest.mark.parametrize("dtype,cols", [(torch.bfloat16, 4096), (torch.float32, 1000)])
+def test_stage1_ragged_and_empty_groups(rows: int, dtype: torch.dtype, cols: int) -> None:
+    """512 groups over row counts that leave a short last group and trailing
+    groups owning no rows (ceil(1030/512)=3 rows per group covers 344 groups);
+    the bf16 4096-column case takes the pipelined three-row loop."""
+    torch.manual_seed(rows)
+    x = torch.randn(rows, cols, device="cuda", dtype=dtype)
+    w = (1 + 0.02 * torch.randn(cols, device="cuda")).to(dtype)
+    dy = torch.randn(rows, cols, device="cuda", dtype=dtype)
+    rstd = torch.empty(rows, device="cuda")
+    _launch_forward(x, w, torch.empty_like(x), rstd, eps=1e-6, store_stats=True)
+    buffers = _make_backward_buffers(x, w, group_size=512)
+    _launch_backward_stage1(dy, x, w, rstd, buffers)
+    _launch_backward_stage2(buffers, cols)
+    torch.cuda.synchronize()
+    dx_ref, dw_ref = oracle.rmsnorm_bwd(host(dy), host(x), host(w), host(rstd), name(dtype))
+    assert_close(buffers.dx, dev(dx_ref, buffers.dx))
+    assert_relative_frobenius(buffers.dw, dev(dw_ref, buffers.dw), max_relative_error=1e-2)
+
+
 def test_backward_is_bitwise_reproducible_and_runs_in_deterministic_mode() -> None:
     torch.manual_seed(5)
     x, w, dy = _problem(rows=515, cols=4096)

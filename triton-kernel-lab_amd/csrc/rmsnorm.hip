@@ -10,10 +10,10 @@
 // dweight = sum over rows of dy*x_hat.
 //
 // The reference accumulates dweight partials under a global spin lock in an
-// order that depends on scheduling. Here each workgroup is one group: it owns
-// the rows r with r % group_size == g, keeps its column partials in registers
-// (a thread always holds the same columns), folds its waves together in LDS
-// in a fixed order and writes partial_dw[g] once. Stage 2 sums the partial
+// order that depends on scheduling. Here each workgroup is one group: it owns a
+// contiguous range of ceil(rows / group_count) rows, keeps its column partials in
+// registers (a thread always holds the same columns), folds its row slots together
+// in LDS in a fixed order and writes partial_dw[g] once. Stage 2 sums the partial
 // rows in a fixed order. Both stages are bitwise reproducible.
 #include "rows.hpp"
 
@@ -60,6 +60,91 @@ __global__ __launch_bounds__(RT >= kNormBlock ? RT : kNormBlock) void rmsnorm_fw
   if (rstd_out != nullptr && lane == 0) rstd_out[row] = rstd;
 }
 
+// Row tensors of the backward stage 1 and their row strides.
+template <typename T>
+struct RowPtrs {
+  const T* x;
+  const T* dy;
+  const T* inc;
+  T* dx;
+  int64_t xs, dys, incs, dxs;
+};
+
+// One row's x, dy, incoming gradient and rstd, held in registers.
+template <typename Row>
+struct RowSet {
+  Row x, dy, inc;
+  float r;
+};
+
+template <typename T, typename Row>
+__device__ __forceinline__ void load_rowset(RowSet<Row>& s, const RowPtrs<T>& p, int64_t row,
+                                            int cols, int lane, const float* rstd) {
+  s.x.load(p.x + row * p.xs, cols, lane);
+  s.dy.load(p.dy + row * p.dys, cols, lane);
+  if (p.inc != nullptr) s.inc.load(p.inc + row * p.incs, cols, lane);
+  s.r = rstd[row];
+}
+
+// Branch-free row load for 16-byte vectors: a raw buffer load per chunk, with columns
+// past `cols` outside the buffer and read as zero. Without branches the compiler can
+// count the loads still in flight exactly and wait only for the row it uses.
+template <typename T, int VEC, int RT, typename Row>
+__device__ __forceinline__ void load_row_buf(Row& r, const T* row, int cols, int lane) {
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)row, (short)0, uint32_t(cols) * uint32_t(sizeof(T)), 0x00020000);
+#pragma unroll
+  for (int i = 0; i < Row::ITEMS; ++i) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 u = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, uint32_t((i * RT + lane) * VEC * sizeof(T)), 0, 0));
+    r.w[i * 4 + 0] = u[0];
+    r.w[i * 4 + 1] = u[1];
+    r.w[i * 4 + 2] = u[2];
+    r.w[i * 4 + 3] = u[3];
+  }
+}
+
+template <typename T, int VEC, int RT, typename Row>
+__device__ __forceinline__ void load_rowset_buf(RowSet<Row>& s, const RowPtrs<T>& p, int64_t row,
+                                                int cols, int lane, const float* rstd) {
+  load_row_buf<T, VEC, RT>(s.x, p.x + row * p.xs, cols, lane);
+  load_row_buf<T, VEC, RT>(s.dy, p.dy + row * p.dys, cols, lane);
+  if (p.inc != nullptr) load_row_buf<T, VEC, RT>(s.inc, p.inc + row * p.incs, cols, lane);
+  s.r = rstd[row];
+}
+
+// dx of one row and its dweight contribution: x_hat = x*rstd, g = w*dy,
+// dx = rstd*(g - x_hat*mean(g*x_hat)) (+ incoming), acc += dy*x_hat. Every thread of the
+// row group calls it (group_allreduce holds block barriers for multi-wave rows).
+template <typename T, int VEC, int RT, int VALS, bool ACC_LDS, typename Row>
+__device__ __forceinline__ void stage1_row(RowSet<Row>& s, const Row& wv, const RowPtrs<T>& p,
+                                           int64_t row, int cols, int lane, float* acc,
+                                           float* fold, float* scratch) {
+  float dot = 0.f;
+#pragma unroll
+  for (int e = 0; e < VALS; ++e) {
+    const float x_hat = s.x.get(e) * s.r;
+    const float d = s.dy.get(e);
+    if constexpr (ACC_LDS)
+      fold[tk::row_column<VEC, RT>(e, lane)] += d * x_hat;
+    else
+      acc[e] += d * x_hat;
+    dot += (wv.get(e) * d) * x_hat;
+  }
+  dot = tk::group_allreduce<RT>(dot, tk::SumOp{}, scratch);
+  const float mean = dot / static_cast<float>(cols);
+#pragma unroll
+  for (int e = 0; e < VALS; ++e) {
+    const float x_hat = s.x.get(e) * s.r;
+    const float g = wv.get(e) * s.dy.get(e);
+    float v = s.r * (g - x_hat * mean);
+    if (p.inc != nullptr) v += s.inc.get(e);
+    s.x.set(e, v);
+  }
+  s.x.store(p.dx + row * p.dxs, cols, lane);
+}
+
 // Threads per workgroup of the backward stage 1: four single-wave row slots,
 // or one multi-wave row group.
 template <int RT>
@@ -70,7 +155,7 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
     T* __restrict__ dx, const T* __restrict__ dy, const T* __restrict__ incoming,
     float* __restrict__ partial, const T* __restrict__ x, const T* __restrict__ weight,
     const float* __restrict__ rstd, int32_t* __restrict__ counts, int rows, int cols,
-    int64_t x_stride, int64_t dy_stride, int64_t inc_stride, int64_t dx_stride, int group_size) {
+    int64_t x_stride, int64_t dy_stride, int64_t inc_stride, int64_t dx_stride) {
   constexpr int SLOTS = bwd_block<RT>() / RT;
   constexpr int WIDTH = RT * VALS;  // columns one row slot covers
   using Row = tk::RawRow<T, VEC, RT, VALS>;
@@ -84,11 +169,16 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
   __shared__ float scratch[RT / 64];
 
   const int group = blockIdx.x;
-  const int slot = threadIdx.x / RT;
+  // A slot is one wave or a whole workgroup, so it is wave-uniform (and so are the row
+  // addresses and buffer descriptors derived from it).
+  const int slot = __builtin_amdgcn_readfirstlane(threadIdx.x / RT);
   const int lane = threadIdx.x % RT;
-  // Rows of this group: group + k*group_size, k = 0, 1, ...; slot s takes k = s mod SLOTS.
-  const int group_rows = (rows - 1 - group) / group_size + 1;
-  const int iters = (group_rows + SLOTS - 1) / SLOTS;
+  // Rows of this group: a contiguous range of rows_per_group rows (neighbouring groups
+  // stream neighbouring rows, which keeps HBM pages open); slot s takes the rows
+  // k = s mod SLOTS of the range.
+  const int rows_per_group = (rows + gridDim.x - 1) / gridDim.x;
+  const int group_first = group * rows_per_group;
+  const int group_rows = max(0, min(rows_per_group, rows - group_first));
 
   // dweight partials of this thread's columns, accumulated over its rows in order.
   float acc[ACC_LDS ? 1 : VALS];
@@ -100,70 +190,46 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
       acc[e] = 0.f;
   }
 
-  // Rows are software-pipelined where registers allow (not in 1024-thread
-  // workgroups, capped at 128 registers): the next row's loads are issued before
-  // the current row is reduced, and stay in flight across the LDS-only barriers.
-  constexpr bool PREFETCH = RT < 1024 && (VEC > 1 || VALS <= 16);
-  Row xv, dv, iv;
-  float r = 0.f;
-  if (PREFETCH && slot < group_rows) {
-    const int64_t row = static_cast<int64_t>(group) + static_cast<int64_t>(slot) * group_size;
-    xv.load(x + row * x_stride, cols, lane);
-    dv.load(dy + row * dy_stride, cols, lane);
-    if (incoming != nullptr) iv.load(incoming + row * inc_stride, cols, lane);
-    r = rstd[row];
-  }
-  for (int it = 0; it < iters; ++it) {
-    const int k = it * SLOTS + slot;
-    // Single-wave slots skip missing rows; the threads of a multi-wave group
-    // (SLOTS == 1) always have a row, so the barriers in group_allreduce line up.
-    if (SLOTS > 1 && k >= group_rows) break;
-    const int64_t row = static_cast<int64_t>(group) + static_cast<int64_t>(k) * group_size;
-    if constexpr (!PREFETCH) {
-      xv.load(x + row * x_stride, cols, lane);
-      dv.load(dy + row * dy_stride, cols, lane);
-      if (incoming != nullptr) iv.load(incoming + row * inc_stride, cols, lane);
-      r = rstd[row];
+  // The weight row is loaded once, before any row: a load issued after the prefetches
+  // would make its wait (in-order vmcnt) wait for them too.
+  Row wv;
+  wv.load(weight, cols, lane);
+  const RowPtrs<T> ptr{x, dy, incoming, dx, x_stride, dy_stride, inc_stride, dx_stride};
+  const int64_t first = group_first;
+  if (group_rows == 0) {
+    // Trailing groups past the last row (rows not a multiple of the group count) own no
+    // rows; they only write a zero partial row. The pipeline below reads unconditionally.
+  } else if constexpr (RT < 1024 && VEC * sizeof(T) == 16) {
+    // Software pipeline, unrolled by three so the three row buffers rotate roles
+    // without register copies (a copy would wait for the load still in flight): the
+    // loads of the next two rows of this slot overlap the current row's reduction.
+    // Loads are unconditional (past the group's last row they re-read that row), so
+    // the wait before each row counts exactly the two younger rows' loads.
+    RowSet<Row> ra, rb, rc;
+    const int last = max(group_rows - 1, 0);
+    auto rowk = [&](int k) { return first + min(k, last); };
+    const int k0 = slot;
+    load_rowset_buf<T, VEC, RT>(ra, ptr, rowk(k0), cols, lane, rstd);
+    load_rowset_buf<T, VEC, RT>(rb, ptr, rowk(k0 + SLOTS), cols, lane, rstd);
+    for (int k = k0; k < group_rows; k += 3 * SLOTS) {
+      load_rowset_buf<T, VEC, RT>(rc, ptr, rowk(k + 2 * SLOTS), cols, lane, rstd);
+      stage1_row<T, VEC, RT, VALS, ACC_LDS>(ra, wv, ptr, first + k, cols, lane, acc, fold, scratch);
+      if (k + SLOTS >= group_rows) break;
+      load_rowset_buf<T, VEC, RT>(ra, ptr, rowk(k + 3 * SLOTS), cols, lane, rstd);
+      stage1_row<T, VEC, RT, VALS, ACC_LDS>(rb, wv, ptr, first + k + SLOTS, cols, lane, acc, fold,
+                                            scratch);
+      if (k + 2 * SLOTS >= group_rows) break;
+      load_rowset_buf<T, VEC, RT>(rb, ptr, rowk(k + 4 * SLOTS), cols, lane, rstd);
+      stage1_row<T, VEC, RT, VALS, ACC_LDS>(rc, wv, ptr, first + k + 2 * SLOTS, cols, lane, acc,
+                                            fold, scratch);
     }
-    const bool more = PREFETCH && k + SLOTS < group_rows;
-    Row xn, dn, in;
-    float rn = 0.f;
-    if (more) {
-      const int64_t next = row + static_cast<int64_t>(SLOTS) * group_size;
-      xn.load(x + next * x_stride, cols, lane);
-      dn.load(dy + next * dy_stride, cols, lane);
-      if (incoming != nullptr) in.load(incoming + next * inc_stride, cols, lane);
-      rn = rstd[next];
-    }
-    Row wv;
-    wv.load(weight, cols, lane);  // 2*cols bytes, served from cache
-    float dot = 0.f;
-#pragma unroll
-    for (int e = 0; e < VALS; ++e) {
-      const float x_hat = xv.get(e) * r;
-      const float d = dv.get(e);
-      if constexpr (ACC_LDS)
-        fold[tk::row_column<VEC, RT>(e, lane)] += d * x_hat;
-      else
-        acc[e] += d * x_hat;
-      dot += (wv.get(e) * d) * x_hat;
-    }
-    dot = tk::group_allreduce<RT>(dot, tk::SumOp{}, scratch);
-    const float mean = dot / static_cast<float>(cols);
-#pragma unroll
-    for (int e = 0; e < VALS; ++e) {
-      const float x_hat = xv.get(e) * r;
-      const float g = wv.get(e) * dv.get(e);
-      float v = r * (g - x_hat * mean);
-      if (incoming != nullptr) v += iv.get(e);
-      xv.set(e, v);
-    }
-    xv.store(dx + row * dx_stride, cols, lane);
-    if (more) {
-      xv = xn;
-      dv = dn;
-      iv = in;
-      r = rn;
+  } else {
+    // 1024-thread workgroups (at most 128 registers) and the unaligned scalar path:
+    // one row at a time.
+    RowSet<Row> ra;
+    for (int k = slot; k < group_rows; k += SLOTS) {
+      load_rowset<T>(ra, ptr, first + k, cols, lane, rstd);
+      stage1_row<T, VEC, RT, VALS, ACC_LDS>(ra, wv, ptr, first + k, cols, lane, acc, fold, scratch);
     }
   }
 
@@ -307,7 +373,7 @@ extern "C" int tk_rmsnorm_bwd_stage1(int dtype, void* dx, const void* dy, const 
                            static_cast<const T*>(dy), static_cast<const T*>(incoming_dx),
                            partial_dw, static_cast<const T*>(x), static_cast<const T*>(weight),
                            rstd, counts, (int)rows, (int)cols, x_row_stride, dy_row_stride,
-                           incoming_dx_row_stride, dx_row_stride, (int)group_size))));
+                           incoming_dx_row_stride, dx_row_stride))));
   return tk::check_launch("rmsnorm_bwd_stage1");
 }
 
