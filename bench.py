@@ -21,6 +21,9 @@ GEMM, attention) per kernel. Memory-bound rows run back-to-back launches that
 rotate over enough copies of their tensors to touch at least 1 GiB (four times
 the 256 MiB last-level cache), so they measure steady HBM streaming without
 cache reuse; MFMA rows flush 1 GiB before each launch.
+``measured_roofs`` holds the ceilings this GPU sustains (the library's copy and
+dense-MFMA calibration kernels); every row and ``roofline`` also carry
+``frac_measured`` against them, beside ``frac`` against the published peaks.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu]
 """
@@ -179,7 +182,75 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
-def kernel_table(torch, device) -> list[dict]:
+def measured_roofs(torch, device) -> dict:
+    """Roofs this GPU sustains, from the library's calibration kernels.
+
+    Copy: tk_roof_copy of 1 GiB back to back (2 GiB of HBM traffic per launch),
+    beside torch's own device copy; the larger is the copy roof. MFMA: tk_roof_mfma
+    with 8192 waves (8 per SIMD) of dense v_mfma_f32_32x32x16 and no memory
+    traffic, timed like the MFMA rows (1 GiB flush before each launch), at about
+    the length of the 8192^3 GEMM (~1 ms) and of the causal attention forward
+    (~4 ms), since sustained clocks fall with the length of a dense MFMA burst.
+    """
+    from tklab import _hip
+
+    src = torch.ones(1 << 28, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    nbytes = src.numel() * 4
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def copy_ms(fn, reps: int = 20) -> float:
+        for _ in range(3):
+            fn()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    own = 2 * nbytes / copy_ms(lambda: _hip.call("tk_roof_copy", src.data_ptr(), dst.data_ptr(),
+                                                  nbytes, stream)) / 1e6
+    ref = 2 * nbytes / copy_ms(lambda: dst.copy_(src)) / 1e6
+    if not torch.equal(src, dst):
+        raise RuntimeError("tk_roof_copy produced a wrong copy")
+    del src, dst
+    flush = torch.empty(1 << 28, dtype=torch.float32, device=device)
+    waves = 8192
+    out = torch.empty(waves, dtype=torch.float32, device=device)
+    mfma: dict[str, dict[str, float]] = {}
+    for dt_name, code in (("float16", 1), ("bfloat16", 2)):
+        mfma[dt_name] = {}
+        for label, iters in (("1ms", 1000), ("4ms", 4000)):
+            times = []
+            for _ in range(6):
+                flush.zero_()
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record()
+                _hip.call("tk_roof_mfma", code, out.data_ptr(), waves, iters, stream)
+                b.record()
+                times.append((a, b))
+            torch.cuda.synchronize()
+            ms = statistics.median(x.elapsed_time(y) for x, y in times[1:])
+            mfma[dt_name][label] = round(waves * iters * 8 * 32768 / ms / 1e9, 1)
+        if not bool(torch.isfinite(out).all()):
+            raise RuntimeError("tk_roof_mfma produced non-finite sums")
+    del flush, out
+    torch.cuda.empty_cache()
+    return {
+        "copy_GBps": round(max(own, ref), 1),
+        "copy_kernels_GBps": {"tk_roof_copy": round(own, 1), "torch copy_": round(ref, 1)},
+        "mfma_TFLOPs": mfma,
+        "note": "measured on this GPU by bench.py; frac_measured divides by copy_GBps "
+                "(HBM rows) or by the MFMA roof of the nearer burst length (MFMA rows)",
+    }
+
+
+def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
     """Per-kernel timings of every benchmark configuration (see the module docstring)."""
     from tklab.kernels import flash_attention as fa
     from tklab.kernels import fused_softmax as sm
@@ -224,14 +295,21 @@ def kernel_table(torch, device) -> list[dict]:
         """`make(i)` returns the launch for tensor copy i (copy 0 may reuse the originals)."""
         ms = streamed(make, nbytes, reps)
         gbps = nbytes / ms / 1e6
-        rows.append({"kernel": name, "config": config, "ms": round(ms, 4), "bytes": nbytes,
-                     "GB/s": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4)})
+        row = {"kernel": name, "config": config, "ms": round(ms, 4), "bytes": nbytes,
+               "GB/s": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4)}
+        if roofs:
+            row["frac_measured"] = round(gbps / roofs["copy_GBps"], 4)
+        rows.append(row)
 
     def mfma_row(name, config, fn, flops, dtype, reps=10):
         ms = timed(fn, reps)
         tf = flops / ms / 1e9
-        rows.append({"kernel": name, "config": config, "ms": round(ms, 4), "flops": flops,
-                     "TFLOP/s": round(tf, 1), "frac": round(tf / MFMA_PEAK_TFLOPS[dtype], 4)})
+        row = {"kernel": name, "config": config, "ms": round(ms, 4), "flops": flops,
+               "TFLOP/s": round(tf, 1), "frac": round(tf / MFMA_PEAK_TFLOPS[dtype], 4)}
+        if roofs:
+            roof = roofs["mfma_TFLOPs"][dtype]["1ms" if ms < 2.5 else "4ms"]
+            row["frac_measured"] = round(tf / roof, 4)
+        rows.append(row)
 
     g = torch.Generator(device=device).manual_seed(0)
     bf16 = torch.bfloat16
@@ -376,8 +454,12 @@ def main() -> int:
     }
     del step
     torch.cuda.empty_cache()
+    roofs = measured_roofs(torch, device)
+    line["measured_roofs"] = roofs
+    roofline["measured_peak"] = roofs["copy_GBps"]
+    roofline["frac_measured"] = round(achieved / roofs["copy_GBps"], 4)
     if not args.no_kernels:
-        line["kernels"] = kernel_table(torch, device)
+        line["kernels"] = kernel_table(torch, device, roofs)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     else:

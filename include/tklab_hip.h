@@ -62,9 +62,10 @@ int tk_rmsnorm_fwd(int dtype, const void* x, const void* residual, const void* w
 
 /* RMSNorm backward, stage 1: per-row dx (plus `incoming_dx` when non-null) and
  * one float32 dweight partial row per group, partial_dw[group_count][cols].
- * Group g (g < group_count = min(group_size, rows)) owns rows r with
- * r % group_size == g and writes partial_dw[g] with a plain store, in a fixed
- * summation order (deterministic, no atomics). `locks` is int32[2*group_size]:
+ * Group g (g < group_count = min(group_size, rows)) owns the contiguous rows
+ * [g*q, min((g+1)*q, rows)) with q = ceil(rows / group_count) and writes
+ * partial_dw[g] with a plain store, in a fixed summation order (deterministic,
+ * no atomics); a group past the last row writes a zero partial row. `locks` is int32[2*group_size]:
  * the first half is left untouched (zero), the second half gets 1 in every
  * slot g < group_count, marking partial row g as written.
  * Replaces `_rms_norm_backward_stage1_kernel[(rows,)]`, src/tklab/kernels/rms_norm.py:309-327. */
@@ -184,8 +185,8 @@ int tk_layernorm_fwd(int dtype, const void* x, const void* weight, const void* b
                      int64_t y_row_stride, float eps, void* stream);
 
 /* LayerNorm backward stage 1: dx per row and float32 dweight/dbias partial rows
- * per group, with the same group, count and determinism contract as
- * tk_rmsnorm_bwd_stage1.
+ * per group, with the same count and determinism contract as
+ * tk_rmsnorm_bwd_stage1; group g owns the rows r with r % group_size == g.
  * Replaces `_layer_norm_backward_stage1_kernel[(rows,)]`, src/tklab/kernels/layer_norm.py:316-333. */
 int tk_layernorm_bwd_stage1(int dtype, void* dx, const void* dy, float* partial_dw,
                             float* partial_db, const void* x, const void* weight,
@@ -197,6 +198,20 @@ int tk_layernorm_bwd_stage1(int dtype, void* dx, const void* dy, float* partial_
  * Replaces `_layer_norm_backward_stage2_kernel[...]`, src/tklab/kernels/layer_norm.py:341-350. */
 int tk_layernorm_bwd_stage2(int dtype, const float* partial_dw, const float* partial_db, void* dw,
                             void* db, int64_t group_count, int64_t cols, void* stream);
+
+/* ---- Calibration kernels (no counterpart in the reference). They measure the
+ * roofs this GPU sustains, so that the kernels above can be priced against
+ * measured ceilings beside the published peaks. */
+
+/* Copy `bytes` (a multiple of 16; 16-byte aligned pointers) from src to dst with
+ * 16-byte accesses, four loads in flight per thread: the streaming roof. */
+int tk_roof_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
+/* Dense MFMA issue with no memory traffic: `waves` waves (a multiple of 4) each
+ * run `iters` (a multiple of 8) iterations of 8 independent v_mfma_f32_32x32x16
+ * (dtype TK_DTYPE_F16 or TK_DTYPE_BF16) on random operand bits held in
+ * registers, and write one float to out[wave]. Work: waves * iters * 8 * 32768 FLOP. */
+int tk_roof_mfma(int dtype, float* out, int64_t waves, int64_t iters, void* stream);
 
 #ifdef __cplusplus
 }

@@ -31,19 +31,35 @@ __global__ __launch_bounds__(RT >= kNormBlock ? RT : kNormBlock) void rmsnorm_fw
   constexpr int SLOTS = RT >= kNormBlock ? 1 : kNormBlock / RT;
   using Row = tk::RawRow<T, VEC, RT, VALS>;
   __shared__ float scratch[RT / 64];
+  // 16-byte rows go through buffer accesses with per-stream cache policies: the
+  // inputs are streamed (non-temporal), the outputs stored with sc1.
+  constexpr bool kBuf = VEC * sizeof(T) == 16;
   const int lane = threadIdx.x % RT;
-  const int row = blockIdx.x * SLOTS + threadIdx.x / RT;
+  // A wave's threads share one row (RT >= 64); readfirstlane makes that visible to
+  // the compiler, so the row's buffer resource lives in scalar registers.
+  const int row = __builtin_amdgcn_readfirstlane(blockIdx.x * SLOTS + threadIdx.x / RT);
   if (row >= rows) return;  // SLOTS > 1 only for barrier-free single-wave rows
 
   // s is kept in the storage type: with a residual it is rounded there anyway.
   Row sv;
-  sv.load(x + row * x_stride, cols, lane);
+  if constexpr (kBuf)
+    sv.template load_buf<tk::kCpolStream>(x + row * x_stride, cols, lane);
+  else
+    sv.load(x + row * x_stride, cols, lane);
   if (residual != nullptr) {
     Row rv;
-    rv.load(residual + row * r_stride, cols, lane);
+    if constexpr (kBuf)
+      rv.template load_buf<tk::kCpolStream>(residual + row * r_stride, cols, lane);
+    else
+      rv.load(residual + row * r_stride, cols, lane);
 #pragma unroll
     for (int e = 0; e < VALS; ++e) sv.set(e, sv.get(e) + rv.get(e));
-    if (residual_sum != nullptr) sv.store(residual_sum + row * s_stride, cols, lane);
+    if (residual_sum != nullptr) {
+      if constexpr (kBuf)
+        sv.template store_buf<tk::kCpolSc1>(residual_sum + row * s_stride, cols, lane);
+      else
+        sv.store(residual_sum + row * s_stride, cols, lane);
+    }
   }
 
   float ss = 0.f;
@@ -56,7 +72,10 @@ __global__ __launch_bounds__(RT >= kNormBlock ? RT : kNormBlock) void rmsnorm_fw
   wv.load(weight, cols, lane);
 #pragma unroll
   for (int e = 0; e < VALS; ++e) wv.set(e, sv.get(e) * rstd * wv.get(e));
-  wv.store(y + row * y_stride, cols, lane);
+  if constexpr (kBuf)
+    wv.template store_buf<tk::kCpolSc1>(y + row * y_stride, cols, lane);
+  else
+    wv.store(y + row * y_stride, cols, lane);
   if (rstd_out != nullptr && lane == 0) rstd_out[row] = rstd;
 }
 
@@ -86,31 +105,15 @@ __device__ __forceinline__ void load_rowset(RowSet<Row>& s, const RowPtrs<T>& p,
   s.r = rstd[row];
 }
 
-// Branch-free row load for 16-byte vectors: a raw buffer load per chunk, with columns
-// past `cols` outside the buffer and read as zero. Without branches the compiler can
-// count the loads still in flight exactly and wait only for the row it uses.
-template <typename T, int VEC, int RT, typename Row>
-__device__ __forceinline__ void load_row_buf(Row& r, const T* row, int cols, int lane) {
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)row, (short)0, uint32_t(cols) * uint32_t(sizeof(T)), 0x00020000);
-#pragma unroll
-  for (int i = 0; i < Row::ITEMS; ++i) {
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    const u32x4 u = __builtin_bit_cast(
-        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, uint32_t((i * RT + lane) * VEC * sizeof(T)), 0, 0));
-    r.w[i * 4 + 0] = u[0];
-    r.w[i * 4 + 1] = u[1];
-    r.w[i * 4 + 2] = u[2];
-    r.w[i * 4 + 3] = u[3];
-  }
-}
-
-template <typename T, int VEC, int RT, typename Row>
+// Branch-free, non-temporal row loads for 16-byte vectors (RawRow::load_buf: columns
+// past `cols` read as zero). Without branches the compiler can count the loads still
+// in flight exactly and wait only for the row it uses.
+template <typename T, typename Row>
 __device__ __forceinline__ void load_rowset_buf(RowSet<Row>& s, const RowPtrs<T>& p, int64_t row,
                                                 int cols, int lane, const float* rstd) {
-  load_row_buf<T, VEC, RT>(s.x, p.x + row * p.xs, cols, lane);
-  load_row_buf<T, VEC, RT>(s.dy, p.dy + row * p.dys, cols, lane);
-  if (p.inc != nullptr) load_row_buf<T, VEC, RT>(s.inc, p.inc + row * p.incs, cols, lane);
+  s.x.template load_buf<tk::kCpolStream>(p.x + row * p.xs, cols, lane);
+  s.dy.template load_buf<tk::kCpolStream>(p.dy + row * p.dys, cols, lane);
+  if (p.inc != nullptr) s.inc.template load_buf<tk::kCpolStream>(p.inc + row * p.incs, cols, lane);
   s.r = rstd[row];
 }
 
@@ -142,7 +145,10 @@ __device__ __forceinline__ void stage1_row(RowSet<Row>& s, const Row& wv, const 
     if (p.inc != nullptr) v += s.inc.get(e);
     s.x.set(e, v);
   }
-  s.x.store(p.dx + row * p.dxs, cols, lane);
+  if constexpr (VEC * sizeof(T) == 16)
+    s.x.template store_buf<tk::kCpolStream>(p.dx + row * p.dxs, cols, lane);
+  else
+    s.x.store(p.dx + row * p.dxs, cols, lane);
 }
 
 // Threads per workgroup of the backward stage 1: four single-wave row slots,
@@ -209,17 +215,17 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
     const int last = max(group_rows - 1, 0);
     auto rowk = [&](int k) { return first + min(k, last); };
     const int k0 = slot;
-    load_rowset_buf<T, VEC, RT>(ra, ptr, rowk(k0), cols, lane, rstd);
-    load_rowset_buf<T, VEC, RT>(rb, ptr, rowk(k0 + SLOTS), cols, lane, rstd);
+    load_rowset_buf<T>(ra, ptr, rowk(k0), cols, lane, rstd);
+    load_rowset_buf<T>(rb, ptr, rowk(k0 + SLOTS), cols, lane, rstd);
     for (int k = k0; k < group_rows; k += 3 * SLOTS) {
-      load_rowset_buf<T, VEC, RT>(rc, ptr, rowk(k + 2 * SLOTS), cols, lane, rstd);
+      load_rowset_buf<T>(rc, ptr, rowk(k + 2 * SLOTS), cols, lane, rstd);
       stage1_row<T, VEC, RT, VALS, ACC_LDS>(ra, wv, ptr, first + k, cols, lane, acc, fold, scratch);
       if (k + SLOTS >= group_rows) break;
-      load_rowset_buf<T, VEC, RT>(ra, ptr, rowk(k + 3 * SLOTS), cols, lane, rstd);
+      load_rowset_buf<T>(ra, ptr, rowk(k + 3 * SLOTS), cols, lane, rstd);
       stage1_row<T, VEC, RT, VALS, ACC_LDS>(rb, wv, ptr, first + k + SLOTS, cols, lane, acc, fold,
                                             scratch);
       if (k + 2 * SLOTS >= group_rows) break;
-      load_rowset_buf<T, VEC, RT>(rb, ptr, rowk(k + 4 * SLOTS), cols, lane, rstd);
+      load_rowset_buf<T>(rb, ptr, rowk(k + 4 * SLOTS), cols, lane, rstd);
       stage1_row<T, VEC, RT, VALS, ACC_LDS>(rc, wv, ptr, first + k + 2 * SLOTS, cols, lane, acc,
                                             fold, scratch);
     }

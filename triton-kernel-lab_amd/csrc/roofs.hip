@@ -1,0 +1,152 @@
+// Calibration kernels: the measured roofs the hot-path kernels are priced
+// against, beside the published peaks.
+//
+//   tk_roof_copy  — device-to-device copy at the HBM streaming limit: 16-byte
+//                   accesses, each thread issuing the loads of kUnroll chunks of a
+//                   contiguous 4 KiB-per-wave run before its stores (the same
+//                   access shape as the elementwise kernels).
+//   tk_roof_mfma  — dense v_mfma_f32_32x32x16_{f16,bf16} issue with no memory
+//                   traffic: each wave keeps kChains independent 32x32 float32
+//                   accumulators so back-to-back MFMAs never wait on one
+//                   another, and writes one float per wave at the end so none of
+//                   the work can be removed.
+//
+// Neither has a counterpart in the reference; they exist so that achieved
+// GB/s and TFLOP/s can be stated as fractions of what this GPU sustains at the
+// clocks it runs at under load, not only of the published peaks.
+#include "tk_common.hpp"
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ copy
+
+constexpr int kCopyBlock = 256;
+constexpr int kCopyUnroll = 4;
+constexpr int64_t kCopyMaxBlocks = 8192;
+
+__global__ __launch_bounds__(kCopyBlock) void roof_copy_kernel(const i32x4* __restrict__ src,
+                                                               i32x4* __restrict__ dst,
+                                                               int64_t chunks) {
+  constexpr int64_t kPass = int64_t(kCopyBlock) * kCopyUnroll;
+  for (int64_t base = int64_t(blockIdx.x) * kPass; base < chunks;
+       base += int64_t(gridDim.x) * kPass) {
+    const int64_t i0 = base + threadIdx.x;
+    i32x4 v[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int64_t i = i0 + int64_t(u) * kCopyBlock;
+      if (i < chunks) v[u] = src[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) {
+      const int64_t i = i0 + int64_t(u) * kCopyBlock;
+      if (i < chunks) dst[i] = v[u];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ MFMA
+
+constexpr int kMfmaBlock = 256;  // four waves, one per SIMD
+constexpr int kChains = 8;       // independent accumulators per wave
+
+template <typename T>
+struct RoofMma;
+template <>
+struct RoofMma<_Float16> {
+  __device__ __forceinline__ static f32x16 run(i32x4 a, i32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct RoofMma<__bf16> {
+  __device__ __forceinline__ static f32x16 run(i32x4 a, i32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(kMfmaBlock) void roof_mfma_kernel(float* __restrict__ out,
+                                                               int iters) {
+  const int wave = (blockIdx.x * kMfmaBlock + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  // Operands with random sign and mantissa bits (magnitudes in [0.5, 1) for f16,
+  // [2^-8, 2^-7) for bf16), a different pair for every chain, so the multiplier
+  // inputs toggle the way real data does; constant operands draw less power and
+  // let the clock run higher than any GEMM can.
+  i32x4 a[kChains], b[kChains];
+  uint32_t h = 0x9E3779B9u * static_cast<uint32_t>(wave * 64 + lane + 1);
+  auto next = [&h]() {  // xorshift32
+    h ^= h << 13;
+    h ^= h >> 17;
+    h ^= h << 5;
+    return static_cast<int>((h & 0x83FF83FFu) | 0x38003800u);
+  };
+#pragma unroll
+  for (int c = 0; c < kChains; ++c) {
+    a[c] = i32x4{next(), next(), next(), next()};
+    b[c] = i32x4{next(), next(), next(), next()};
+  }
+  f32x16 acc[kChains];
+#pragma unroll
+  for (int c = 0; c < kChains; ++c) acc[c] = f32x16{};
+  // kChains iterations per trip, so that every operand index is static.
+  for (int it = 0; it < iters; it += kChains) {
+#pragma unroll
+    for (int r = 0; r < kChains; ++r)
+#pragma unroll
+      for (int c = 0; c < kChains; ++c)
+        acc[c] = RoofMma<T>::run(a[c], b[(c + r) & (kChains - 1)], acc[c]);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < kChains; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += acc[c][r];
+  if (lane == 0) out[wave] = s;
+}
+
+}  // namespace
+
+extern "C" int tk_roof_copy(const void* src, void* dst, int64_t bytes, void* stream) {
+  if (bytes < 0 || bytes % 16 != 0)
+    return tk::fail("tk_roof_copy: bytes must be a non-negative multiple of 16 (got %lld)",
+                    static_cast<long long>(bytes));
+  if (bytes == 0) return 0;
+  if (src == nullptr || dst == nullptr || !tk::aligned16(src) || !tk::aligned16(dst))
+    return tk::fail("tk_roof_copy: src and dst must be non-null and 16-byte aligned");
+  const int64_t chunks = bytes / 16;
+  int64_t blocks = tk::cdiv(chunks, int64_t(kCopyBlock) * kCopyUnroll);
+  if (blocks > kCopyMaxBlocks) blocks = kCopyMaxBlocks;
+  hipLaunchKernelGGL(roof_copy_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kCopyBlock), 0,
+                     tk::as_stream(stream), static_cast<const i32x4*>(src),
+                     static_cast<i32x4*>(dst), chunks);
+  return tk::check_launch("tk_roof_copy");
+}
+
+extern "C" int tk_roof_mfma(int dtype, float* out, int64_t waves, int64_t iters, void* stream) {
+  if (dtype != TK_DTYPE_F16 && dtype != TK_DTYPE_BF16)
+    return tk::fail("tk_roof_mfma: dtype must be TK_DTYPE_F16 or TK_DTYPE_BF16");
+  if (waves <= 0 || waves % (kMfmaBlock / 64) != 0 || waves > (int64_t(1) << 24))
+    return tk::fail("tk_roof_mfma: waves must be a positive multiple of %d up to 2^24 (got %lld)",
+                    kMfmaBlock / 64, static_cast<long long>(waves));
+  if (iters <= 0 || iters % kChains != 0 || iters > (int64_t(1) << 30))
+    return tk::fail("tk_roof_mfma: iters must be a positive multiple of %d up to 2^30 (got %lld)",
+                    kChains, static_cast<long long>(iters));
+  if (out == nullptr) return tk::fail("tk_roof_mfma: out is null");
+  const dim3 grid(static_cast<unsigned>(waves / (kMfmaBlock / 64)));
+  if (dtype == TK_DTYPE_F16)
+    hipLaunchKernelGGL(roof_mfma_kernel<_Float16>, grid, dim3(kMfmaBlock), 0,
+                       tk::as_stream(stream), out, static_cast<int>(iters));
+  else
+    hipLaunchKernelGGL(roof_mfma_kernel<__bf16>, grid, dim3(kMfmaBlock), 0,
+                       tk::as_stream(stream), out, static_cast<int>(iters));
+  return tk::check_launch("tk_roof_mfma");
+}

@@ -62,6 +62,8 @@ _SIGNATURES: dict[str, list[object]] = {
         _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P,
     ],
     "tk_layernorm_bwd_stage2": [_I32, _P, _P, _P, _P, _I64, _I64, _P],
+    "tk_roof_copy": [_P, _P, _I64, _P],
+    "tk_roof_mfma": [_I32, _P, _I64, _I64, _P],
 }
 
 EXPORTED_SYMBOLS: tuple[str, ...] = ("tk_abi_version", "tk_last_error", *_SIGNATURES)

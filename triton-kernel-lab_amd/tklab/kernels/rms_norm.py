@@ -7,9 +7,9 @@ with the reference's validation order and messages (``rms_norm.py:176-204``).
 
 Backward. The reference reduces dweight partials under a global spin lock in
 a scheduling-dependent order and therefore refuses PyTorch's deterministic
-mode (``rms_norm.py:370-378``). Here each of ``group_size`` workgroups owns
-the rows ``r % group_size == g``, writes one float32 partial row with a plain
-store, and stage 2 sums the partial rows in a fixed order. The result is
+mode (``rms_norm.py:370-378``). Here each of ``min(group_size, rows)``
+workgroups owns one contiguous range of ``ceil(rows / groups)`` rows, writes
+one float32 partial row with a plain store (zero for a group past the last row), and stage 2 sums the partial rows in a fixed order. The result is
 bitwise reproducible, so deterministic mode is honoured instead of refused.
 ``_BackwardBuffers.locks`` keeps its reference layout (``locks || counts``):
 the lock half stays zero and stage 1 sets count ``g`` to 1 for every active
