@@ -61,8 +61,6 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-kernels", action="store_true", help="skip the per-config kernel table")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--calibrate-copy", action="store_true",
-                   help="first run three 1 GiB device copies (reference kernel for PMC byte counts)")
     return p.parse_args()
 
 
@@ -403,13 +401,6 @@ def main() -> int:
         return 2
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
-    if args.calibrate_copy:
-        src = torch.ones(1 << 28, dtype=torch.float32, device=device)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
     step = Step(torch, device)
     ms_step, per_kernel = time_step(torch, step, args.steps, args.warmup)
     step_bytes = sum(STEP_BYTES.values())

@@ -106,8 +106,9 @@ __device__ __forceinline__ void load_rowset(RowSet<Row>& s, const RowPtrs<T>& p,
 }
 
 // Branch-free, non-temporal row loads for 16-byte vectors (RawRow::load_buf: columns
-// past `cols` read as zero). Without branches the compiler can count the loads still
-// in flight exactly and wait only for the row it uses.
+// at or past `cols` read as zero, so cols = 0 loads nothing from memory). Without
+// branches the compiler can count the loads still in flight exactly and wait only for
+// the row it uses.
 template <typename T, typename Row>
 __device__ __forceinline__ void load_rowset_buf(RowSet<Row>& s, const RowPtrs<T>& p, int64_t row,
                                                 int cols, int lane, const float* rstd) {
@@ -209,23 +210,25 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
     // Software pipeline, unrolled by three so the three row buffers rotate roles
     // without register copies (a copy would wait for the load still in flight): the
     // loads of the next two rows of this slot overlap the current row's reduction.
-    // Loads are unconditional (past the group's last row they re-read that row), so
-    // the wait before each row counts exactly the two younger rows' loads.
+    // Loads are issued unconditionally, so the wait before each row counts exactly the
+    // two younger rows' loads; past the group's last row they use a zero-length buffer
+    // (the last row's address, zero extent), which returns zeros without memory traffic.
     RowSet<Row> ra, rb, rc;
     const int last = max(group_rows - 1, 0);
     auto rowk = [&](int k) { return first + min(k, last); };
+    auto extent = [&](int k) { return k < group_rows ? cols : 0; };
     const int k0 = slot;
-    load_rowset_buf<T>(ra, ptr, rowk(k0), cols, lane, rstd);
-    load_rowset_buf<T>(rb, ptr, rowk(k0 + SLOTS), cols, lane, rstd);
+    load_rowset_buf<T>(ra, ptr, rowk(k0), extent(k0), lane, rstd);
+    load_rowset_buf<T>(rb, ptr, rowk(k0 + SLOTS), extent(k0 + SLOTS), lane, rstd);
     for (int k = k0; k < group_rows; k += 3 * SLOTS) {
-      load_rowset_buf<T>(rc, ptr, rowk(k + 2 * SLOTS), cols, lane, rstd);
+      load_rowset_buf<T>(rc, ptr, rowk(k + 2 * SLOTS), extent(k + 2 * SLOTS), lane, rstd);
       stage1_row<T, VEC, RT, VALS, ACC_LDS>(ra, wv, ptr, first + k, cols, lane, acc, fold, scratch);
       if (k + SLOTS >= group_rows) break;
-      load_rowset_buf<T>(ra, ptr, rowk(k + 3 * SLOTS), cols, lane, rstd);
+      load_rowset_buf<T>(ra, ptr, rowk(k + 3 * SLOTS), extent(k + 3 * SLOTS), lane, rstd);
       stage1_row<T, VEC, RT, VALS, ACC_LDS>(rb, wv, ptr, first + k + SLOTS, cols, lane, acc, fold,
                                             scratch);
       if (k + 2 * SLOTS >= group_rows) break;
-      load_rowset_buf<T>(rb, ptr, rowk(k + 4 * SLOTS), cols, lane, rstd);
+      load_rowset_buf<T>(rb, ptr, rowk(k + 4 * SLOTS), extent(k + 4 * SLOTS), lane, rstd);
       stage1_row<T, VEC, RT, VALS, ACC_LDS>(rc, wv, ptr, first + k + 2 * SLOTS, cols, lane, acc,
                                             fold, scratch);
     }
