@@ -204,7 +204,7 @@ int tk_layernorm_bwd_stage2(int dtype, const float* partial_dw, const float* par
  * measured ceilings beside the published peaks. */
 
 /* Copy `bytes` (a multiple of 16; 16-byte aligned pointers) from src to dst with
- * 16-byte accesses, four loads in flight per thread: the streaming roof. */
+ * 16-byte non-temporal accesses, four loads in flight per thread: the streaming roof. */
 int tk_roof_copy(const void* src, void* dst, int64_t bytes, void* stream);
 
 /* Dense MFMA issue with no memory traffic: `waves` waves (a multiple of 4) each

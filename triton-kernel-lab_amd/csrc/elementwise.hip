@@ -6,7 +6,9 @@
 // issues the loads of its kUnroll chunks before any arithmetic, so every wave keeps
 // a contiguous 4 KiB run per tensor in flight (one chunk per thread, or chunks far
 // apart, leave HBM well short of its bandwidth). Row strides are honoured, so row-sliced views need no copy; the
-// row of a chunk comes from a multiply-shift division by chunks_per_row.
+// row of a chunk comes from a multiply-shift division by chunks_per_row. Tensors
+// touched once are loaded and stored non-temporally; the RoPE cos/sin tables use
+// plain loads, since a broadcast table (row stride 0) is reused by every row.
 //
 // Floating-point contraction is disabled so each product and sum is rounded
 // separately, the same way PyTorch's pointwise ops evaluate these formulas.
@@ -67,8 +69,8 @@ __global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(
       const int i = i0 + u * kBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
-      tk::load_vec<T, VEC>(value + p.row * vs + p.col, v[u]);
-      tk::load_vec<T, VEC>(gate + p.row * gs + p.col, g[u]);
+      tk::load_vec_stream<T, VEC>(value + p.row * vs + p.col, v[u]);
+      tk::load_vec_stream<T, VEC>(gate + p.row * gs + p.col, g[u]);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -77,7 +79,7 @@ __global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
 #pragma unroll
       for (int j = 0; j < VEC; ++j) v[u][j] = v[u][j] * g[u][j] * stable_sigmoid(g[u][j]);
-      tk::store_vec<T, VEC>(y + p.row * ys + p.col, v[u]);
+      tk::store_vec_stream<T, VEC>(y + p.row * ys + p.col, v[u]);
     }
   }
 }
@@ -99,9 +101,9 @@ __global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(
       const int i = i0 + u * kBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
-      tk::load_vec<T, VEC>(dy + p.row * dys + p.col, d[u]);
-      tk::load_vec<T, VEC>(value + p.row * vs + p.col, v[u]);
-      tk::load_vec<T, VEC>(gate + p.row * gs + p.col, g[u]);
+      tk::load_vec_stream<T, VEC>(dy + p.row * dys + p.col, d[u]);
+      tk::load_vec_stream<T, VEC>(value + p.row * vs + p.col, v[u]);
+      tk::load_vec_stream<T, VEC>(gate + p.row * gs + p.col, g[u]);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -117,8 +119,8 @@ __global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(
         dv[j] = d[u][j] * silu;
         dg[j] = d[u][j] * v[u][j] * dsilu;
       }
-      tk::store_vec<T, VEC>(dvalue + p.row * dvs + p.col, dv);
-      tk::store_vec<T, VEC>(dgate + p.row * dgs + p.col, dg);
+      tk::store_vec_stream<T, VEC>(dvalue + p.row * dvs + p.col, dv);
+      tk::store_vec_stream<T, VEC>(dgate + p.row * dgs + p.col, dg);
     }
   }
 }
@@ -142,8 +144,8 @@ __global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       const T* xr = x + p.row * xs;
-      tk::load_vec<T, VEC>(xr + p.col, x1[u]);
-      tk::load_vec<T, VEC>(xr + half + p.col, x2[u]);
+      tk::load_vec_stream<T, VEC>(xr + p.col, x1[u]);
+      tk::load_vec_stream<T, VEC>(xr + half + p.col, x2[u]);
       tk::load_vec<T, VEC>(cosv + p.row * cs + p.col, co[u]);
       tk::load_vec<T, VEC>(sinv + p.row * ss + p.col, si[u]);
     }
@@ -159,8 +161,8 @@ __global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
         y2[j] = x2[u][j] * co[u][j] + x1[u][j] * si[u][j];
       }
       T* yr = y + p.row * ys;
-      tk::store_vec<T, VEC>(yr + p.col, y1);
-      tk::store_vec<T, VEC>(yr + half + p.col, y2);
+      tk::store_vec_stream<T, VEC>(yr + p.col, y1);
+      tk::store_vec_stream<T, VEC>(yr + half + p.col, y2);
     }
   }
 }
@@ -185,8 +187,8 @@ __global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       const T* dyr = dy + p.row * dys;
-      tk::load_vec<T, VEC>(dyr + p.col, d1[u]);
-      tk::load_vec<T, VEC>(dyr + half + p.col, d2[u]);
+      tk::load_vec_stream<T, VEC>(dyr + p.col, d1[u]);
+      tk::load_vec_stream<T, VEC>(dyr + half + p.col, d2[u]);
       tk::load_vec<T, VEC>(cosv + p.row * cs + p.col, co[u]);
       tk::load_vec<T, VEC>(sinv + p.row * ss + p.col, si[u]);
     }
@@ -202,22 +204,22 @@ __global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
         o2[j] = d2[u][j] * co[u][j] - d1[u][j] * si[u][j];
       }
       T* dxr = dx + p.row * dxs;
-      tk::store_vec<T, VEC>(dxr + p.col, o1);
-      tk::store_vec<T, VEC>(dxr + half + p.col, o2);
+      tk::store_vec_stream<T, VEC>(dxr + p.col, o1);
+      tk::store_vec_stream<T, VEC>(dxr + half + p.col, o2);
       if (need_x) {
         float x1[VEC], x2[VEC];
         const T* xr = x + p.row * xs;
-        tk::load_vec<T, VEC>(xr + p.col, x1);
-        tk::load_vec<T, VEC>(xr + half + p.col, x2);
+        tk::load_vec_stream<T, VEC>(xr + p.col, x1);
+        tk::load_vec_stream<T, VEC>(xr + half + p.col, x2);
         if (dcos != nullptr) {
 #pragma unroll
           for (int j = 0; j < VEC; ++j) o1[j] = d1[u][j] * x1[j] + d2[u][j] * x2[j];
-          tk::store_vec<T, VEC>(dcos + p.row * dcs + p.col, o1);
+          tk::store_vec_stream<T, VEC>(dcos + p.row * dcs + p.col, o1);
         }
         if (dsin != nullptr) {
 #pragma unroll
           for (int j = 0; j < VEC; ++j) o2[j] = -d1[u][j] * x2[j] + d2[u][j] * x1[j];
-          tk::store_vec<T, VEC>(dsin + p.row * dss + p.col, o2);
+          tk::store_vec_stream<T, VEC>(dsin + p.row * dss + p.col, o2);
         }
       }
     }

@@ -2,9 +2,9 @@
 // against, beside the published peaks.
 //
 //   tk_roof_copy  — device-to-device copy at the HBM streaming limit: 16-byte
-//                   accesses, each thread issuing the loads of kUnroll chunks of a
-//                   contiguous 4 KiB-per-wave run before its stores (the same
-//                   access shape as the elementwise kernels).
+//                   non-temporal accesses, each thread issuing the loads of kUnroll
+//                   chunks of a contiguous 4 KiB-per-wave run before its stores (the
+//                   access shape and cache policy of the elementwise kernels).
 //   tk_roof_mfma  — dense v_mfma_f32_32x32x16_{f16,bf16} issue with no memory
 //                   traffic: each wave keeps kChains independent 32x32 float32
 //                   accumulators so back-to-back MFMAs never wait on one
@@ -40,12 +40,12 @@ __global__ __launch_bounds__(kCopyBlock) void roof_copy_kernel(const i32x4* __re
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) {
       const int64_t i = i0 + int64_t(u) * kCopyBlock;
-      if (i < chunks) v[u] = src[i];
+      if (i < chunks) v[u] = __builtin_nontemporal_load(src + i);
     }
 #pragma unroll
     for (int u = 0; u < kCopyUnroll; ++u) {
       const int64_t i = i0 + int64_t(u) * kCopyBlock;
-      if (i < chunks) dst[i] = v[u];
+      if (i < chunks) __builtin_nontemporal_store(v[u], dst + i);
     }
   }
 }

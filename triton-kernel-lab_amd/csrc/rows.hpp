@@ -53,6 +53,43 @@ __device__ __forceinline__ void store_row(T* __restrict__ row, int cols, int lan
   }
 }
 
+// Branch-free 16-byte row access through a buffer resource spanning the row, with
+// cache policy CPOL; columns at or past `cols` load as `fill` and are not stored.
+// `row` must be wave-uniform (see RawRow::load_buf).
+template <typename T, int VEC, int RT, int VALS, int CPOL>
+__device__ __forceinline__ void load_row_buf(const T* row, int cols, int lane, float* v,
+                                             float fill) {
+  static_assert(VEC * sizeof(T) == 16, "16-byte vectors only");
+  constexpr int ITEMS = VALS / VEC;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<T*>(row), (short)0, uint32_t(cols) * uint32_t(sizeof(T)), 0x00020000);
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int c = (i * RT + lane) * VEC;
+    const Vec<T, VEC> r = __builtin_bit_cast(
+        Vec<T, VEC>, __builtin_amdgcn_raw_buffer_load_b128(rs, uint32_t(c * int(sizeof(T))), 0, CPOL));
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) v[i * VEC + j] = c < cols ? to_f32(r.v[j]) : fill;
+  }
+}
+
+template <typename T, int VEC, int RT, int VALS, int CPOL>
+__device__ __forceinline__ void store_row_buf(T* row, int cols, int lane, const float* v) {
+  static_assert(VEC * sizeof(T) == 16, "16-byte vectors only");
+  constexpr int ITEMS = VALS / VEC;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      row, (short)0, uint32_t(cols) * uint32_t(sizeof(T)), 0x00020000);
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int c = (i * RT + lane) * VEC;
+    Vec<T, VEC> r;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) r.v[j] = from_f32<T>(v[i * VEC + j]);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, r), rs,
+                                           uint32_t(c * int(sizeof(T))), 0, CPOL);
+  }
+}
+
 // Column of element e (0 <= e < VALS) held by thread `lane`.
 template <int VEC, int RT>
 __device__ __forceinline__ int row_column(int e, int lane) {
