@@ -321,6 +321,17 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
 
     mem_row("tk_softmax_fwd", "f32 4096x4096", softmax_copy, 2 * x.numel() * 4)
     del x
+    # Online softmax (rows past the single-pass limit): f32 [64, 1048576]. Bytes as the
+    # single-pass cost model (one read, one write); the kernel reads each row twice.
+    xw = torch.randn(64, 1 << 20, device=device, generator=g)
+
+    def online_copy(i):
+        xi = xw if i == 0 else xw.clone()
+        yi = torch.empty_like(xw)
+        return lambda: sm._launch_online((xi,), yi)
+
+    mem_row("tk_softmax_online_fwd", "f32 64x1048576", online_copy, 2 * xw.numel() * 4)
+    del xw
     # Config 3: SwiGLU bf16 [16384, 14336].
     gate = torch.randn(16384, 14336, device=device, dtype=bf16, generator=g)
     up = torch.randn(16384, 14336, device=device, dtype=bf16, generator=g)

@@ -46,6 +46,18 @@ const char* tk_last_error(void);
 int tk_softmax_fwd(int dtype, const void* x, void* y, int64_t rows, int64_t cols,
                    int64_t x_row_stride, int64_t y_row_stride, void* stream);
 
+/* Online softmax for rows of any width: the same y = exp(x - max) / sum per row,
+ * for the rows the single-pass kernel rejects (more than 65536 columns). No
+ * reference kernel exists; the reference's validator points callers there
+ * (src/tklab/kernels/fused_softmax.py:75-79, "use an online softmax").
+ * Each row is split into chunks of 16384 columns: a first launch writes every
+ * chunk's (max, sum of exp) into `partials`, float32[2 * rows * ceil(cols / 16384)],
+ * a second folds a row's partials in a fixed order and writes y.
+ * Two reads and one write per element; deterministic. cols <= 2^31 - 1. */
+int tk_softmax_online_fwd(int dtype, const void* x, void* y, float* partials, int64_t rows,
+                          int64_t cols, int64_t x_row_stride, int64_t y_row_stride,
+                          void* stream);
+
 /* RMSNorm forward with an optional fused residual add.
  *   s = residual ? round_dtype(x + residual) : x
  *   rstd = 1 / sqrt(mean(s^2) + eps);  y = s * rstd * weight

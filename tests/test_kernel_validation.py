@@ -27,6 +27,24 @@ def test_softmax_requires_a_gpu_tensor() -> None:
         softmax(torch.zeros(2, 8))
 
 
+def test_online_softmax_lifts_only_the_width_limit() -> None:
+    from tklab.kernels.fused_softmax import online_softmax
+
+    wide = torch.empty(2, 70000, device="meta")
+    with pytest.raises(ValueError, match="use an online softmax"):
+        softmax(wide)
+    with pytest.raises(ValueError, match="requires CUDA"):
+        online_softmax(wide)
+    with pytest.raises(ValueError, match="2D tensor"):
+        online_softmax(torch.empty(2, 3, 4, device="meta"))
+    with pytest.raises(ValueError, match="empty dimensions"):
+        online_softmax(torch.empty(0, 70000, device="meta"))
+    with pytest.raises(ValueError, match="contiguous final dimension"):
+        online_softmax(torch.empty(2, 140000, device="meta")[:, ::2])
+    with pytest.raises(ValueError, match="float16, bfloat16 and float32"):
+        online_softmax(torch.empty(2, 70000, device="meta", dtype=torch.float64))
+
+
 @pytest.mark.parametrize(
     ("x", "fragment"),
     [

@@ -71,3 +71,64 @@ def test_constant_rows_are_uniform_and_large_values_stay_finite() -> None:
     torch.testing.assert_close(y[0], torch.full_like(y[0], 1e-3), rtol=1e-6, atol=0)
     torch.testing.assert_close(y[2, 500:], torch.full_like(y[2, 500:], 2e-3), rtol=1e-6, atol=0)
     assert torch.all(y[2, :500] == 0)
+
+
+# ---------------------------------------------------------------- online softmax
+
+
+def _check_online(x: torch.Tensor) -> None:
+    from tklab.kernels.fused_softmax import online_softmax
+
+    y = online_softmax(x)
+    expected = dev(oracle.softmax(host(x), name(x.dtype)), y)
+    assert_close(y, expected)
+    assert_close(y, torch.softmax(x.float(), dim=-1))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("cols", [1, 1000, 16384, 16385, 65536, 65537, 200003])
+def test_online_widths_and_dtypes(dtype: torch.dtype, cols: int) -> None:
+    """Chunk edges (16384, 16385), the single-pass limit and past it, ragged tails."""
+    torch.manual_seed(cols + 7)
+    _check_online(torch.randn(5, cols, device="cuda", dtype=dtype))
+
+
+def test_online_matches_single_pass_where_both_apply() -> None:
+    from tklab.kernels.fused_softmax import online_softmax
+
+    torch.manual_seed(8)
+    x = torch.randn(64, 4096, device="cuda")
+    y1 = softmax(x)
+    y2 = online_softmax(x)
+    # One chunk per row: the same maximum, a sum over the same values.
+    torch.testing.assert_close(y2, y1, rtol=1e-6, atol=1e-9)
+
+
+def test_online_wide_row_sums_to_one_and_is_deterministic() -> None:
+    from tklab.kernels.fused_softmax import online_softmax
+
+    torch.manual_seed(9)
+    x = torch.randn(3, 1 << 21, device="cuda") * 4
+    x[1, 123456] = 80.0  # one dominant entry, far from the chunk holding the others
+    y = online_softmax(x)
+    rows = y.double().sum(dim=1)
+    torch.testing.assert_close(rows, torch.ones_like(rows), rtol=0, atol=1e-4)
+    assert_close(y, torch.softmax(x, dim=-1))
+    assert torch.equal(online_softmax(x), y)
+
+
+def test_online_strided_misaligned_and_masked_rows() -> None:
+    from tklab.kernels.fused_softmax import _launch_online
+
+    torch.manual_seed(10)
+    x = torch.randn(6, 2 * 70001, device="cuda")[:, 1:70002]  # misaligned, scalar path
+    _check_online(x)
+    x = torch.randn(4, 40000, device="cuda")
+    x[0, :20000] = -torch.inf  # whole chunks of -inf contribute nothing
+    x[2] = -1e30
+    out_storage = torch.full((4, 50000), 7.0, device="cuda")
+    out = out_storage[:, :40000]
+    _launch_online((x,), out)
+    assert_close(out, torch.softmax(x, dim=-1))
+    assert torch.all(out[0, :20000] == 0)
+    assert torch.all(out_storage[:, 40000:] == 7.0)

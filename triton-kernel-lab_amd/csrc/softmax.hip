@@ -51,7 +51,122 @@ __global__ __launch_bounds__(RT >= 256 ? RT : 256) void softmax_fwd_kernel(
     tk::store_row<T, VEC, RT, VALS>(y + row * y_stride, cols, lane, v);
 }
 
+// ------------------------------------------------------------------ online softmax
+//
+// Rows of any width (beyond the single-pass register budget): each row is split
+// into chunks of kOnlineChunk columns, one 256-thread workgroup per chunk.
+//   partial: chunk max m_c and s_c = sum exp(x - m_c) over the chunk (one read).
+//   apply:   M = max_c m_c, S = sum_c s_c * exp(m_c - M), both folded in a fixed
+//            order by every workgroup of the row; then y = exp(x - M) * (1 / S)
+//            (a second read of the chunk, one write).
+// HBM traffic is two reads and one write per element; the workspace holds two
+// floats per chunk.
+
+constexpr int kOnlineThreads = 256;
+constexpr int kOnlineVals = 64;
+constexpr int kOnlineChunk = kOnlineThreads * kOnlineVals;  // 16384 columns
+
+// The first read keeps the default cache policy (a chunk may still be in the
+// last-level cache when the second pass reads it); the second read is the last use.
+template <typename T, int VEC, int CPOL>
+__device__ __forceinline__ void load_chunk(const T* p, int n, int lane, float* v) {
+  if constexpr (VEC * sizeof(T) == 16)
+    tk::load_row_buf<T, VEC, kOnlineThreads, kOnlineVals, CPOL>(p, n, lane, v, -INFINITY);
+  else
+    tk::load_row<T, VEC, kOnlineThreads, kOnlineVals>(p, n, lane, v, -INFINITY);
+}
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(kOnlineThreads) void softmax_online_partial_kernel(
+    const T* __restrict__ x, float* __restrict__ partials, int cols, int chunks,
+    int64_t x_stride) {
+  __shared__ float scratch[kOnlineThreads / 64];
+  const int row = blockIdx.x / chunks;
+  const int chunk = blockIdx.x - row * chunks;
+  const int c0 = chunk * kOnlineChunk;
+  const int n = min(kOnlineChunk, cols - c0);
+  float v[kOnlineVals];
+  load_chunk<T, VEC, tk::kCpolDefault>(x + row * x_stride + c0, n, threadIdx.x, v);
+  float m = v[0];
+#pragma unroll
+  for (int e = 1; e < kOnlineVals; ++e) m = fmaxf(m, v[e]);
+  m = tk::group_allreduce<kOnlineThreads>(m, tk::MaxOp{}, scratch);
+  float s = 0.f;
+  if (m != -INFINITY) {
+#pragma unroll
+    for (int e = 0; e < kOnlineVals; ++e) s += expf(v[e] - m);
+  }
+  s = tk::group_allreduce<kOnlineThreads>(s, tk::SumOp{}, scratch);
+  if (threadIdx.x == 0) {
+    float* out = partials + 2 * static_cast<int64_t>(blockIdx.x);
+    out[0] = m;
+    out[1] = s;
+  }
+}
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(kOnlineThreads) void softmax_online_apply_kernel(
+    const T* __restrict__ x, T* __restrict__ y, const float* __restrict__ partials, int cols,
+    int chunks, int64_t x_stride, int64_t y_stride) {
+  __shared__ float scratch[kOnlineThreads / 64];
+  const int row = blockIdx.x / chunks;
+  const int chunk = blockIdx.x - row * chunks;
+  const int c0 = chunk * kOnlineChunk;
+  const int n = min(kOnlineChunk, cols - c0);
+  float v[kOnlineVals];
+  load_chunk<T, VEC, tk::kCpolStream>(x + row * x_stride + c0, n, threadIdx.x, v);
+  // Row statistics from the chunk partials, in a fixed order (identical in every
+  // workgroup of the row).
+  const float* pr = partials + 2 * static_cast<int64_t>(row) * chunks;
+  float m = -INFINITY;
+  for (int j = threadIdx.x; j < chunks; j += kOnlineThreads) m = fmaxf(m, pr[2 * j]);
+  m = tk::group_allreduce<kOnlineThreads>(m, tk::MaxOp{}, scratch);
+  float s = 0.f;
+  for (int j = threadIdx.x; j < chunks; j += kOnlineThreads) {
+    const float mj = pr[2 * j];
+    if (mj != -INFINITY) s += pr[2 * j + 1] * expf(mj - m);
+  }
+  s = tk::group_allreduce<kOnlineThreads>(s, tk::SumOp{}, scratch);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int e = 0; e < kOnlineVals; ++e) v[e] = expf(v[e] - m) * inv;
+  T* yr = y + row * y_stride + c0;
+  if constexpr (VEC * sizeof(T) == 16)
+    tk::store_row_buf<T, VEC, kOnlineThreads, kOnlineVals, tk::kCpolStream>(yr, n, threadIdx.x,
+                                                                             v);
+  else
+    tk::store_row<T, VEC, kOnlineThreads, kOnlineVals>(yr, n, threadIdx.x, v);
+}
+
 }  // namespace
+
+extern "C" int tk_softmax_online_fwd(int dtype, const void* x, void* y, float* partials,
+                                     int64_t rows, int64_t cols, int64_t x_row_stride,
+                                     int64_t y_row_stride, void* stream) {
+  if (!tk::valid_dtype(dtype)) return tk::fail("online softmax: unsupported dtype code %d", dtype);
+  if (x == nullptr || y == nullptr || partials == nullptr)
+    return tk::fail("online softmax: null pointer");
+  if (rows <= 0 || cols <= 0) return tk::fail("online softmax: empty problem");
+  if (cols > INT32_MAX) return tk::fail("online softmax: more than 2^31-1 columns");
+  const int64_t chunks = tk::cdiv(cols, kOnlineChunk);
+  if (rows * chunks > INT32_MAX) return tk::fail("online softmax: too many chunks");
+  const int es = tk::elem_size(dtype);
+  const int vec = 16 / es;
+  const bool vector_ok = tk::aligned16(x) && tk::aligned16(y) && cols % vec == 0 &&
+                         (x_row_stride * es) % 16 == 0 && (y_row_stride * es) % 16 == 0;
+  const dim3 grid(static_cast<unsigned>(rows * chunks));
+  const dim3 block(kOnlineThreads);
+  hipStream_t s = tk::as_stream(stream);
+  TK_DISPATCH_DTYPE(dtype, T,
+    TK_DISPATCH_VEC(T, vector_ok,
+      hipLaunchKernelGGL((softmax_online_partial_kernel<T, VEC>), grid, block, 0, s,
+                         static_cast<const T*>(x), partials, (int)cols, (int)chunks,
+                         x_row_stride);
+      hipLaunchKernelGGL((softmax_online_apply_kernel<T, VEC>), grid, block, 0, s,
+                         static_cast<const T*>(x), static_cast<T*>(y), partials, (int)cols,
+                         (int)chunks, x_row_stride, y_row_stride)));
+  return tk::check_launch("online softmax");
+}
 
 extern "C" int tk_softmax_fwd(int dtype, const void* x, void* y, int64_t rows, int64_t cols,
                               int64_t x_row_stride, int64_t y_row_stride, void* stream) {

@@ -32,6 +32,7 @@ _I64P = ctypes.POINTER(ctypes.c_int64)
 # name -> argument types, in header order (the return type is always int).
 _SIGNATURES: dict[str, list[object]] = {
     "tk_softmax_fwd": [_I32, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "tk_softmax_online_fwd": [_I32, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "tk_rmsnorm_fwd": [_I32, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _P],
     "tk_rmsnorm_bwd_stage1": [
         _I32, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P,

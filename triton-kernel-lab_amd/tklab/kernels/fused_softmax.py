@@ -4,6 +4,11 @@ Public contract of ``src/tklab/kernels/fused_softmax.py``: ``softmax(x)`` for a
 2-D tensor with a unit-stride final dimension and at most 65 536 columns; the
 validation order and messages are the reference's (``fused_softmax.py:68-87``).
 bfloat16 is accepted in addition to float16 and float32.
+
+``online_softmax(x)`` is the path the reference's width check names for rows
+beyond that limit (``fused_softmax.py:75-79``): the same function of each row,
+computed over 16 384-column chunks (``tk_softmax_online_fwd``) for any width up
+to 2^31 - 1 columns.
 """
 
 from __future__ import annotations
@@ -38,14 +43,65 @@ def softmax(x: torch.Tensor) -> torch.Tensor:
     return output
 
 
-def _validate(x: torch.Tensor) -> None:
-    """Check the single-pass softmax contract (reference ``fused_softmax.py:68-87``)."""
+def online_softmax(x: torch.Tensor) -> torch.Tensor:
+    """Softmax over the final dimension of a 2-D tensor of any width.
+
+    Same contract as :func:`softmax` without the 65 536-column limit. Each row is
+    reduced over 16 384-column chunks whose (max, sum of exp) partials are folded
+    in a fixed order, so results are deterministic; they match :func:`softmax`
+    to float32 rounding of the row sum.
+
+    Raises:
+        ValueError: on an unsupported shape, dtype, layout or device.
+    """
+    _validate(x, single_pass=False)
+    output = _make_output((x,))
+    _launch_online((x,), output)
+    return output
+
+
+def _launch_online(args: TensorArgs, output: torch.Tensor) -> None:
+    """Run the online softmax into a preallocated output."""
+    (x,) = args
+    _validate(x, single_pass=False)
+    if output.shape != x.shape or output.device != x.device or output.dtype != x.dtype:
+        raise ValueError("output metadata must match the input")
+    if output.stride(1) != 1:
+        raise ValueError("softmax output requires a contiguous final dimension")
+    assert_int32_addressable(output, name="output")
+    rows, columns = x.shape
+    chunks = -(-columns // ONLINE_CHUNK_COLUMNS)
+    partials = torch.empty(2 * rows * chunks, device=x.device, dtype=torch.float32)
+    _hip.call(
+        "tk_softmax_online_fwd",
+        _hip.dtype_code(x.dtype),
+        x.data_ptr(),
+        output.data_ptr(),
+        partials.data_ptr(),
+        rows,
+        columns,
+        x.stride(0),
+        output.stride(0),
+        _hip.stream_of(x),
+    )
+
+
+# Columns per chunk of tk_softmax_online_fwd (256 threads x 64 values); the
+# workspace holds two floats per chunk.
+ONLINE_CHUNK_COLUMNS = 16384
+
+
+def _validate(x: torch.Tensor, *, single_pass: bool = True) -> None:
+    """Check the single-pass softmax contract (reference ``fused_softmax.py:68-87``).
+
+    ``single_pass=False`` drops the width limit (the online path).
+    """
     if x.ndim != 2:
         raise ValueError("softmax expects a 2D tensor shaped (rows, columns)")
     rows, columns = x.shape
     if rows == 0 or columns == 0:
         raise ValueError("softmax does not support empty dimensions")
-    if columns > _MAX_FUSED_COLUMNS:
+    if single_pass and columns > _MAX_FUSED_COLUMNS:
         raise ValueError(
             f"n_cols={columns} exceeds the {_MAX_FUSED_COLUMNS}-column "
             "single-pass limit; use an online softmax"
