@@ -363,6 +363,19 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
     mem_row("tk_rope_bwd", "bf16 [4,32,4096,128] dx only", lambda i: rope_copy(i, True),
             3 * q.numel() * 2)
     del q, cos, sin
+    # GQA decode (reference decode model geometry Hq 32, Hkv 8, D 128; B 32, L 8192):
+    # bytes = unique KV + Q + O (the model's Bytes_min).
+    from tklab.kernels import gqa_decode as gd
+
+    qd = torch.randn(32, 32, 128, device=device, dtype=bf16, generator=g)
+    kd = torch.randn(32, 8, 8192, 128, device=device, dtype=bf16, generator=g)
+    vd = torch.randn_like(kd)
+    od = torch.empty_like(qd)
+    lsed = torch.empty(32, 32, device=device)
+    mem_row("tk_gqa_decode", "bf16 B32 Hq32 Hkv8 L8192 D128",
+            lambda i: (lambda: gd._launch(qd, kd, vd, None, od, lsed, scale=128 ** -0.5)),
+            2 * kd.numel() * 2 + 2 * qd.numel() * 2)
+    del qd, kd, vd, od, lsed
     # Config 4: GEMM.
     for dt_name, dt in (("float16", torch.float16), ("bfloat16", bf16)):
         for m, nn, k in ((8192, 8192, 8192), (4096, 4096, 4096), (8191, 8192, 8192)):

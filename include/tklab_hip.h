@@ -211,6 +211,26 @@ int tk_layernorm_bwd_stage1(int dtype, void* dx, const void* dy, float* partial_
 int tk_layernorm_bwd_stage2(int dtype, const float* partial_dw, const float* partial_db, void* dw,
                             void* db, int64_t group_count, int64_t cols, void* stream);
 
+/* Grouped-query attention decode: for each (batch b, query head h) one query row
+ * q[b][h] attends to the first clamp(seqlens[b], 0, max_len) keys of KV head
+ * h / (q_heads / kv_heads) (all max_len when `seqlens` is NULL); o[b][h] in the
+ * storage dtype, `lse` (nullable) float32 [batch][q_heads], base 2.
+ * No reference kernel exists: the workload and head mapping are the reference's
+ * decode model (docs/research/gqa_decode_model.md, "Canonical decode workload",
+ * "Semantic GQA mapping"); the arithmetic is its attention forward for one query
+ * row (src/tklab/kernels/flash_attention.py:90-117, 248-264).
+ * Strides in elements: q_strides/o_strides {batch, head}, k/v_strides {batch,
+ * head, position}; the head dimension is unit-stride; bases 16-byte aligned and
+ * strides multiples of 8. dtype F16 or BF16; head_dim 64 or 128; q_heads /
+ * kv_heads in {1, 2, 4, 8}. `partials` is float32 workspace of
+ * batch * q_heads * ceil(max_len / split_len) * (head_dim + 4) elements;
+ * split_len (keys per split-kernel wave) is a positive multiple of 64. */
+int tk_gqa_decode(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+                  float* partials, const int32_t* seqlens, int64_t batch, int64_t q_heads,
+                  int64_t kv_heads, int64_t max_len, int64_t head_dim, int64_t split_len,
+                  const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                  const int64_t* o_strides, float scale, void* stream);
+
 /* ---- Calibration kernels (no counterpart in the reference). They measure the
  * roofs this GPU sustains, so that the kernels above can be priced against
  * measured ceilings beside the published peaks. */

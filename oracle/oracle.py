@@ -45,6 +45,10 @@ def _load() -> ctypes.CDLL:
             "or_rope_bwd": [_F, _F, _F, _F, _F, _F, _F, _I, _I, ctypes.c_int],
             "or_gemm": [_F, _F, _F, _I, _I, _I, ctypes.c_int],
             "or_attn_fwd": [_F, _F, _F, _F, _F, _I, _I, _I, ctypes.c_float, ctypes.c_int, ctypes.c_int],
+            "or_gqa_decode": [
+                _F, _F, _F, ctypes.c_void_p, _F, _F, _I, _I, _I, _I, _I, ctypes.c_float,
+                ctypes.c_int,
+            ],
             "or_attn_bwd": [
                 _F, _F, _F, _F, _F, _F, _F, _F, _F, _F, _I, _I, _I, ctypes.c_float, ctypes.c_int,
                 ctypes.c_int,
@@ -199,6 +203,29 @@ def attn_fwd(
         _p(q), _p(k), _p(v), _p(o), _p(lse), heads, seq, d, scale, int(causal), _dt(dtype)
     )
     return o.reshape(shape), lse.reshape(shape[:-1])
+
+
+def gqa_decode(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    scale: float,
+    dtype: str,
+    lens: np.ndarray | None = None,
+) -> tuple[np.ndarray, np.ndarray]:
+    """Return ``(o, lse)`` for q ``[B, Hq, d]`` and k, v ``[B, Hkv, L, d]``; lse base 2."""
+    q, k, v = (_f32(t) for t in (q, k, v))
+    batch, q_heads, d = q.shape
+    _, kv_heads, length, _ = k.shape
+    o = np.empty_like(q)
+    lse = np.empty((batch, q_heads), dtype=np.float32)
+    lens_arr = None if lens is None else np.ascontiguousarray(lens, dtype=np.int32)
+    lens_p = None if lens_arr is None else lens_arr.ctypes.data_as(ctypes.c_void_p)
+    _load().or_gqa_decode(
+        _p(q), _p(k), _p(v), lens_p, _p(o), _p(lse), batch, q_heads, kv_heads, length, d,
+        scale, _dt(dtype),
+    )
+    return o, lse
 
 
 def attn_bwd(

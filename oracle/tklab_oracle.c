@@ -19,7 +19,9 @@
  * Pinning: tests/test_oracle.py checks every function here against PyTorch
  * library routines (softmax, F.rms_norm, F.silu, matmul, SDPA, autograd) and
  * closed forms (constant rows, identity matrices, norm preservation, the
- * inverse-rotation identity, single-key attention, the base-2 LSE closed form).
+ * inverse-rotation identity, single-key attention, the base-2 LSE closed form);
+ * or_gqa_decode reduces to the last row of causal or_attn_fwd, to repeated KV
+ * heads and to truncated caches, and matches PyTorch's SDPA.
  */
 #include <math.h>
 #include <stdint.h>
@@ -274,6 +276,58 @@ void or_attn_fwd(const float* q, const float* k, const float* v, float* o, float
       float* oi = o + (h * seq + i) * d;
       for (int64_t t = 0; t < d; ++t) oi[t] = or_round((float)(acc[t] / l), dt);
       if (lse) lse[h * seq + i] = m + log2f((float)l);
+    }
+  }
+}
+
+/* Grouped-query attention decode: for each (batch b, query head h) one query
+ * row q[b][h] attends to the first n_b = clamp(lens[b], 0, L) rows of the KV
+ * head kv = h / (q_heads / kv_heads) (docs/research/gqa_decode_model.md,
+ * "Semantic GQA mapping"), with exactly the arithmetic of or_attn_fwd for one
+ * row (flash_attention.py:90-117, 248-264). n_b = 0 gives o = 0, lse = -inf.
+ * q, o: [batch][q_heads][d]; k, v: [batch][kv_heads][L][d]; lens may be NULL
+ * (n_b = L); lse: [batch][q_heads] (may be NULL). */
+void or_gqa_decode(const float* q, const float* k, const float* v, const int32_t* lens, float* o,
+                   float* lse, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t len,
+                   int64_t d, float scale, int dt) {
+  const float scale_log2 = (float)(scale * kLog2e);
+  const int64_t group = q_heads / kv_heads;
+#pragma omp parallel for collapse(2) schedule(dynamic, 4)
+  for (int64_t b = 0; b < batch; ++b) {
+    for (int64_t h = 0; h < q_heads; ++h) {
+      int64_t nk = lens ? lens[b] : len;
+      if (nk < 0) nk = 0;
+      if (nk > len) nk = len;
+      const float* qi = q + (b * q_heads + h) * d;
+      const float* kh = k + (b * kv_heads + h / group) * len * d;
+      const float* vh = v + (b * kv_heads + h / group) * len * d;
+      float* oi = o + (b * q_heads + h) * d;
+      if (nk == 0) {
+        for (int64_t t = 0; t < d; ++t) oi[t] = 0.0f;
+        if (lse) lse[b * q_heads + h] = -INFINITY;
+        continue;
+      }
+      float* s = (float*)malloc(sizeof(float) * (size_t)nk);
+      double* acc = (double*)malloc(sizeof(double) * (size_t)d);
+      float m = -INFINITY;
+      for (int64_t j = 0; j < nk; ++j) {
+        double dot = 0.0;
+        for (int64_t t = 0; t < d; ++t) dot += (double)qi[t] * kh[j * d + t];
+        s[j] = (float)dot * scale_log2;
+        m = fmaxf(m, s[j]);
+      }
+      double l = 0.0;
+      for (int64_t t = 0; t < d; ++t) acc[t] = 0.0;
+      for (int64_t j = 0; j < nk; ++j) {
+        const float p = exp2f(s[j] - m);
+        l += p;
+        const double pr = or_round(p, dt);
+        for (int64_t t = 0; t < d; ++t) acc[t] += pr * vh[j * d + t];
+      }
+      for (int64_t t = 0; t < d; ++t) oi[t] = or_round((float)(acc[t] / l), dt);
+      if (lse) lse[b * q_heads + h] = m + log2f((float)l);
+      free(s);
+      free(acc);
     }
   }
 }

@@ -243,3 +243,52 @@ def test_attention_bf16_operand_rounding_stays_within_the_dtype_bound() -> None:
     o, _ = oracle.attn_fwd(q, k, v, 32 ** -0.5, False, "bfloat16")
     ref = F.scaled_dot_product_attention(_t(q), _t(k), _t(v))
     assert np.max(np.abs(o - ref.numpy())) < 2e-2
+
+
+# ---------------------------------------------------------------- GQA decode
+
+
+def test_gqa_decode_is_the_last_row_of_causal_attention() -> None:
+    """G = 1, full length: one decode row is row L-1 of causal attention (same loops)."""
+    q_full, k, v = (_rand(2, 3, 37, 32, seed=s) for s in (41, 42, 43))
+    for dt in ("float32", "bfloat16"):
+        o_full, lse_full = oracle.attn_fwd(q_full, k, v, 32 ** -0.5, True, dt)
+        o, lse = oracle.gqa_decode(q_full[:, :, -1], k, v, 32 ** -0.5, dt)
+        np.testing.assert_array_equal(o, o_full[:, :, -1])
+        np.testing.assert_array_equal(lse, lse_full[:, :, -1])
+
+
+def test_gqa_decode_equals_repeated_kv_heads_and_truncated_caches() -> None:
+    q = _rand(3, 8, 64, seed=44)
+    k, v = _rand(3, 2, 50, 64, seed=45), _rand(3, 2, 50, 64, seed=46)
+    lens = np.array([50, 17, 1], dtype=np.int32)
+    o, lse = oracle.gqa_decode(q, k, v, 0.125, "bfloat16", lens)
+    # kv_head(h) = h // 4: repeating each KV head 4 times makes it plain multi-head.
+    o_rep, lse_rep = oracle.gqa_decode(
+        q, np.repeat(k, 4, axis=1), np.repeat(v, 4, axis=1), 0.125, "bfloat16", lens
+    )
+    np.testing.assert_array_equal(o, o_rep)
+    np.testing.assert_array_equal(lse, lse_rep)
+    for b, n in enumerate(lens):
+        o_b, lse_b = oracle.gqa_decode(
+            q[b : b + 1], np.ascontiguousarray(k[b : b + 1, :, :n]),
+            np.ascontiguousarray(v[b : b + 1, :, :n]), 0.125, "bfloat16",
+        )
+        np.testing.assert_array_equal(o[b], o_b[0])
+        np.testing.assert_array_equal(lse[b], lse_b[0])
+    o0, lse0 = oracle.gqa_decode(q, k, v, 0.125, "float32", np.array([0, 5, 99], dtype=np.int32))
+    assert np.all(o0[0] == 0) and np.all(np.isneginf(lse0[0]))
+    np.testing.assert_array_equal(
+        o0[2], oracle.gqa_decode(q, k, v, 0.125, "float32")[0][2]
+    )  # lengths above L read the whole cache
+
+
+def test_gqa_decode_matches_sdpa_with_grouped_heads() -> None:
+    q = _rand(2, 8, 1, 32, seed=47)
+    k, v = _rand(2, 2, 40, 32, seed=48), _rand(2, 2, 40, 32, seed=49)
+    o, lse = oracle.gqa_decode(q[:, :, 0], k, v, 32 ** -0.5, "float32")
+    ref = F.scaled_dot_product_attention(_t(q), _t(k), _t(v), enable_gqa=True)
+    _close(o, ref[:, :, 0].numpy(), rtol=1e-5, atol=1e-6)
+    scores = _t(q) @ _t(np.repeat(k, 4, axis=1)).transpose(-2, -1) * 32 ** -0.5
+    _close(lse, (torch.logsumexp(scores, -1)[:, :, 0] * math.log2(math.e)).numpy(), rtol=1e-6,
+           atol=1e-6)

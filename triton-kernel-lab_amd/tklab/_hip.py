@@ -63,6 +63,10 @@ _SIGNATURES: dict[str, list[object]] = {
         _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P,
     ],
     "tk_layernorm_bwd_stage2": [_I32, _P, _P, _P, _P, _I64, _I64, _P],
+    "tk_gqa_decode": [
+        _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _I64P,
+        _I64P, _F32, _P,
+    ],
     "tk_roof_copy": [_P, _P, _I64, _P],
     "tk_roof_mfma": [_I32, _P, _I64, _I64, _P],
 }
