@@ -223,3 +223,28 @@ def test_attention_contract(shape, dtype, fragment) -> None:
     q = torch.zeros(shape, dtype=dtype, device="meta")
     with pytest.raises(ValueError, match=fragment):
         attention_noncausal(q, q, q)
+
+
+def test_gqa_decode_contract() -> None:
+    from tklab.kernels.gqa_decode import gqa_decode, split_length
+
+    q = torch.empty(2, 8, 128, device="meta", dtype=torch.bfloat16)
+    k = torch.empty(2, 2, 100, 128, device="meta", dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="expects q"):
+        gqa_decode(q[0], k, k)
+    with pytest.raises(ValueError, match="identical shapes"):
+        gqa_decode(q, k, k[:, :, :50])
+    with pytest.raises(ValueError, match="1, 2, 4 or 8 times"):
+        gqa_decode(torch.empty(2, 6, 128, device="meta", dtype=torch.bfloat16), k, k)
+    with pytest.raises(ValueError, match="head_dim 64 and 128"):
+        q96 = torch.empty(2, 8, 96, device="meta", dtype=torch.bfloat16)
+        k96 = torch.empty(2, 2, 100, 96, device="meta", dtype=torch.bfloat16)
+        gqa_decode(q96, k96, k96)
+    with pytest.raises(ValueError, match="float16 or bfloat16"):
+        gqa_decode(q.float(), k.float(), k.float())
+    with pytest.raises(ValueError, match="requires CUDA"):
+        gqa_decode(q, k, k)
+    # Splits: multiples of 64 keys, about 1024 waves, never longer than the cache.
+    assert split_length(32, 8, 8192) == 2048
+    assert split_length(1, 1, 100) == 64
+    assert all(split_length(b, 8, n) % 64 == 0 for b in (1, 7, 64) for n in (1, 999, 70000))
