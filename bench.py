@@ -388,6 +388,29 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
             mfma_row("tk_gemm", f"{dt_name} {m}x{nn}x{k}", lambda: mm._launch_fp32acc((a, b), c),
                      2 * m * nn * k, dt_name)
             del a, b, c
+    # Config 3 fused into its producer: the gate/up GEMM with SwiGLU in the epilogue,
+    # x [16384, 4096] @ W_gate, W_up [4096, 14336] -> y [16384, 14336] (two GEMMs' FLOPs);
+    # `unfused_ms` is two tk_gemm launches plus tk_swiglu_fwd on the same operands.
+    from tklab.kernels import matmul_swiglu as mms
+    from tklab.kernels import swiglu as sgl
+
+    sc = 4096 ** -0.25
+    xm = (torch.randn(16384, 4096, device=device, generator=g) * sc).to(bf16)
+    wgm = (torch.randn(4096, 14336, device=device, generator=g) * sc).to(bf16)
+    wum = (torch.randn(4096, 14336, device=device, generator=g) * sc).to(bf16)
+    ym = torch.empty(16384, 14336, device=device, dtype=bf16)
+    gm, um = torch.empty_like(ym), torch.empty_like(ym)
+    mfma_row("tk_gemm_swiglu", "bf16 16384x14336x4096 (gate+up GEMMs, SwiGLU epilogue)",
+             lambda: mms._launch(xm, wgm, wum, ym), 2 * 2 * 16384 * 14336 * 4096, "bfloat16",
+             reps=5)
+
+    def unfused():
+        mm._launch_fp32acc((xm, wgm), gm)
+        mm._launch_fp32acc((xm, wum), um)
+        sgl._launch_forward(um, gm, ym)
+
+    rows[-1]["unfused_ms"] = round(timed(unfused, 5), 4)
+    del xm, wgm, wum, ym, gm, um
     # Config 5: attention.
     for causal, nctx, d in ((True, 8192, 128), (False, 4096, 128), (True, 8192, 64), (False, 4096, 64)):
         shape = (4, 32, nctx, d)

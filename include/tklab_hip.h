@@ -134,6 +134,22 @@ int tk_gemm(int dtype, const void* a, const void* b, void* c, int64_t m, int64_t
             int64_t stride_bn, int64_t stride_cm, int64_t stride_cn, int acc_fp16,
             void* stream);
 
+/* GEMM with the SwiGLU nonlinearity fused into its epilogue:
+ *   y = value * gate * sigmoid(gate), gate = a * b_gate, value = a * b_up,
+ * with a [m, k] and both weights [k, n]; gate and value are rounded to `dtype`
+ * before the nonlinearity, exactly as when two tk_gemm calls store them and
+ * tk_swiglu_fwd reads them back, so the result is bitwise that composition's while
+ * the two m x n intermediates never reach HBM. No reference kernel exists: the
+ * reference lists this fusion among its next steps around
+ * src/tklab/kernels/swiglu.py:28-59 and matmul.py:72-164. Needs unit inner
+ * strides, 16-byte aligned rows, k % 32 == 0, n % 8 == 0 and operand extents
+ * below 2 GiB (otherwise non-zero status: compose tk_gemm and tk_swiglu_fwd).
+ * dtype TK_DTYPE_F16 or TK_DTYPE_BF16. */
+int tk_gemm_swiglu(int dtype, const void* a, const void* b_gate, const void* b_up, void* y,
+                   int64_t m, int64_t n, int64_t k, int64_t stride_am, int64_t stride_ak,
+                   int64_t stride_gk, int64_t stride_gn, int64_t stride_uk, int64_t stride_un,
+                   int64_t stride_ym, int64_t stride_yn, void* stream);
+
 /* Flash attention forward over q/k/v/o[batch][heads][seq][head_dim]
  * (head_dim unit-stride; strides given for batch, head and seq), head_dim in
  * {64, 128}, dtype TK_DTYPE_F16 or TK_DTYPE_BF16. Online softmax in base 2

@@ -13,11 +13,7 @@ constexpr int kBlock = 256;
 
 enum Activation { kRelu = 0, kGelu = 1, kSilu = 2, kTanh = 3 };
 
-__device__ __forceinline__ float stable_sigmoid(float z) {
-  const float e = expf(-fabsf(z));
-  const float d = 1.0f + e;
-  return z >= 0.f ? 1.0f / d : e / d;
-}
+using tk::stable_sigmoid;
 
 template <int ACT>
 __device__ __forceinline__ float act_value(float x) {

@@ -20,13 +20,7 @@ namespace {
 
 constexpr int kBlock = 256;
 
-// sigmoid from exp(-|z|), branch-stable for any z
-// (src/tklab/kernels/_elementwise_math.py:12-18).
-__device__ __forceinline__ float stable_sigmoid(float z) {
-  const float e = expf(-fabsf(z));
-  const float d = 1.0f + e;
-  return z >= 0.f ? 1.0f / d : e / d;
-}
+using tk::stable_sigmoid;
 
 constexpr int kUnroll = 4;
 constexpr int64_t kMaxBlocks = 8192;  // 32 workgroups per CU; the loop covers the rest

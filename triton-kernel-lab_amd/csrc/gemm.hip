@@ -296,3 +296,27 @@ extern "C" int tk_gemm(int dtype, const void* a, const void* b, void* c, int64_t
   }
   return tk::check_launch("gemm");
 }
+
+extern "C" int tk_gemm_swiglu(int dtype, const void* a, const void* b_gate, const void* b_up,
+                              void* y, int64_t m, int64_t n, int64_t k, int64_t stride_am,
+                              int64_t stride_ak, int64_t stride_gk, int64_t stride_gn,
+                              int64_t stride_uk, int64_t stride_un, int64_t stride_ym,
+                              int64_t stride_yn, void* stream) {
+  if (dtype != TK_DTYPE_F16 && dtype != TK_DTYPE_BF16)
+    return tk::fail("gemm_swiglu: dtype must be float16 or bfloat16");
+  if (a == nullptr || b_gate == nullptr || b_up == nullptr || y == nullptr)
+    return tk::fail("gemm_swiglu: null pointer");
+  if (m <= 0 || n <= 0 || k <= 0) return tk::fail("gemm_swiglu: empty problem");
+  if (stride_ym <= 0 || stride_yn <= 0) return tk::fail("gemm_swiglu: strides must be positive");
+  const int64_t lim = INT32_MAX;
+  if (m > lim || n > lim || k > lim || (m - 1) * stride_ym + (n - 1) * stride_yn > lim)
+    return tk::fail("gemm_swiglu: operand exceeds the int32 offset range");
+  if (!tk::gemm_dma_applies(a, b_gate, m, n, k, stride_am, stride_ak, stride_gk, stride_gn) ||
+      !tk::gemm_dma_applies(a, b_up, m, n, k, stride_am, stride_ak, stride_uk, stride_un))
+    return tk::fail("gemm_swiglu: needs unit inner strides, 16-byte aligned rows, k %% 32 == 0, "
+                    "n %% 8 == 0 and operands below 2 GiB");
+  if (tk::cdiv(m, BM) * tk::cdiv(n, 128) > INT32_MAX) return tk::fail("gemm_swiglu: too many tiles");
+  tk::gemm_swiglu_dma_launch(dtype, a, b_gate, b_up, y, m, n, k, stride_am, stride_gk, stride_uk,
+                             stride_ym, stride_yn, tk::as_stream(stream));
+  return tk::check_launch("gemm_swiglu");
+}

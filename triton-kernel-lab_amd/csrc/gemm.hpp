@@ -16,4 +16,11 @@ void gemm_dma_launch(int dtype, const void* a, const void* b, void* c, int64_t m
                      int64_t k, int64_t stride_am, int64_t stride_bk, int64_t stride_cm,
                      int64_t stride_cn, hipStream_t stream);
 
+// Enqueues the SwiGLU-fused DMA kernel: y = swiglu(value = a * b_up, gate = a * b_gate),
+// both weights [K, N] row-major; each must satisfy gemm_dma_applies with `a`.
+void gemm_swiglu_dma_launch(int dtype, const void* a, const void* b_gate, const void* b_up,
+                            void* y, int64_t m, int64_t n, int64_t k, int64_t stride_am,
+                            int64_t stride_gk, int64_t stride_uk, int64_t stride_ym,
+                            int64_t stride_yn, hipStream_t stream);
+
 }  // namespace tk

@@ -30,8 +30,23 @@
 //
 // Tile order: workgroup w runs on XCD w % 8; tiles are renumbered so each XCD walks a
 // contiguous range in groups of 4 M-tiles, sharing A and B panels in that XCD's L2.
+//
+// SwiGLU variant (kSwiGLU): Y = swiglu(value = A*B_up, gate = A*B_gate) for two weights
+// [K, N]. A block computes 256 x 128 of Y from a 256-column B tile holding the gate
+// columns n0..n0+127 then the same up columns, laid out in LDS as two 128-column blocks
+// (256-byte k-rows, 32-byte granule g of k-row k at g ^ (2 * (k & 3)): still 64 distinct
+// banks per read phase), so every B DMA instruction reads one weight. Wave (wm, wq)
+// takes gate columns 32wq.. as its N tile 0 and the same up columns as N tile 1, and
+// the epilogue rounds both to the storage type (as the unfused GEMMs store them) and
+// writes value * gate * sigmoid(gate): the two M x N intermediates never reach HBM and
+// the result is bitwise that of the two GEMMs followed by the SwiGLU kernel.
 #include "gemm.hpp"
 #include "tk_common.hpp"
+
+// No floating-point contraction in this file: the SwiGLU epilogue must round
+// value * gate * sigmoid(gate) to float32 and then to the storage type, as the SwiGLU
+// kernel and the reference do (a fused multiply-convert would round once).
+#pragma clang fp contract(off)
 
 namespace {
 
@@ -71,10 +86,10 @@ struct Mfma<__bf16> {
 
 struct Problem {
   int m, n, k;
-  int lda, ldb;
+  int lda, ldb, ldb2;  // ldb2: the up weight's k stride (SwiGLU variant)
   int64_t scm, scn;
   int tiles_m, tiles_n;
-  uint32_t a_bytes, b_bytes;
+  uint32_t a_bytes, b_bytes, b2_bytes;
 };
 
 template <int N>
@@ -116,11 +131,12 @@ __device__ __forceinline__ i32x4 read_a(int i, uint32_t addr) {
   }
 }
 
-// B fragment for k half KK (16 k-rows = 8 KiB): k-rows +0..3 and +4..7 of this lane group.
-template <int KK>
+// B fragment for k half KK (16 k-rows of ROWB bytes): k-rows +0..3 and +4..7 of this
+// lane group.
+template <int KK, int ROWB>
 __device__ __forceinline__ i32x4 read_b(uint32_t addr) {
-  const i32x2 lo = lds_read_tr16<kOperandBytes + KK * 8192>(addr);
-  const i32x2 hi = lds_read_tr16<kOperandBytes + KK * 8192 + 2048>(addr);
+  const i32x2 lo = lds_read_tr16<kOperandBytes + KK * 16 * ROWB>(addr);
+  const i32x2 hi = lds_read_tr16<kOperandBytes + KK * 16 * ROWB + 4 * ROWB>(addr);
   return i32x4{lo[0], lo[1], hi[0], hi[1]};
 }
 
@@ -136,22 +152,33 @@ __device__ __forceinline__ void wait_lgkm(Frags& f) {
                  "+v"(f.b[1]));
 }
 
+// Y = value * gate * sigmoid(gate) on values already rounded to T, in the SwiGLU
+// kernel's operation order (contraction off: each product rounded separately).
 template <typename T>
+__device__ __forceinline__ T swiglu_out(float gate_acc, float up_acc) {
+  const float g = tk::round_to<T>(gate_acc);
+  const float v = tk::round_to<T>(up_acc);
+  return tk::from_f32<T>(v * g * tk::stable_sigmoid(g));
+}
+
+template <typename T, bool kSwiGLU>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(2, 2))) void
-gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restrict__ C,
-                Problem p) {
+gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ B2,
+                T* __restrict__ C, Problem p) {
+  constexpr int kTileN = kSwiGLU ? 128 : BN;  // output columns per block
+  constexpr int kRowB = kSwiGLU ? 256 : 512;  // bytes per B k-row in LDS
   __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
 
   const int total = p.tiles_m * p.tiles_n;
   int w = blockIdx.x;
   if (total % kXcds == 0) w = (w % kXcds) * (total / kXcds) + w / kXcds;
-  const int per_group = kGroupM * p.tiles_n;
+  const int per_group = kGroupM * p.tiles_n;  // p.tiles_n counts kTileN-column tiles
   const int first_m = (w / per_group) * kGroupM;
   const int group_m = min(p.tiles_m - first_m, kGroupM);
   const int tile_m = first_m + (w % per_group) % group_m;
   const int tile_n = (w % per_group) / group_m;
-  const int m0 = tile_m * BM, n0 = tile_n * BN;
+  const int m0 = tile_m * BM, n0 = tile_n * kTileN;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -160,8 +187,12 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restrict_
   const int lhalf = lane >> 5;
   const __amdgpu_buffer_rsrc_t ra =
       __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, p.a_bytes, 0x00020000);
+  // SwiGLU: waves 0-3 fill the gate block, waves 4-7 the up block.
+  const bool up_half = kSwiGLU && wave >= 4;
   const __amdgpu_buffer_rsrc_t rb =
-      __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, p.b_bytes, 0x00020000);
+      up_half ? __builtin_amdgcn_make_buffer_rsrc((void*)B2, (short)0, p.b2_bytes, 0x00020000)
+              : __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, p.b_bytes, 0x00020000);
+  const int ldb = up_half ? p.ldb2 : p.ldb;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
 
   // DMA sources for K tile 0 (bytes). Wave w fills A rows 32w .. 32w+31 (2 loads of 16
@@ -173,12 +204,21 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restrict_
     const int r = (wave * 2 + i) * 16 + (lane >> 2);
     const int c = (lane & 3) ^ ((r >> 2) & 3);
     a_src[i] = (m0 + r < p.m) ? uint32_t((m0 + r) * p.lda + c * 8) * 2u : kOob;
-    const int kr = (wave * 2 + i) * 2 + (lane >> 5);
-    const int slot = lane & 31;
-    const int chunk = (((slot >> 1) ^ (2 * (kr & 3))) << 1) | (slot & 1);
-    b_src[i] = (n0 + chunk * 8 < p.n) ? uint32_t(kr * p.ldb + n0 + chunk * 8) * 2u : kOob;
+    if constexpr (kSwiGLU) {
+      // Load L = 2*wave + i: block L / 8 (gate, up), k-rows 4*(L % 8) .. +3 of 256 B.
+      const int L = wave * 2 + i;
+      const int kr = 4 * (L & 7) + (lane >> 4);
+      const int slot = lane & 15;
+      const int chunk = (((slot >> 1) ^ (2 * (kr & 3))) << 1) | (slot & 1);
+      b_src[i] = (n0 + chunk * 8 < p.n) ? uint32_t(kr * ldb + n0 + chunk * 8) * 2u : kOob;
+    } else {
+      const int kr = (wave * 2 + i) * 2 + (lane >> 5);
+      const int slot = lane & 31;
+      const int chunk = (((slot >> 1) ^ (2 * (kr & 3))) << 1) | (slot & 1);
+      b_src[i] = (n0 + chunk * 8 < p.n) ? uint32_t(kr * ldb + n0 + chunk * 8) * 2u : kOob;
+    }
   }
-  const uint32_t b_tile_bytes = uint32_t(BK * p.ldb) * 2u;
+  const uint32_t b_tile_bytes = uint32_t(BK * ldb) * 2u;
   const int kt = p.k / BK;
 
   // DMA x (0..3: two A loads, two B loads) of K tile `tile` into ring slot `slot`. Tiles past the end reload the
@@ -206,8 +246,15 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restrict_
     const int g = lane >> 4, jj = (lane & 15) >> 2, q = lane & 3;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int n = wn + j * 32 + (g & 1) * 16 + 4 * q;
-      b_addr[j] = (((g >> 1) * 8 + jj) * 256 + (((n >> 4) ^ (2 * jj)) * 16) + (n & 15)) * 2;
+      if constexpr (kSwiGLU) {
+        // N tile j is block j (gate, up), columns 32 * (wave & 3) ..
+        const int n = (wave & 3) * 32 + (g & 1) * 16 + 4 * q;
+        b_addr[j] = j * 8192 +
+                    (((g >> 1) * 8 + jj) * 128 + (((n >> 4) ^ (2 * jj)) * 16) + (n & 15)) * 2;
+      } else {
+        const int n = wn + j * 32 + (g & 1) * 16 + 4 * q;
+        b_addr[j] = (((g >> 1) * 8 + jj) * 256 + (((n >> 4) ^ (2 * jj)) * 16) + (n & 15)) * 2;
+      }
     }
   }
 
@@ -230,7 +277,7 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restrict_
 #pragma unroll
   for (int i = 0; i < 4; ++i) f0.a[i] = read_a(i, lds_base + a_addr[0]);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) f0.b[j] = read_b<0>(lds_base + b_addr[j]);
+  for (int j = 0; j < 2; ++j) f0.b[j] = read_b<0, kRowB>(lds_base + b_addr[j]);
 
   int stage = 0, fill = kAhead;
   for (int t = 0; t < kt; ++t) {
@@ -248,8 +295,8 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restrict_
       if (x < 4) {
         f1.a[x] = read_a(x, base + a_addr[1]);
       } else if (x < 6) {
-        if (x == 4) f1.b[0] = read_b<1>(base + b_addr[0]);
-        else f1.b[1] = read_b<1>(base + b_addr[1]);
+        if (x == 4) f1.b[0] = read_b<1, kRowB>(base + b_addr[0]);
+        else f1.b[1] = read_b<1, kRowB>(base + b_addr[1]);
       }
       if (x >= 4) dma(x - 4, t + kAhead, fill);
       sched_fence();
@@ -270,8 +317,8 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restrict_
       if (x < 4) {
         f0.a[x] = read_a(x, next_base + a_addr[0]);
       } else if (x < 6) {
-        if (x == 4) f0.b[0] = read_b<0>(next_base + b_addr[0]);
-        else f0.b[1] = read_b<0>(next_base + b_addr[1]);
+        if (x == 4) f0.b[0] = read_b<0, kRowB>(next_base + b_addr[0]);
+        else f0.b[1] = read_b<0, kRowB>(next_base + b_addr[1]);
       }
       sched_fence();
     }
@@ -282,16 +329,30 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, T* __restrict_
   wait_vmcnt<0>();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
+  if constexpr (kSwiGLU) {
+    const int n = n0 + (wave & 3) * 32 + lrow;
+    if (n < p.n) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + wn + j * 32 + lrow;
-      if (n >= p.n) continue;
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+          if (m < p.m) C[m * p.scm + n * p.scn] = swiglu_out<T>(acc[i][0][r], acc[i][1][r]);
+        }
+      }
+    }
+  } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-        if (m < p.m) C[m * p.scm + n * p.scn] = tk::from_f32<T>(acc[i][j][r]);
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn + j * 32 + lrow;
+        if (n >= p.n) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+          if (m < p.m) C[m * p.scm + n * p.scn] = tk::from_f32<T>(acc[i][j][r]);
+        }
       }
     }
   }
@@ -315,26 +376,57 @@ bool gemm_dma_applies(const void* a, const void* b, int64_t m, int64_t n, int64_
 void gemm_dma_launch(int dtype, const void* a, const void* b, void* c, int64_t m, int64_t n,
                      int64_t k, int64_t stride_am, int64_t stride_bk, int64_t stride_cm,
                      int64_t stride_cn, hipStream_t stream) {
+  const uint32_t b_bytes = (uint32_t)(((k - 1) * stride_bk + n) * 2);
   Problem p{(int)m,
             (int)n,
             (int)k,
             (int)stride_am,
+            (int)stride_bk,
             (int)stride_bk,
             stride_cm,
             stride_cn,
             (int)cdiv(m, BM),
             (int)cdiv(n, BN),
             (uint32_t)(((m - 1) * stride_am + k) * 2),
-            (uint32_t)(((k - 1) * stride_bk + n) * 2)};
+            b_bytes,
+            b_bytes};
   const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
   if (dtype == TK_DTYPE_F16)
-    hipLaunchKernelGGL((gemm_dma_kernel<_Float16>), grid, dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL((gemm_dma_kernel<_Float16, false>), grid, dim3(kThreads), 0, stream,
                        static_cast<const _Float16*>(a), static_cast<const _Float16*>(b),
-                       static_cast<_Float16*>(c), p);
+                       static_cast<const _Float16*>(b), static_cast<_Float16*>(c), p);
   else
-    hipLaunchKernelGGL((gemm_dma_kernel<__bf16>), grid, dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL((gemm_dma_kernel<__bf16, false>), grid, dim3(kThreads), 0, stream,
                        static_cast<const __bf16*>(a), static_cast<const __bf16*>(b),
-                       static_cast<__bf16*>(c), p);
+                       static_cast<const __bf16*>(b), static_cast<__bf16*>(c), p);
+}
+
+void gemm_swiglu_dma_launch(int dtype, const void* a, const void* b_gate, const void* b_up,
+                            void* y, int64_t m, int64_t n, int64_t k, int64_t stride_am,
+                            int64_t stride_gk, int64_t stride_uk, int64_t stride_ym,
+                            int64_t stride_yn, hipStream_t stream) {
+  Problem p{(int)m,
+            (int)n,
+            (int)k,
+            (int)stride_am,
+            (int)stride_gk,
+            (int)stride_uk,
+            stride_ym,
+            stride_yn,
+            (int)cdiv(m, BM),
+            (int)cdiv(n, 128),
+            (uint32_t)(((m - 1) * stride_am + k) * 2),
+            (uint32_t)(((k - 1) * stride_gk + n) * 2),
+            (uint32_t)(((k - 1) * stride_uk + n) * 2)};
+  const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
+  if (dtype == TK_DTYPE_F16)
+    hipLaunchKernelGGL((gemm_dma_kernel<_Float16, true>), grid, dim3(kThreads), 0, stream,
+                       static_cast<const _Float16*>(a), static_cast<const _Float16*>(b_gate),
+                       static_cast<const _Float16*>(b_up), static_cast<_Float16*>(y), p);
+  else
+    hipLaunchKernelGGL((gemm_dma_kernel<__bf16, true>), grid, dim3(kThreads), 0, stream,
+                       static_cast<const __bf16*>(a), static_cast<const __bf16*>(b_gate),
+                       static_cast<const __bf16*>(b_up), static_cast<__bf16*>(y), p);
 }
 
 }  // namespace tk

@@ -68,8 +68,8 @@ __device__ __forceinline__ int pack2(float lo, float hi) {
     const uint32_t b = __builtin_bit_cast(uint16_t, static_cast<__bf16>(hi));
     return static_cast<int>(a | (b << 16));
   } else {
-    const uint32_t a = __builtin_bit_cast(uint16_t, static_cast<_Float16>(lo));
-    const uint32_t b = __builtin_bit_cast(uint16_t, static_cast<_Float16>(hi));
+    const uint32_t a = __builtin_bit_cast(uint16_t, tk::from_f32<_Float16>(lo));
+    const uint32_t b = __builtin_bit_cast(uint16_t, tk::from_f32<_Float16>(hi));
     return static_cast<int>(a | (b << 16));
   }
 }
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(kCombineThreads) void gqa_decode_combine_kernel(
       a += acc_s[r][t];
       ls += sum_s[r];
     }
-    o[b * s.ob + h * s.oh + t] = static_cast<T>(ls > 0.f ? a / ls : 0.f);
+    o[b * s.ob + h * s.oh + t] = tk::from_f32<T>(ls > 0.f ? a / ls : 0.f);
     if (lse != nullptr && t == 0)
       lse[static_cast<int64_t>(b) * s.q_heads + h] = ls > 0.f ? mx + log2f(ls) : -INFINITY;
   }

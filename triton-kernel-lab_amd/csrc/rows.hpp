@@ -112,7 +112,7 @@ __device__ __forceinline__ uint32_t f32_to_bits(float f) {
   if constexpr (sizeof(T) == 4) {
     return __float_as_uint(f);
   } else {
-    return __builtin_bit_cast(uint16_t, static_cast<T>(f));
+    return __builtin_bit_cast(uint16_t, from_f32<T>(f));
   }
 }
 

@@ -41,9 +41,28 @@ __device__ __forceinline__ float to_f32(__bf16 v) { return static_cast<float>(v)
 template <typename T>
 __device__ __forceinline__ T from_f32(float v) { return static_cast<T>(v); }
 
+// float16 results are rounded to float32 first, as the reference computes in float32
+// and then casts. Without the opaque step the backend folds a preceding float32
+// multiply into the conversion (v_fma_mixlo_f16 rounds the exact product once), which
+// differs from float32-then-float16 rounding when the float32 product is a float16 tie.
+template <>
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float v) {
+  asm("" : "+v"(v));
+  return static_cast<_Float16>(v);
+}
+
 // Round a float32 value to T and back (T = float is the identity).
 template <typename T>
 __device__ __forceinline__ float round_to(float v) { return to_f32(from_f32<T>(v)); }
+
+// sigmoid from exp(-|z|), branch-stable for any z
+// (src/tklab/kernels/_elementwise_math.py:12-18). Shared by the SwiGLU kernels and
+// the fused GEMM + SwiGLU epilogue so both evaluate it with the same instructions.
+__device__ __forceinline__ float stable_sigmoid(float z) {
+  const float e = expf(-fabsf(z));
+  const float d = 1.0f + e;
+  return z >= 0.f ? 1.0f / d : e / d;
+}
 
 // ---------------------------------------------------------------- vector IO
 
