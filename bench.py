@@ -429,6 +429,21 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
                                                   causal=causal),
                  int(2.5 * flops), "bfloat16", reps=5)
         del qq, kk, vv, do, o, lse, delta, gq, gk, gv
+    # Grouped-query attention at the causal config with 8 KV heads (4 query heads each).
+    shape, kv_shape = (4, 32, 8192, 128), (4, 8, 8192, 128)
+    qq, do = (torch.randn(shape, device=device, dtype=bf16, generator=g) for _ in range(2))
+    kk, vv = (torch.randn(kv_shape, device=device, dtype=bf16, generator=g) for _ in range(2))
+    o = torch.empty_like(qq)
+    lse = torch.empty(shape[:-1], device=device, dtype=torch.float32)
+    flops = fa.attention_flops(4, 32, 8192, 128, causal=True)
+    tag = "bf16 B4 H32 Hkv8 N8192 D128 causal"
+    mfma_row("tk_attn_fwd_gqa", tag,
+             lambda: fa._launch_gqa_forward(qq, kk, vv, o, lse, causal=True), flops, "bfloat16",
+             reps=5)
+    mfma_row("tk_attn_bwd_gqa (preprocess+dkdv+dq)", tag + ", 2.5x fwd FLOPs",
+             lambda: fa._launch_gqa_backward(qq, kk, vv, o, lse, do, causal=True),
+             int(2.5 * flops), "bfloat16", reps=5)
+    del qq, kk, vv, do, o, lse
     del flush
     torch.cuda.empty_cache()
     return rows

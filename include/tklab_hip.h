@@ -186,6 +186,32 @@ int tk_attn_bwd_dq(int dtype, const void* q, const void* k, const void* v, const
                    int64_t heads, int64_t seq, int64_t head_dim, const int64_t* strides,
                    float sm_scale, int causal, void* stream);
 
+/* Grouped-query attention (prefill / training): q, o, dO, dQ have `heads` heads, k, v,
+ * dK, dV have `kv_heads` (heads % kv_heads == 0) and query head h uses K/V head
+ * h / (heads / kv_heads). Same arithmetic as tk_attn_fwd / tk_attn_bwd_dkdv /
+ * tk_attn_bwd_dq (which are the kv_heads == heads case); delta comes from
+ * tk_attn_bwd_preprocess with the query-side strides. dK and dV sum a KV head's query
+ * heads in a fixed order (deterministic). Strides: q_strides {batch, head, seq} of the
+ * query side, kv_strides of the KV side. Needs each head's rows below 2 GiB.
+ * No reference kernel exists: the reference lists grouped-query attention among its
+ * next steps (README.md:509-514; docs/research/gqa_decode_model.md fixes the head
+ * mapping). */
+int tk_attn_fwd_gqa(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+                    int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
+                    int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
+                    const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
+                    int causal, void* stream);
+int tk_attn_bwd_dkdv_gqa(int dtype, const void* q, const void* k, const void* v,
+                         const void* dout, void* dk, void* dv, const float* lse,
+                         const float* delta, int64_t batch, int64_t heads, int64_t kv_heads,
+                         int64_t seq, int64_t head_dim, const int64_t* q_strides,
+                         const int64_t* kv_strides, float sm_scale, int causal, void* stream);
+int tk_attn_bwd_dq_gqa(int dtype, const void* q, const void* k, const void* v,
+                       const void* dout, void* dq, const float* lse, const float* delta,
+                       int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
+                       int64_t head_dim, const int64_t* q_strides, const int64_t* kv_strides,
+                       float sm_scale, int causal, void* stream);
+
 /* ---- Registry kernels outside the transformer hot path ---------------- */
 
 /* out[i*out_stride] = x[i*x_stride] + y[i*y_stride], i < n (strides may be 0).

@@ -743,8 +743,8 @@ extern "C" int tk_attn_fwd(int dtype, const void* q, const void* k, const void* 
   if (!tk::aligned16(q) || !tk::aligned16(k) || !tk::aligned16(v) || !tk::aligned16(o))
     return tk::fail("attn_fwd: tensors must be 16-byte aligned");
   if (tk::attn_fwd_dma_applies(seq, head_dim, k_strides, v_strides)) {
-    tk::attn_fwd_dma_launch(dtype, q, k, v, o, lse, batch, heads, seq, head_dim, q_strides,
-                            k_strides, v_strides, o_strides, sm_scale, causal != 0,
+    tk::attn_fwd_dma_launch(dtype, q, k, v, o, lse, batch, heads, heads, seq, head_dim,
+                            q_strides, k_strides, v_strides, o_strides, sm_scale, causal != 0,
                             tk::as_stream(stream));
     return tk::check_launch("attn_fwd");
   }
@@ -836,9 +836,10 @@ extern "C" int tk_attn_bwd_dkdv(int dtype, const void* q, const void* k, const v
   if (bwd_shape("attn_bwd_dkdv", dtype, ptrs, 8, batch, heads, seq, head_dim, strides, sm_scale,
                 128, &s))
     return 1;
-  if (tk::attn_bwd_dma_applies(seq, head_dim, strides)) {
-    tk::attn_bwd_dkdv_dma_launch(dtype, q, k, v, dout, dk, dv, lse, delta, batch, heads, seq,
-                                 head_dim, strides, sm_scale, causal != 0, tk::as_stream(stream));
+  if (tk::attn_bwd_dma_applies(seq, head_dim, strides, strides)) {
+    tk::attn_bwd_dkdv_dma_launch(dtype, q, k, v, dout, dk, dv, lse, delta, batch, heads, heads,
+                                 seq, head_dim, strides, strides, sm_scale, causal != 0,
+                                 tk::as_stream(stream));
     return tk::check_launch("attn_bwd_dkdv");
   }
   const dim3 grid(static_cast<unsigned>(s.tiles));
@@ -856,13 +857,100 @@ extern "C" int tk_attn_bwd_dq(int dtype, const void* q, const void* k, const voi
   if (bwd_shape("attn_bwd_dq", dtype, ptrs, 7, batch, heads, seq, head_dim, strides, sm_scale, 128,
                 &s))
     return 1;
-  if (tk::attn_bwd_dma_applies(seq, head_dim, strides)) {
-    tk::attn_bwd_dq_dma_launch(dtype, q, k, v, dout, dq, lse, delta, batch, heads, seq, head_dim,
-                               strides, sm_scale, causal != 0, tk::as_stream(stream));
+  if (tk::attn_bwd_dma_applies(seq, head_dim, strides, strides)) {
+    tk::attn_bwd_dq_dma_launch(dtype, q, k, v, dout, dq, lse, delta, batch, heads, heads, seq,
+                               head_dim, strides, strides, sm_scale, causal != 0,
+                               tk::as_stream(stream));
     return tk::check_launch("attn_bwd_dq");
   }
   const dim3 grid(static_cast<unsigned>(s.tiles));
   TK_ATTN_DISPATCH(dtype, head_dim, causal, attn_bwd_dq_kernel, grid, (const T*)q, (const T*)k,
                    (const T*)v, (const T*)dout, (T*)dq, lse, delta, s);
   return tk::check_launch("attn_bwd_dq");
+}
+
+// ---------------------------------------------------------------- grouped-query attention
+//
+// Query head h attends with K/V head h / (heads / kv_heads). Same kernels as the
+// multi-head entry points (which are the kv_heads == heads case); the dK/dV pass sums a
+// KV head's query heads in a fixed order, so the backward stays deterministic. Needs the
+// buffer->LDS kernels (each head's rows below 2 GiB).
+
+namespace {
+int gqa_check(const char* what, int dtype, const void* const* ptrs, int nptr, int64_t batch,
+              int64_t heads, int64_t kv_heads, int64_t seq, int64_t head_dim,
+              const int64_t* const* strides, const bool* kv_side, int nstr) {
+  if (check_common(what, dtype, batch, heads, seq, head_dim)) return 1;
+  if (kv_heads <= 0 || heads % kv_heads != 0)
+    return tk::fail("%s: heads must be a positive multiple of kv_heads", what);
+  for (int i = 0; i < nptr; ++i) {
+    if (!ptrs[i]) return tk::fail("%s: null pointer", what);
+    if (!tk::aligned16(ptrs[i])) return tk::fail("%s: tensors must be 16-byte aligned", what);
+  }
+  for (int i = 0; i < nstr; ++i) {
+    if (!strides[i]) return tk::fail("%s: null pointer", what);
+    if (!strides_ok(strides[i], batch, kv_side[i] ? kv_heads : heads, seq, head_dim))
+      return tk::fail("%s: strides must be positive multiples of 8 within int32 range", what);
+  }
+  return 0;
+}
+}  // namespace
+
+extern "C" int tk_attn_fwd_gqa(int dtype, const void* q, const void* k, const void* v, void* o,
+                               float* lse, int64_t batch, int64_t heads, int64_t kv_heads,
+                               int64_t seq, int64_t head_dim, const int64_t* q_strides,
+                               const int64_t* k_strides, const int64_t* v_strides,
+                               const int64_t* o_strides, float sm_scale, int causal,
+                               void* stream) {
+  const void* ptrs[] = {q, k, v, o};
+  const int64_t* st[] = {q_strides, k_strides, v_strides, o_strides};
+  const bool kv[] = {false, true, true, false};
+  if (gqa_check("attn_fwd_gqa", dtype, ptrs, 4, batch, heads, kv_heads, seq, head_dim, st, kv, 4))
+    return 1;
+  if (!tk::attn_fwd_dma_applies(seq, head_dim, k_strides, v_strides))
+    return tk::fail("attn_fwd_gqa: each head's rows must span less than 2 GiB");
+  tk::attn_fwd_dma_launch(dtype, q, k, v, o, lse, batch, heads, kv_heads, seq, head_dim,
+                          q_strides, k_strides, v_strides, o_strides, sm_scale, causal != 0,
+                          tk::as_stream(stream));
+  return tk::check_launch("attn_fwd_gqa");
+}
+
+extern "C" int tk_attn_bwd_dkdv_gqa(int dtype, const void* q, const void* k, const void* v,
+                                    const void* dout, void* dk, void* dv, const float* lse,
+                                    const float* delta, int64_t batch, int64_t heads,
+                                    int64_t kv_heads, int64_t seq, int64_t head_dim,
+                                    const int64_t* q_strides, const int64_t* kv_strides,
+                                    float sm_scale, int causal, void* stream) {
+  const void* ptrs[] = {q, k, v, dout, dk, dv, lse, delta};
+  const int64_t* st[] = {q_strides, kv_strides};
+  const bool kv[] = {false, true};
+  if (gqa_check("attn_bwd_dkdv_gqa", dtype, ptrs, 8, batch, heads, kv_heads, seq, head_dim, st,
+                kv, 2))
+    return 1;
+  if (!tk::attn_bwd_dma_applies(seq, head_dim, q_strides, kv_strides))
+    return tk::fail("attn_bwd_dkdv_gqa: each head's rows must span less than 2 GiB");
+  tk::attn_bwd_dkdv_dma_launch(dtype, q, k, v, dout, dk, dv, lse, delta, batch, heads, kv_heads,
+                               seq, head_dim, q_strides, kv_strides, sm_scale, causal != 0,
+                               tk::as_stream(stream));
+  return tk::check_launch("attn_bwd_dkdv_gqa");
+}
+
+extern "C" int tk_attn_bwd_dq_gqa(int dtype, const void* q, const void* k, const void* v,
+                                  const void* dout, void* dq, const float* lse,
+                                  const float* delta, int64_t batch, int64_t heads,
+                                  int64_t kv_heads, int64_t seq, int64_t head_dim,
+                                  const int64_t* q_strides, const int64_t* kv_strides,
+                                  float sm_scale, int causal, void* stream) {
+  const void* ptrs[] = {q, k, v, dout, dq, lse, delta};
+  const int64_t* st[] = {q_strides, kv_strides};
+  const bool kv[] = {false, true};
+  if (gqa_check("attn_bwd_dq_gqa", dtype, ptrs, 7, batch, heads, kv_heads, seq, head_dim, st, kv,
+                2))
+    return 1;
+  if (!tk::attn_bwd_dma_applies(seq, head_dim, q_strides, kv_strides))
+    return tk::fail("attn_bwd_dq_gqa: each head's rows must span less than 2 GiB");
+  tk::attn_bwd_dq_dma_launch(dtype, q, k, v, dout, dq, lse, delta, batch, heads, kv_heads, seq,
+                             head_dim, q_strides, kv_strides, sm_scale, causal != 0,
+                             tk::as_stream(stream));
+  return tk::check_launch("attn_bwd_dq_gqa");
 }

@@ -1,5 +1,7 @@
 // Internal interface between the attention entry points (attention.hip) and the
-// buffer->LDS DMA kernels (attention_fwd.hip, attention_bwd.hip).
+// buffer->LDS DMA kernels (attention_fwd.hip, attention_bwd.hip). `kv_heads` divides
+// `heads`: query head h reads K/V head h / (heads / kv_heads) (kv_heads == heads is
+// multi-head attention).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <cstdint>
@@ -12,25 +14,30 @@ bool attn_fwd_dma_applies(int64_t seq, int64_t head_dim, const int64_t* k_stride
                           const int64_t* v_strides);
 
 void attn_fwd_dma_launch(int dtype, const void* q, const void* k, const void* v, void* o,
-                         float* lse, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
-                         const int64_t* q_strides, const int64_t* k_strides,
+                         float* lse, int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
+                         int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
                          const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
                          bool causal, hipStream_t stream);
 
-// True when one head's rows (shared layout of q, k, v, dO, dQ, dK, dV) span less than
-// 2 GiB. The caller has already checked dtype, head_dim and 16-byte row alignment.
-bool attn_bwd_dma_applies(int64_t seq, int64_t head_dim, const int64_t* strides);
+// True when one query head's rows (layout of q, dO, dQ) and one KV head's rows (layout
+// of k, v, dK, dV) each span less than 2 GiB. The caller has already checked dtype,
+// head_dim and 16-byte row alignment.
+bool attn_bwd_dma_applies(int64_t seq, int64_t head_dim, const int64_t* q_strides,
+                          const int64_t* kv_strides);
 
+// dK, dV per KV head, summed over its query heads in a fixed order (single writer).
 void attn_bwd_dkdv_dma_launch(int dtype, const void* q, const void* k, const void* v,
                               const void* dout, void* dk, void* dv, const float* lse,
-                              const float* delta, int64_t batch, int64_t heads, int64_t seq,
-                              int64_t head_dim, const int64_t* strides, float sm_scale,
-                              bool causal, hipStream_t stream);
+                              const float* delta, int64_t batch, int64_t heads,
+                              int64_t kv_heads, int64_t seq, int64_t head_dim,
+                              const int64_t* q_strides, const int64_t* kv_strides,
+                              float sm_scale, bool causal, hipStream_t stream);
 
 void attn_bwd_dq_dma_launch(int dtype, const void* q, const void* k, const void* v,
                             const void* dout, void* dq, const float* lse, const float* delta,
-                            int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
-                            const int64_t* strides, float sm_scale, bool causal,
+                            int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
+                            int64_t head_dim, const int64_t* q_strides,
+                            const int64_t* kv_strides, float sm_scale, bool causal,
                             hipStream_t stream);
 
 }  // namespace tk

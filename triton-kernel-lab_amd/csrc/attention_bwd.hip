@@ -34,11 +34,15 @@ __device__ __forceinline__ void wait_lgkm_n() {
 }
 
 struct BwdShape {
-  int heads, seq;
-  int64_t st[3];  // batch, head, sequence strides shared by q, k, v, dO, dQ, dK, dV
+  int heads, seq;       // query heads
+  int group;            // query heads per KV head (1: multi-head attention)
+  int64_t st[3];        // batch, head, sequence strides of q, dO, dQ
+  int64_t kst[3];       // batch, head, sequence strides of k, v, dK, dV
   float scale, scale_log2;
-  int blocks_per_head, tiles;
-  uint32_t head_bytes;  // extent of one head's rows
+  int blocks_per_head;  // 128-row blocks per head
+  int tiles, kv_tiles;  // dQ grid (query heads), dK/dV grid (KV heads)
+  uint32_t head_bytes;     // extent of one query head's rows
+  uint32_t kv_head_bytes;  // extent of one KV head's rows
 };
 
 template <int D>
@@ -217,14 +221,19 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   constexpr int NDMA = 2 * G::DMA_PER_TILE + 1; // per wave per block
   __shared__ __attribute__((aligned(1024))) char lds[G::STAGES * STB];
 
+  // Workgroup -> (batch, KV head, key block). The KV head's `group` query heads are
+  // streamed one after another as one sequence of query blocks (virtual block J: head
+  // J / nblk), so dK and dV sum over the group in a fixed order with a single writer.
   int w = blockIdx.x;
-  if (s.tiles % 8 == 0) w = (w % 8) * (s.tiles / 8) + w / 8;
-  const int bh = w / s.blocks_per_head;
+  if (s.kv_tiles % 8 == 0) w = (w % 8) * (s.kv_tiles / 8) + w / 8;
+  const int bkv = w / s.blocks_per_head;
   const int kblk = w % s.blocks_per_head;
-  const int b = bh / s.heads, h = bh % s.heads;
-  const int64_t base = b * s.st[0] + h * s.st[1];
+  const int kv_heads = s.heads / s.group;
+  const int b = bkv / kv_heads, kvh = bkv % kv_heads;
+  const int64_t kvbase = b * s.kst[0] + kvh * s.kst[1];
+  const int64_t qbase = b * s.st[0] + int64_t(kvh) * s.group * s.st[1];
   const int N = s.seq;
-  const int64_t sn = s.st[2];
+  const int64_t sn = s.st[2], kn = s.kst[2];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -237,18 +246,17 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   i32x4 kf[KS], vf[KS];
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) {
-    const int64_t off = base + int64_t(key) * sn + kk * 16 + hi * 8;
+    const int64_t off = kvbase + int64_t(key) * kn + kk * 16 + hi * 8;
     kf[kk] = key < N ? *reinterpret_cast<const i32x4*>(K + off) : i32x4{0, 0, 0, 0};
     vf[kk] = key < N ? *reinterpret_cast<const i32x4*>(V + off) : i32x4{0, 0, 0, 0};
   }
 
-  const __amdgpu_buffer_rsrc_t rq =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(Q + base), (short)0, s.head_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rdo =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(dO + base), (short)0, s.head_bytes, 0x00020000);
-  const float* stat_src = (wave < 2 ? lse : delta) + int64_t(bh) * N;
-  const __amdgpu_buffer_rsrc_t rst =
-      __builtin_amdgcn_make_buffer_rsrc((void*)stat_src, (short)0, uint32_t(N) * 4u, 0x00020000);
+  // Query-side sources of the group's first head; head g adds g head strides. Each
+  // head gets its own buffer extent, so rows past the sequence end read as zero.
+  const T* q_head0 = Q + qbase;
+  const T* do_head0 = dO + qbase;
+  const float* stat_head0 =
+      (wave < 2 ? lse : delta) + (int64_t(b) * s.heads + int64_t(kvh) * s.group) * N;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
 
   uint32_t q_src[G::DMA_PER_TILE];
@@ -260,12 +268,34 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   const int first = CAUSAL ? kb0 / BB : 0;  // first query block with a query >= kb0
   const int nblk = (N + BB - 1) / BB - first;
 
-  // DMA of relative block J into stage ST (clamped: past-the-end blocks reload the last).
-#define TK_BWD_DKDV_DMA(J, ST)                                                              \
+  // DMA of the next block in stream order (head dg of the group, relative block dj) into
+  // stage ST; past the end the last block is reloaded. Blocks are fetched strictly in
+  // order, so a cursor replaces a division, and the head's buffer resources are rebuilt
+  // only when the cursor moves to the next head.
+  int dg = 0, dj = 0;
+  __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)q_head0, (short)0,
+                                                                s.head_bytes, 0x00020000);
+  __amdgpu_buffer_rsrc_t rdo = __builtin_amdgcn_make_buffer_rsrc((void*)do_head0, (short)0,
+                                                                 s.head_bytes, 0x00020000);
+  __amdgpu_buffer_rsrc_t rst = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)stat_head0, (short)0, uint32_t(N) * 4u, 0x00020000);
+#define TK_BWD_DKDV_DMA(ST)                                                                 \
   {                                                                                         \
-    const int qb_ = first + min((J), nblk - 1);                                             \
+    const int qb_ = first + (dg >= s.group ? nblk - 1 : dj);                                \
     dma_tiles<D>(rq, rdo, lds + (ST) * STB, q_src, q_src, qb_ * blk_bytes, wave);           \
     dma_stats(rst, lds + (ST) * STB + 2 * TILE + wave * 128, st_src, qb_ * BB * 4, lane);   \
+    if (dg < s.group && ++dj == nblk) {                                                     \
+      dj = 0;                                                                               \
+      if (++dg < s.group) {                                                                 \
+        const int64_t h_ = int64_t(dg) * s.st[1];                                           \
+        rq = __builtin_amdgcn_make_buffer_rsrc((void*)(q_head0 + h_), (short)0,             \
+                                               s.head_bytes, 0x00020000);                   \
+        rdo = __builtin_amdgcn_make_buffer_rsrc((void*)(do_head0 + h_), (short)0,           \
+                                                s.head_bytes, 0x00020000);                  \
+        rst = __builtin_amdgcn_make_buffer_rsrc((void*)(stat_head0 + int64_t(dg) * N),      \
+                                                (short)0, uint32_t(N) * 4u, 0x00020000);    \
+      }                                                                                     \
+    }                                                                                       \
   }
 
   f32x16 acc_dv[DT], acc_dk[DT];
@@ -285,23 +315,24 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   const uint32_t sa = (hi * 4) * 4;  // statistics: query offset 4 hi within each group of 8
   const float sl2 = s.scale_log2;
 
-  TK_BWD_DKDV_DMA(0, 0)
-  TK_BWD_DKDV_DMA(1, 1)
+  TK_BWD_DKDV_DMA(0)
+  TK_BWD_DKDV_DMA(1)
   int stage = 0, fill = 2;
   // Causal: this wave's blocks start at the first one holding a query >= its first key.
   const int wave_first = CAUSAL ? min(nblk, (wk0 / BB) - first) : 0;
+  for (int g = 0; g < s.group; ++g) {
   int j = 0;
   for (; j < wave_first; ++j) {
     wait_vmcnt<NDMA>();
     barrier_no_fence();
-    TK_BWD_DKDV_DMA(j + 2, fill)
+    TK_BWD_DKDV_DMA(fill)
     stage = stage + 1 == G::STAGES ? 0 : stage + 1;
     fill = fill + 1 == G::STAGES ? 0 : fill + 1;
   }
   for (; j < nblk; ++j) {
     wait_vmcnt<NDMA>();
     barrier_no_fence();
-    TK_BWD_DKDV_DMA(j + 2, fill)
+    TK_BWD_DKDV_DMA(fill)
     const int q0 = (first + j) * BB;
     // Lane addresses for this stage; the dO tile and the 16-row steps are immediates.
     const uint32_t sbase = lds_base + stage * STB;
@@ -381,14 +412,15 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
     stage = stage + 1 == G::STAGES ? 0 : stage + 1;
     fill = fill + 1 == G::STAGES ? 0 : fill + 1;
   }
+  }
 #undef TK_BWD_DKDV_DMA
   wait_vmcnt<0>();
 
   // dK = scale (dK^T)^T, dV = (dV^T)^T: register r of tile dt is feature
   // 32 dt + 8 (r / 4) + 4 hi + r % 4 of this lane's key.
   if (key < N) {
-    T* dkr = dK + base + int64_t(key) * sn;
-    T* dvr = dV + base + int64_t(key) * sn;
+    T* dkr = dK + kvbase + int64_t(key) * kn;
+    T* dvr = dV + kvbase + int64_t(key) * kn;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -426,8 +458,9 @@ attn_bwd_dq_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   const int qblk = CAUSAL ? s.blocks_per_head - 1 - w % s.blocks_per_head : w % s.blocks_per_head;
   const int b = bh / s.heads, h = bh % s.heads;
   const int64_t base = b * s.st[0] + h * s.st[1];
+  const int64_t kvbase = b * s.kst[0] + (h / s.group) * s.kst[1];  // KV head h / group
   const int N = s.seq;
-  const int64_t sn = s.st[2];
+  const int64_t sn = s.st[2], kn = s.kst[2];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -447,18 +480,18 @@ attn_bwd_dq_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   const float lse_q = query < N ? lse[int64_t(bh) * N + query] : 0.f;
   const float delta_q = query < N ? delta[int64_t(bh) * N + query] : 0.f;
 
-  const __amdgpu_buffer_rsrc_t rk =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(K + base), (short)0, s.head_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(V + base), (short)0, s.head_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(K + kvbase), (short)0, s.kv_head_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(V + kvbase), (short)0, s.kv_head_bytes, 0x00020000);
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
   uint32_t k_src[G::DMA_PER_TILE], v_src[G::DMA_PER_TILE];
 #pragma unroll
   for (int x = 0; x < G::DMA_PER_TILE; ++x) {
-    k_src[x] = tile_src<D, true>(wave, x, lane, sn);
-    v_src[x] = tile_src<D, false>(wave, x, lane, sn);
+    k_src[x] = tile_src<D, true>(wave, x, lane, kn);
+    v_src[x] = tile_src<D, false>(wave, x, lane, kn);
   }
-  const uint32_t blk_bytes = uint32_t(BB * sn) * 2u;
+  const uint32_t blk_bytes = uint32_t(BB * kn) * 2u;
   const int kv_end = CAUSAL ? min(N, q0 + G::BW) : N;
   const int nblk = (kv_end + BB - 1) / BB;
 
@@ -617,23 +650,30 @@ attn_bwd_dq_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   }
 }
 
-BwdShape make_shape(int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
-                    const int64_t* strides, float sm_scale) {
+BwdShape make_shape(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
+                    int64_t head_dim, const int64_t* q_strides, const int64_t* kv_strides,
+                    float sm_scale) {
   BwdShape s{};
   s.heads = (int)heads;
   s.seq = (int)seq;
-  for (int i = 0; i < 3; ++i) s.st[i] = strides[i];
+  s.group = (int)(heads / kv_heads);
+  for (int i = 0; i < 3; ++i) {
+    s.st[i] = q_strides[i];
+    s.kst[i] = kv_strides[i];
+  }
   s.scale = sm_scale;
   s.scale_log2 = sm_scale * 1.4426950408889634f;
   s.blocks_per_head = (int)tk::cdiv(seq, 128);
   s.tiles = (int)(s.blocks_per_head * batch * heads);
-  s.head_bytes = (uint32_t)(((seq - 1) * strides[2] + head_dim) * 2);
+  s.kv_tiles = (int)(s.blocks_per_head * batch * kv_heads);
+  s.head_bytes = (uint32_t)(((seq - 1) * q_strides[2] + head_dim) * 2);
+  s.kv_head_bytes = (uint32_t)(((seq - 1) * kv_strides[2] + head_dim) * 2);
   return s;
 }
 
-#define TK_BWD_LAUNCH(KERNEL, ...)                                                          \
+#define TK_BWD_LAUNCH(TILES, KERNEL, ...)                                                   \
   do {                                                                                      \
-    const dim3 grid(static_cast<unsigned>(s.tiles));                                       \
+    const dim3 grid(static_cast<unsigned>(TILES));                                         \
     if (dtype == TK_DTYPE_F16) {                                                            \
       using T = _Float16;                                                                   \
       if (head_dim == 64) {                                                                 \
@@ -659,28 +699,36 @@ BwdShape make_shape(int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
 
 namespace tk {
 
-bool attn_bwd_dma_applies(int64_t seq, int64_t head_dim, const int64_t* strides) {
-  return ((seq - 1) * strides[2] + head_dim) * 2 < (int64_t(1) << 31);
+bool attn_bwd_dma_applies(int64_t seq, int64_t head_dim, const int64_t* q_strides,
+                          const int64_t* kv_strides) {
+  // 32-bit buffer offsets: one head's rows must span less than 2 GiB.
+  const int64_t lim = int64_t(1) << 31;
+  return ((seq - 1) * q_strides[2] + head_dim) * 2 < lim &&
+         ((seq - 1) * kv_strides[2] + head_dim) * 2 < lim;
 }
 
 void attn_bwd_dkdv_dma_launch(int dtype, const void* q, const void* k, const void* v,
                               const void* dout, void* dk, void* dv, const float* lse,
-                              const float* delta, int64_t batch, int64_t heads, int64_t seq,
-                              int64_t head_dim, const int64_t* strides, float sm_scale,
-                              bool causal, hipStream_t stream) {
-  const BwdShape s = make_shape(batch, heads, seq, head_dim, strides, sm_scale);
-  TK_BWD_LAUNCH(attn_bwd_dkdv_dma_kernel, (const T*)q, (const T*)k, (const T*)v,
+                              const float* delta, int64_t batch, int64_t heads,
+                              int64_t kv_heads, int64_t seq, int64_t head_dim,
+                              const int64_t* q_strides, const int64_t* kv_strides,
+                              float sm_scale, bool causal, hipStream_t stream) {
+  const BwdShape s =
+      make_shape(batch, heads, kv_heads, seq, head_dim, q_strides, kv_strides, sm_scale);
+  TK_BWD_LAUNCH(s.kv_tiles, attn_bwd_dkdv_dma_kernel, (const T*)q, (const T*)k, (const T*)v,
                 (const T*)dout, (T*)dk, (T*)dv, lse, delta, s);
 }
 
 void attn_bwd_dq_dma_launch(int dtype, const void* q, const void* k, const void* v,
                             const void* dout, void* dq, const float* lse, const float* delta,
-                            int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
-                            const int64_t* strides, float sm_scale, bool causal,
+                            int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
+                            int64_t head_dim, const int64_t* q_strides,
+                            const int64_t* kv_strides, float sm_scale, bool causal,
                             hipStream_t stream) {
-  const BwdShape s = make_shape(batch, heads, seq, head_dim, strides, sm_scale);
-  TK_BWD_LAUNCH(attn_bwd_dq_dma_kernel, (const T*)q, (const T*)k, (const T*)v, (const T*)dout,
-                (T*)dq, lse, delta, s);
+  const BwdShape s =
+      make_shape(batch, heads, kv_heads, seq, head_dim, q_strides, kv_strides, sm_scale);
+  TK_BWD_LAUNCH(s.tiles, attn_bwd_dq_dma_kernel, (const T*)q, (const T*)k, (const T*)v,
+                (const T*)dout, (T*)dq, lse, delta, s);
 }
 
 }  // namespace tk

@@ -42,6 +42,7 @@ constexpr int kThreads = 512;
 
 struct Shape {
   int heads, seq;
+  int group;  // query heads per KV head: K/V of head h are those of KV head h / group
   int64_t q[3], k[3], v[3], o[3];  // batch, head, sequence strides (elements)
   float scale_log2;
   int q_blocks, tiles;
@@ -99,9 +100,10 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
   const int bh = w / s.q_blocks;
   const int qb = CAUSAL ? s.q_blocks - 1 - w % s.q_blocks : w % s.q_blocks;
   const int b = bh / s.heads, h = bh % s.heads;
+  const int kvh = h / s.group;
   const T* Qh = Q + b * s.q[0] + h * s.q[1];
-  const T* Kh = K + b * s.k[0] + h * s.k[1];
-  const T* Vh = V + b * s.v[0] + h * s.v[1];
+  const T* Kh = K + b * s.k[0] + kvh * s.k[1];
+  const T* Vh = V + b * s.v[0] + kvh * s.v[1];
   T* Oh = O + b * s.o[0] + h * s.o[1];
   const int N = s.seq;
 
@@ -354,13 +356,14 @@ bool attn_fwd_dma_applies(int64_t seq, int64_t head_dim, const int64_t* k_stride
 }
 
 void attn_fwd_dma_launch(int dtype, const void* q, const void* k, const void* v, void* o,
-                         float* lse, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
-                         const int64_t* q_strides, const int64_t* k_strides,
+                         float* lse, int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
+                         int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
                          const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
                          bool causal, hipStream_t stream) {
   Shape s{};
   s.heads = (int)heads;
   s.seq = (int)seq;
+  s.group = (int)(heads / kv_heads);
   for (int i = 0; i < 3; ++i) {
     s.q[i] = q_strides[i];
     s.k[i] = k_strides[i];

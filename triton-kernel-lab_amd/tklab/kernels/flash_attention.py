@@ -11,6 +11,11 @@ without a per-length recompile.
 
 The registry keeps the reference's spec shape (batch 1, 16 heads, head_dim
 64, ``flash_attention.py:27-29``) so its FLOP model and tests carry over.
+
+``grouped_query_attention(q, k, v, *, causal)`` extends the same kernels to K/V
+with fewer heads than Q (query head ``h`` uses KV head ``h // (heads //
+kv_heads)``), forward and backward; dK/dV sum a KV head's query heads in a fixed
+order, so the backward stays deterministic.
 """
 
 from __future__ import annotations
@@ -248,6 +253,121 @@ def attention_noncausal(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> to
 def attention_causal(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
     """Dense causal scaled dot-product attention with autograd."""
     return _attention(q, k, v, causal=True)
+
+
+def _validate_gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    """Grouped-query contract: the dense one with K/V heads dividing Q heads."""
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("attention expects Q, K, and V shaped (batch, heads, sequence, dim)")
+    if k.shape != v.shape:
+        raise ValueError("K and V must have identical shapes")
+    if q.shape[0] != k.shape[0] or q.shape[2:] != k.shape[2:]:
+        raise ValueError("Q and K/V must agree on batch, sequence and head_dim")
+    if 0 in q.shape or 0 in k.shape:
+        raise ValueError("attention does not support empty dimensions")
+    if q.shape[1] % k.shape[1]:
+        raise ValueError("the number of Q heads must be a multiple of the K/V heads")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("Q, K, and V must be on the same device")
+    if q.device.type != "cuda":
+        raise ValueError("attention requires CUDA (ROCm/HIP) tensors")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError("Q, K, and V must have the same dtype")
+    if q.dtype not in _DTYPES:
+        raise ValueError("attention supports float16 and bfloat16 inputs only")
+    if q.shape[-1] not in _HEAD_DIMS:
+        raise ValueError(f"attention requires head_dim in {_HEAD_DIMS}")
+    for name, tensor in (("Q", q), ("K", k), ("V", v)):
+        if not tensor.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+        assert_int32_addressable(tensor, name=name)
+
+
+def _launch_gqa_forward(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, output: torch.Tensor,
+    softmax_lse: torch.Tensor | None, *, causal: bool,
+) -> None:
+    """Grouped-query forward into preallocated buffers (``softmax_lse`` may be None)."""
+    batch, heads, n_ctx, head_dim = q.shape
+    _hip.call(
+        "tk_attn_fwd_gqa", _hip.dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+        output.data_ptr(), _hip.ptr(softmax_lse), batch, heads, k.shape[1], n_ctx, head_dim,
+        _strides(q), _strides(k), _strides(v), _strides(output), 1.0 / math.sqrt(head_dim),
+        int(causal), _hip.stream_of(q),
+    )
+
+
+def _launch_gqa_backward(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, output: torch.Tensor,
+    softmax_lse: torch.Tensor, do: torch.Tensor, *, causal: bool,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Grouped-query backward: delta, dK/dV per KV head, dQ per query head."""
+    if do.shape != q.shape or do.device != q.device or do.dtype != q.dtype:
+        raise ValueError("attention upstream gradient metadata must match Q")
+    do = do.contiguous()
+    batch, heads, n_ctx, head_dim = q.shape
+    kv_heads = k.shape[1]
+    code = _hip.dtype_code(q.dtype)
+    stream = _hip.stream_of(q)
+    scale = 1.0 / math.sqrt(head_dim)
+    delta = torch.empty((batch, heads, n_ctx), dtype=torch.float32, device=q.device)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    qs, kvs = _strides(q), _strides(k)
+    _hip.call("tk_attn_bwd_preprocess", code, output.data_ptr(), do.data_ptr(), delta.data_ptr(),
+              batch, heads, n_ctx, head_dim, qs, stream)
+    _hip.call("tk_attn_bwd_dkdv_gqa", code, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+              do.data_ptr(), dk.data_ptr(), dv.data_ptr(), softmax_lse.data_ptr(),
+              delta.data_ptr(), batch, heads, kv_heads, n_ctx, head_dim, qs, kvs, scale,
+              int(causal), stream)
+    _hip.call("tk_attn_bwd_dq_gqa", code, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+              do.data_ptr(), dq.data_ptr(), softmax_lse.data_ptr(), delta.data_ptr(), batch,
+              heads, kv_heads, n_ctx, head_dim, qs, kvs, scale, int(causal), stream)
+    return dq, dk, dv
+
+
+class _GQAFunction(torch.autograd.Function):
+    """Autograd bridge of grouped-query attention: saves Q, K, V, O and the LSE."""
+
+    @staticmethod
+    def forward(
+        ctx: Any, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool
+    ) -> torch.Tensor:
+        output = torch.empty_like(q)
+        batch, heads, n_ctx, _ = q.shape
+        softmax_lse = torch.empty((batch, heads, n_ctx), dtype=torch.float32, device=q.device)
+        _launch_gqa_forward(q, k, v, output, softmax_lse, causal=causal)
+        ctx.save_for_backward(q, k, v, output, softmax_lse)
+        ctx.causal = causal
+        return output
+
+    @staticmethod
+    @once_differentiable
+    def backward(
+        ctx: Any, do: torch.Tensor
+    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, None]:
+        q, k, v, output, softmax_lse = ctx.saved_tensors
+        dq, dk, dv = _launch_gqa_backward(q, k, v, output, softmax_lse, do, causal=ctx.causal)
+        return dq, dk, dv, None
+
+
+def grouped_query_attention(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
+) -> torch.Tensor:
+    """Scaled dot-product attention with K/V shared by groups of query heads.
+
+    ``q`` is ``(batch, heads, sequence, head_dim)``, ``k`` and ``v`` are
+    ``(batch, kv_heads, sequence, head_dim)`` with ``heads % kv_heads == 0``;
+    query head ``h`` attends with KV head ``h // (heads // kv_heads)``. Same
+    numerics as :func:`attention_causal` / :func:`attention_noncausal`, with
+    autograd (first order).
+    """
+    _validate_gqa(q, k, v)
+    needs_grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
+    if not needs_grad:
+        output = torch.empty_like(q)
+        _launch_gqa_forward(q, k, v, output, None, causal=causal)
+        return output
+    return cast(torch.Tensor, _GQAFunction.apply(q, k, v, causal))
 
 
 def _reference_factory(*, causal: bool) -> TensorFn:
