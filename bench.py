@@ -32,6 +32,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import math
 import os
@@ -469,6 +470,27 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
              lambda: fa._launch_gqa_backward(qq, kk, vv, o, lse, do, causal=True),
              int(2.5 * flops), "bfloat16", reps=5)
     del qq, kk, vv, do, o, lse
+    # Variable-length causal attention: one packed batch of 32768 tokens in sequences of
+    # 8192, 2 x 4096, 4 x 2048 and 8 x 1024 (H32 Hkv8 D128); FLOPs summed per sequence.
+    lengths = [8192] + [4096] * 2 + [2048] * 4 + [1024] * 8
+    total = sum(lengths)
+    cu = torch.tensor([0] + list(itertools.accumulate(lengths)), device=device,
+                      dtype=torch.int32)
+    qq, do = (torch.randn(total, 32, 128, device=device, dtype=bf16, generator=g)
+              for _ in range(2))
+    kk, vv = (torch.randn(total, 8, 128, device=device, dtype=bf16, generator=g)
+              for _ in range(2))
+    o = torch.empty_like(qq)
+    lse = torch.empty(32, total, device=device, dtype=torch.float32)
+    flops = sum(fa.attention_flops(1, 32, n, 128, causal=True) for n in lengths)
+    tag = "bf16 H32 Hkv8 D128 causal, 32768 tokens in 15 sequences of 1024-8192"
+    mfma_row("tk_attn_fwd_varlen", tag,
+             lambda: fa._launch_varlen_forward(qq, kk, vv, cu, 8192, o, lse, causal=True),
+             flops, "bfloat16", reps=5)
+    mfma_row("tk_attn_bwd_varlen (preprocess+dkdv+dq)", tag + ", 2.5x fwd FLOPs",
+             lambda: fa._launch_varlen_backward(qq, kk, vv, cu, 8192, o, lse, do, causal=True),
+             int(2.5 * flops), "bfloat16", reps=5)
+    del qq, kk, vv, do, o, lse, cu
     del flush
     torch.cuda.empty_cache()
     return rows

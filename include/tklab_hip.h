@@ -212,6 +212,32 @@ int tk_attn_bwd_dq_gqa(int dtype, const void* q, const void* k, const void* v,
                        int64_t head_dim, const int64_t* q_strides, const int64_t* kv_strides,
                        float sm_scale, int causal, void* stream);
 
+/* Variable-length attention: packed q, o, dO, dQ [total][heads][head_dim] and k, v,
+ * dK, dV [total][kv_heads][head_dim] (strides {token, head}; head_dim unit-stride),
+ * int32 cu_seqlens[batch + 1]: sequence b is rows cu_seqlens[b] .. cu_seqlens[b+1]
+ * (max_seqlen the longest). Same arithmetic as tk_attn_fwd_gqa / _bwd_*_gqa per
+ * sequence; LSE and delta are float32 [heads][total] (delta from tk_attn_bwd_preprocess
+ * with batch 1, seq total, strides {total * token, head, token}). Lengths are clamped
+ * into [0, total] and to max_seqlen inside the kernels. No reference kernel exists: the
+ * reference lists variable-length batches among its next steps (README.md:509-514). */
+int tk_attn_fwd_varlen(int dtype, const void* q, const void* k, const void* v, void* o,
+                       float* lse, const int32_t* cu_seqlens, int64_t batch, int64_t heads,
+                       int64_t kv_heads, int64_t max_seqlen, int64_t total, int64_t head_dim,
+                       const int64_t* q_strides, const int64_t* kv_strides,
+                       const int64_t* o_strides, float sm_scale, int causal, void* stream);
+int tk_attn_bwd_dkdv_varlen(int dtype, const void* q, const void* k, const void* v,
+                            const void* dout, void* dk, void* dv, const float* lse,
+                            const float* delta, const int32_t* cu_seqlens, int64_t batch,
+                            int64_t heads, int64_t kv_heads, int64_t max_seqlen, int64_t total,
+                            int64_t head_dim, const int64_t* q_strides,
+                            const int64_t* kv_strides, float sm_scale, int causal, void* stream);
+int tk_attn_bwd_dq_varlen(int dtype, const void* q, const void* k, const void* v,
+                          const void* dout, void* dq, const float* lse, const float* delta,
+                          const int32_t* cu_seqlens, int64_t batch, int64_t heads,
+                          int64_t kv_heads, int64_t max_seqlen, int64_t total, int64_t head_dim,
+                          const int64_t* q_strides, const int64_t* kv_strides, float sm_scale,
+                          int causal, void* stream);
+
 /* ---- Registry kernels outside the transformer hot path ---------------- */
 
 /* out[i*out_stride] = x[i*x_stride] + y[i*y_stride], i < n (strides may be 0).

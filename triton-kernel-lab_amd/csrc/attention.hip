@@ -954,3 +954,107 @@ extern "C" int tk_attn_bwd_dq_gqa(int dtype, const void* q, const void* k, const
                              tk::as_stream(stream));
   return tk::check_launch("attn_bwd_dq_gqa");
 }
+
+// ---------------------------------------------------------------- variable-length batches
+//
+// Packed [total][heads][head_dim] tensors with int32 cu_seqlens[batch + 1]: sequence b is
+// rows cu_seqlens[b] .. cu_seqlens[b+1]. Strides are {token, head} in elements. The kernels
+// clamp every sequence into [0, total] and to max_seqlen, so a malformed lengths table
+// cannot address memory outside the tensors. LSE and delta are float32 [heads][total]
+// (tk_attn_bwd_preprocess with batch 1, seq total and strides {total * token, head, token}
+// computes delta in that layout).
+
+namespace {
+int varlen_check(const char* what, int dtype, const void* const* ptrs, int nptr,
+                 const int32_t* cu, int64_t batch, int64_t heads, int64_t kv_heads,
+                 int64_t max_seqlen, int64_t total, int64_t head_dim,
+                 const int64_t* const* strides, const bool* kv_side, int nstr) {
+  if (check_common(what, dtype, batch, heads, max_seqlen, head_dim)) return 1;
+  if (cu == nullptr) return tk::fail("%s: null pointer", what);
+  if (kv_heads <= 0 || heads % kv_heads != 0)
+    return tk::fail("%s: heads must be a positive multiple of kv_heads", what);
+  if (total <= 0 || total > INT32_MAX || max_seqlen > total)
+    return tk::fail("%s: total must be positive and at least max_seqlen", what);
+  for (int i = 0; i < nptr; ++i) {
+    if (!ptrs[i]) return tk::fail("%s: null pointer", what);
+    if (!tk::aligned16(ptrs[i])) return tk::fail("%s: tensors must be 16-byte aligned", what);
+  }
+  for (int i = 0; i < nstr; ++i) {
+    const int64_t* st = strides[i];
+    if (!st) return tk::fail("%s: null pointer", what);
+    const int64_t h = kv_side[i] ? kv_heads : heads;
+    if (st[0] <= 0 || st[1] <= 0 || st[0] % 8 || st[1] % 8 ||
+        (total - 1) * st[0] + (h - 1) * st[1] + head_dim - 1 > INT32_MAX)
+      return tk::fail("%s: strides must be positive multiples of 8 within int32 range", what);
+    // Each head's rows go through one 32-bit buffer range.
+    if (((total - 1) * st[0] + head_dim) * 2 >= (int64_t(1) << 31))
+      return tk::fail("%s: each head's rows must span less than 2 GiB", what);
+  }
+  return 0;
+}
+
+// {token, head} -> the kernels' {batch, head, sequence} strides (batch stride 0).
+struct Strides3 {
+  int64_t v[3];
+};
+Strides3 packed(const int64_t* st) { return {{0, st[1], st[0]}}; }
+}  // namespace
+
+extern "C" int tk_attn_fwd_varlen(int dtype, const void* q, const void* k, const void* v,
+                                  void* o, float* lse, const int32_t* cu_seqlens, int64_t batch,
+                                  int64_t heads, int64_t kv_heads, int64_t max_seqlen,
+                                  int64_t total, int64_t head_dim, const int64_t* q_strides,
+                                  const int64_t* kv_strides, const int64_t* o_strides,
+                                  float sm_scale, int causal, void* stream) {
+  const void* ptrs[] = {q, k, v, o};
+  const int64_t* st[] = {q_strides, kv_strides, o_strides};
+  const bool kv[] = {false, true, false};
+  if (varlen_check("attn_fwd_varlen", dtype, ptrs, 4, cu_seqlens, batch, heads, kv_heads,
+                   max_seqlen, total, head_dim, st, kv, 3))
+    return 1;
+  const Strides3 qs = packed(q_strides), ks = packed(kv_strides), os = packed(o_strides);
+  tk::attn_fwd_dma_launch(dtype, q, k, v, o, lse, batch, heads, kv_heads, max_seqlen, head_dim,
+                          qs.v, ks.v, ks.v, os.v, sm_scale, causal != 0, tk::as_stream(stream),
+                          cu_seqlens, total);
+  return tk::check_launch("attn_fwd_varlen");
+}
+
+extern "C" int tk_attn_bwd_dkdv_varlen(int dtype, const void* q, const void* k, const void* v,
+                                       const void* dout, void* dk, void* dv, const float* lse,
+                                       const float* delta, const int32_t* cu_seqlens,
+                                       int64_t batch, int64_t heads, int64_t kv_heads,
+                                       int64_t max_seqlen, int64_t total, int64_t head_dim,
+                                       const int64_t* q_strides, const int64_t* kv_strides,
+                                       float sm_scale, int causal, void* stream) {
+  const void* ptrs[] = {q, k, v, dout, dk, dv, lse, delta};
+  const int64_t* st[] = {q_strides, kv_strides};
+  const bool kv[] = {false, true};
+  if (varlen_check("attn_bwd_dkdv_varlen", dtype, ptrs, 8, cu_seqlens, batch, heads, kv_heads,
+                   max_seqlen, total, head_dim, st, kv, 2))
+    return 1;
+  const Strides3 qs = packed(q_strides), ks = packed(kv_strides);
+  tk::attn_bwd_dkdv_dma_launch(dtype, q, k, v, dout, dk, dv, lse, delta, batch, heads, kv_heads,
+                               max_seqlen, head_dim, qs.v, ks.v, sm_scale, causal != 0,
+                               tk::as_stream(stream), cu_seqlens, total);
+  return tk::check_launch("attn_bwd_dkdv_varlen");
+}
+
+extern "C" int tk_attn_bwd_dq_varlen(int dtype, const void* q, const void* k, const void* v,
+                                     const void* dout, void* dq, const float* lse,
+                                     const float* delta, const int32_t* cu_seqlens,
+                                     int64_t batch, int64_t heads, int64_t kv_heads,
+                                     int64_t max_seqlen, int64_t total, int64_t head_dim,
+                                     const int64_t* q_strides, const int64_t* kv_strides,
+                                     float sm_scale, int causal, void* stream) {
+  const void* ptrs[] = {q, k, v, dout, dq, lse, delta};
+  const int64_t* st[] = {q_strides, kv_strides};
+  const bool kv[] = {false, true};
+  if (varlen_check("attn_bwd_dq_varlen", dtype, ptrs, 7, cu_seqlens, batch, heads, kv_heads,
+                   max_seqlen, total, head_dim, st, kv, 2))
+    return 1;
+  const Strides3 qs = packed(q_strides), ks = packed(kv_strides);
+  tk::attn_bwd_dq_dma_launch(dtype, q, k, v, dout, dq, lse, delta, batch, heads, kv_heads,
+                             max_seqlen, head_dim, qs.v, ks.v, sm_scale, causal != 0,
+                             tk::as_stream(stream), cu_seqlens, total);
+  return tk::check_launch("attn_bwd_dq_varlen");
+}

@@ -1,7 +1,9 @@
 // Internal interface between the attention entry points (attention.hip) and the
 // buffer->LDS DMA kernels (attention_fwd.hip, attention_bwd.hip). `kv_heads` divides
 // `heads`: query head h reads K/V head h / (heads / kv_heads) (kv_heads == heads is
-// multi-head attention).
+// multi-head attention). With `cu_seqlens` (int32[batch + 1]) the batch is variable-length:
+// sequence b is rows cu_seqlens[b] .. cu_seqlens[b + 1] of a packed [total][head][dim]
+// layout (batch strides 0, `seq` the longest length) and LSE / delta are [head][total].
 #pragma once
 #include <hip/hip_runtime.h>
 #include <cstdint>
@@ -17,7 +19,8 @@ void attn_fwd_dma_launch(int dtype, const void* q, const void* k, const void* v,
                          float* lse, int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
                          int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
                          const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
-                         bool causal, hipStream_t stream);
+                         bool causal, hipStream_t stream, const int32_t* cu_seqlens = nullptr,
+                         int64_t total = 0);
 
 // True when one query head's rows (layout of q, dO, dQ) and one KV head's rows (layout
 // of k, v, dK, dV) each span less than 2 GiB. The caller has already checked dtype,
@@ -31,13 +34,15 @@ void attn_bwd_dkdv_dma_launch(int dtype, const void* q, const void* k, const voi
                               const float* delta, int64_t batch, int64_t heads,
                               int64_t kv_heads, int64_t seq, int64_t head_dim,
                               const int64_t* q_strides, const int64_t* kv_strides,
-                              float sm_scale, bool causal, hipStream_t stream);
+                              float sm_scale, bool causal, hipStream_t stream,
+                              const int32_t* cu_seqlens = nullptr, int64_t total = 0);
 
 void attn_bwd_dq_dma_launch(int dtype, const void* q, const void* k, const void* v,
                             const void* dout, void* dq, const float* lse, const float* delta,
                             int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
                             int64_t head_dim, const int64_t* q_strides,
                             const int64_t* kv_strides, float sm_scale, bool causal,
-                            hipStream_t stream);
+                            hipStream_t stream, const int32_t* cu_seqlens = nullptr,
+                            int64_t total = 0);
 
 }  // namespace tk

@@ -43,7 +43,28 @@ struct BwdShape {
   int tiles, kv_tiles;  // dQ grid (query heads), dK/dV grid (KV heads)
   uint32_t head_bytes;     // extent of one query head's rows
   uint32_t kv_head_bytes;  // extent of one KV head's rows
+  // Variable-length batches (null for equal lengths): sequence b is rows cu[b] ..
+  // cu[b+1] of packed [total][head][dim] tensors (batch strides 0; seq is the longest
+  // length), and lse / delta are [head][total].
+  const int32_t* cu;
+  int total, batch;
 };
+
+// Sequence b of a batch: its first row and length, and the buffer extents of one of
+// its query-side / KV-side heads. Varlen lengths are clamped into [0, total] and to
+// seq, so no lengths table can address rows outside the packed tensors.
+struct SeqSpan {
+  int start, n;
+  uint32_t q_bytes, kv_bytes;
+};
+
+template <int D>
+__device__ __forceinline__ SeqSpan seq_span(const BwdShape& s, int b) {
+  if (s.cu == nullptr) return {0, s.seq, s.head_bytes, s.kv_head_bytes};
+  const VarlenRows r = varlen_rows(s.cu, b, s.total, s.seq);
+  return {r.start, r.n, uint32_t(((r.n - 1) * s.st[2] + D) * 2),
+          uint32_t(((r.n - 1) * s.kst[2] + D) * 2)};
+}
 
 template <int D>
 struct BwdGeo {
@@ -224,21 +245,42 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   // Workgroup -> (batch, KV head, key block). The KV head's `group` query heads are
   // streamed one after another as one sequence of query blocks (virtual block J: head
   // J / nblk), so dK and dV sum over the group in a fixed order with a single writer.
-  int w = blockIdx.x;
-  if (s.kv_tiles % 8 == 0) w = (w % 8) * (s.kv_tiles / 8) + w / 8;
-  const int bkv = w / s.blocks_per_head;
-  const int kblk = w % s.blocks_per_head;
+  // Varlen: the heavy-first schedule over every sequence's key blocks (level = blocks
+  // after this one, so causal's longest query ranges start first), KV heads interleaved
+  // over the XCDs.
   const int kv_heads = s.heads / s.group;
-  const int b = bkv / kv_heads, kvh = bkv % kv_heads;
-  const int64_t kvbase = b * s.kst[0] + kvh * s.kst[1];
-  const int64_t qbase = b * s.st[0] + int64_t(kvh) * s.group * s.st[1];
-  const int N = s.seq;
+  int b, kvh, kblk;
+  if (s.cu != nullptr) {
+    kvh = varlen_head(blockIdx.x, kv_heads);
+    VarlenTile vt;
+    if (!varlen_tile(s.cu, s.batch, s.total, s.seq, G::BW, blockIdx.x / kv_heads, vt)) return;
+    b = vt.b;
+    const int nb = (varlen_rows(s.cu, b, s.total, s.seq).n + G::BW - 1) / G::BW;
+    kblk = nb - 1 - vt.level;
+  } else {
+    int w = blockIdx.x;
+    if (s.kv_tiles % 8 == 0) w = (w % 8) * (s.kv_tiles / 8) + w / 8;
+    const int bkv = w / s.blocks_per_head;
+    kblk = w % s.blocks_per_head;
+    b = bkv / kv_heads;
+    kvh = bkv % kv_heads;
+  }
+  const SeqSpan sp = seq_span<D>(s, b);
+  const int N = sp.n;
   const int64_t sn = s.st[2], kn = s.kst[2];
+  const int64_t kvbase = b * s.kst[0] + kvh * s.kst[1] + int64_t(sp.start) * kn;
+  const int64_t qbase = b * s.st[0] + int64_t(kvh) * s.group * s.st[1] + int64_t(sp.start) * sn;
+  // Statistics of the group's first query head; head g of the group is g heads later.
+  const int64_t stat_head = s.cu != nullptr ? s.total : N;
+  const int64_t stat0 = s.cu != nullptr
+                            ? int64_t(kvh) * s.group * s.total + sp.start
+                            : (int64_t(b) * s.heads + int64_t(kvh) * s.group) * N;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, hi = lane >> 5;
   const int kb0 = kblk * G::BW;
+  if (kb0 >= N) return;  // varlen: past this sequence's end (uniform)
   const int wk0 = kb0 + wave * G::LW;
   const int key = wk0 + l32;  // this lane's key (column of S and dP)
 
@@ -255,8 +297,7 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   // head gets its own buffer extent, so rows past the sequence end read as zero.
   const T* q_head0 = Q + qbase;
   const T* do_head0 = dO + qbase;
-  const float* stat_head0 =
-      (wave < 2 ? lse : delta) + (int64_t(b) * s.heads + int64_t(kvh) * s.group) * N;
+  const float* stat_head0 = (wave < 2 ? lse : delta) + stat0;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
 
   uint32_t q_src[G::DMA_PER_TILE];
@@ -274,9 +315,9 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   // only when the cursor moves to the next head.
   int dg = 0, dj = 0;
   __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)q_head0, (short)0,
-                                                                s.head_bytes, 0x00020000);
+                                                                sp.q_bytes, 0x00020000);
   __amdgpu_buffer_rsrc_t rdo = __builtin_amdgcn_make_buffer_rsrc((void*)do_head0, (short)0,
-                                                                 s.head_bytes, 0x00020000);
+                                                                 sp.q_bytes, 0x00020000);
   __amdgpu_buffer_rsrc_t rst = __builtin_amdgcn_make_buffer_rsrc(
       (void*)stat_head0, (short)0, uint32_t(N) * 4u, 0x00020000);
 #define TK_BWD_DKDV_DMA(ST)                                                                 \
@@ -289,10 +330,10 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
       if (++dg < s.group) {                                                                 \
         const int64_t h_ = int64_t(dg) * s.st[1];                                           \
         rq = __builtin_amdgcn_make_buffer_rsrc((void*)(q_head0 + h_), (short)0,             \
-                                               s.head_bytes, 0x00020000);                   \
+                                               sp.q_bytes, 0x00020000);                     \
         rdo = __builtin_amdgcn_make_buffer_rsrc((void*)(do_head0 + h_), (short)0,           \
-                                                s.head_bytes, 0x00020000);                  \
-        rst = __builtin_amdgcn_make_buffer_rsrc((void*)(stat_head0 + int64_t(dg) * N),      \
+                                                sp.q_bytes, 0x00020000);                    \
+        rst = __builtin_amdgcn_make_buffer_rsrc((void*)(stat_head0 + dg * stat_head),       \
                                                 (short)0, uint32_t(N) * 4u, 0x00020000);    \
       }                                                                                     \
     }                                                                                       \
@@ -452,20 +493,37 @@ attn_bwd_dq_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   constexpr int NDMA = 2 * G::DMA_PER_TILE;
   __shared__ __attribute__((aligned(1024))) char lds[G::STAGES * STB];
 
-  int w = blockIdx.x;
-  if (s.tiles % 8 == 0) w = (w % 8) * (s.tiles / 8) + w / 8;
-  const int bh = w / s.blocks_per_head;
-  const int qblk = CAUSAL ? s.blocks_per_head - 1 - w % s.blocks_per_head : w % s.blocks_per_head;
-  const int b = bh / s.heads, h = bh % s.heads;
-  const int64_t base = b * s.st[0] + h * s.st[1];
-  const int64_t kvbase = b * s.kst[0] + (h / s.group) * s.kst[1];  // KV head h / group
-  const int N = s.seq;
+  // Varlen: the heavy-first schedule over every sequence's query blocks (level = query
+  // block), heads interleaved over the XCDs.
+  int b, h, qblk;
+  if (s.cu != nullptr) {
+    h = varlen_head(blockIdx.x, s.heads);
+    VarlenTile vt;
+    if (!varlen_tile(s.cu, s.batch, s.total, s.seq, G::BW, blockIdx.x / s.heads, vt)) return;
+    b = vt.b;
+    qblk = vt.level;
+  } else {
+    int w = blockIdx.x;
+    if (s.tiles % 8 == 0) w = (w % 8) * (s.tiles / 8) + w / 8;
+    const int bh = w / s.blocks_per_head;
+    qblk = CAUSAL ? s.blocks_per_head - 1 - w % s.blocks_per_head : w % s.blocks_per_head;
+    b = bh / s.heads;
+    h = bh % s.heads;
+  }
+  const SeqSpan sp = seq_span<D>(s, b);
+  const int N = sp.n;
   const int64_t sn = s.st[2], kn = s.kst[2];
+  const int64_t base = b * s.st[0] + h * s.st[1] + int64_t(sp.start) * sn;
+  const int64_t kvbase =
+      b * s.kst[0] + (h / s.group) * s.kst[1] + int64_t(sp.start) * kn;  // KV head h / group
+  const int64_t stat = s.cu != nullptr ? int64_t(h) * s.total + sp.start
+                                       : (int64_t(b) * s.heads + h) * N;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, hi = lane >> 5;
   const int q0 = qblk * G::BW;
+  if (q0 >= N) return;  // varlen: past this sequence's end (uniform)
   const int wq0 = q0 + wave * G::LW;
   const int query = wq0 + l32;
 
@@ -477,13 +535,13 @@ attn_bwd_dq_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
     qf[kk] = query < N ? *reinterpret_cast<const i32x4*>(Q + off) : i32x4{0, 0, 0, 0};
     of[kk] = query < N ? *reinterpret_cast<const i32x4*>(dO + off) : i32x4{0, 0, 0, 0};
   }
-  const float lse_q = query < N ? lse[int64_t(bh) * N + query] : 0.f;
-  const float delta_q = query < N ? delta[int64_t(bh) * N + query] : 0.f;
+  const float lse_q = query < N ? lse[stat + query] : 0.f;
+  const float delta_q = query < N ? delta[stat + query] : 0.f;
 
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(K + kvbase), (short)0, s.kv_head_bytes, 0x00020000);
+      (void*)(K + kvbase), (short)0, sp.kv_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(V + kvbase), (short)0, s.kv_head_bytes, 0x00020000);
+      (void*)(V + kvbase), (short)0, sp.kv_bytes, 0x00020000);
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
   uint32_t k_src[G::DMA_PER_TILE], v_src[G::DMA_PER_TILE];
 #pragma unroll
@@ -652,8 +710,10 @@ attn_bwd_dq_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
 
 BwdShape make_shape(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
                     int64_t head_dim, const int64_t* q_strides, const int64_t* kv_strides,
-                    float sm_scale) {
+                    float sm_scale, const int32_t* cu_seqlens, int64_t total) {
   BwdShape s{};
+  s.cu = cu_seqlens;
+  s.total = (int)total;
   s.heads = (int)heads;
   s.seq = (int)seq;
   s.group = (int)(heads / kv_heads);
@@ -663,9 +723,12 @@ BwdShape make_shape(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
   }
   s.scale = sm_scale;
   s.scale_log2 = sm_scale * 1.4426950408889634f;
+  s.batch = (int)batch;
   s.blocks_per_head = (int)tk::cdiv(seq, 128);
-  s.tiles = (int)(s.blocks_per_head * batch * heads);
-  s.kv_tiles = (int)(s.blocks_per_head * batch * kv_heads);
+  const int64_t per_head = cu_seqlens != nullptr ? varlen_tiles(batch, total, seq, 128)
+                                                 : s.blocks_per_head * batch;
+  s.tiles = (int)(per_head * heads);
+  s.kv_tiles = (int)(per_head * kv_heads);
   s.head_bytes = (uint32_t)(((seq - 1) * q_strides[2] + head_dim) * 2);
   s.kv_head_bytes = (uint32_t)(((seq - 1) * kv_strides[2] + head_dim) * 2);
   return s;
@@ -712,9 +775,10 @@ void attn_bwd_dkdv_dma_launch(int dtype, const void* q, const void* k, const voi
                               const float* delta, int64_t batch, int64_t heads,
                               int64_t kv_heads, int64_t seq, int64_t head_dim,
                               const int64_t* q_strides, const int64_t* kv_strides,
-                              float sm_scale, bool causal, hipStream_t stream) {
-  const BwdShape s =
-      make_shape(batch, heads, kv_heads, seq, head_dim, q_strides, kv_strides, sm_scale);
+                              float sm_scale, bool causal, hipStream_t stream,
+                              const int32_t* cu_seqlens, int64_t total) {
+  const BwdShape s = make_shape(batch, heads, kv_heads, seq, head_dim, q_strides, kv_strides,
+                                sm_scale, cu_seqlens, total);
   TK_BWD_LAUNCH(s.kv_tiles, attn_bwd_dkdv_dma_kernel, (const T*)q, (const T*)k, (const T*)v,
                 (const T*)dout, (T*)dk, (T*)dv, lse, delta, s);
 }
@@ -724,9 +788,9 @@ void attn_bwd_dq_dma_launch(int dtype, const void* q, const void* k, const void*
                             int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
                             int64_t head_dim, const int64_t* q_strides,
                             const int64_t* kv_strides, float sm_scale, bool causal,
-                            hipStream_t stream) {
-  const BwdShape s =
-      make_shape(batch, heads, kv_heads, seq, head_dim, q_strides, kv_strides, sm_scale);
+                            hipStream_t stream, const int32_t* cu_seqlens, int64_t total) {
+  const BwdShape s = make_shape(batch, heads, kv_heads, seq, head_dim, q_strides, kv_strides,
+                                sm_scale, cu_seqlens, total);
   TK_BWD_LAUNCH(s.tiles, attn_bwd_dq_dma_kernel, (const T*)q, (const T*)k, (const T*)v,
                 (const T*)dout, (T*)dq, lse, delta, s);
 }

@@ -107,4 +107,98 @@ __device__ __forceinline__ float sum_with_partner(float x) {
   return __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
 }
 
+// ---- Variable-length batches ---------------------------------------------------------
+// Sequence b is rows cu[b] .. cu[b+1] of the packed tensors. Both offsets are clamped
+// into [0, total] (the end also to >= the start) and the length to seq, so no lengths
+// table can address rows outside the packed tensors.
+struct VarlenRows {
+  int start, n;
+};
+__device__ __forceinline__ VarlenRows varlen_rows(const int32_t* cu, int b, int total, int seq) {
+  const int start = min(max(cu[b], 0), total);
+  return {start, min(min(max(cu[b + 1], start), total) - start, seq)};
+}
+
+// Sum over the wave of v in [0, 2^bits): one ballot per bit, so the result is scalar.
+__device__ __forceinline__ int wave_sum_bits(int v, int bits) {
+  int sum = 0;
+  for (int k = 0; k < bits; ++k) sum += __popcll(__ballot((v >> k) & 1)) << k;
+  return sum;
+}
+
+// Heavy-first tile schedule of a variable-length batch, shared by every head. Sequence
+// b has nb_b = ceil(n_b / blk) blocks and contributes one tile to each level
+// 0 .. nb_b - 1; tiles are numbered from the top level down and by sequence within a
+// level, so tile 0 is the last block of the longest sequence and every sequence's
+// heaviest tiles start before any lighter ones. Tiles at levels >= j number
+// C(j) = sum_b max(0, nb_b - j): tile t is at the largest level j with C(j) > t
+// (binary search over the levels), and is the (t - C(j+1))-th sequence with
+// nb_b > j. The first 64 sequences' block counts stay in a register; longer batches
+// reload the offsets on each pass. The caller makes t wave-uniform; the results are
+// scalar. Returns false when t is past the last tile.
+struct VarlenTile {
+  int b, level;
+};
+__device__ __forceinline__ bool varlen_tile(const int32_t* cu, int batch, int total, int seq,
+                                            int blk, int t, VarlenTile& out) {
+  const int lane = threadIdx.x & 63;
+  const int levels = (seq + blk - 1) / blk;
+  const int bits = 32 - __builtin_clz(unsigned(levels));  // max(0, nb - j) <= levels
+  auto blocks = [&](int b) {
+    return b < batch ? (varlen_rows(cu, b, total, seq).n + blk - 1) / blk : 0;
+  };
+  const int nb0 = blocks(lane);
+  auto chunk = [&](int b0) { return b0 == 0 ? nb0 : blocks(b0 + lane); };
+  auto tiles_from = [&](int j) {
+    int c = 0;
+    for (int b0 = 0; b0 < batch; b0 += 64) c += wave_sum_bits(max(chunk(b0) - j, 0), bits);
+    return c;
+  };
+  if (t >= tiles_from(0)) return false;
+  int lo = 0, hi = levels, c_hi = 0;  // C(lo) > t >= C(hi) == c_hi
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    const int c = tiles_from(mid);
+    if (c > t) {
+      lo = mid;
+    } else {
+      hi = mid;
+      c_hi = c;
+    }
+  }
+  int r = t - c_hi;  // rank among the sequences with more than lo blocks
+  for (int b0 = 0; b0 < batch; b0 += 64) {
+    const bool has = chunk(b0) > lo;
+    const uint64_t m = __ballot(has);
+    const int c = __popcll(m);
+    if (r < c) {
+      const int below =
+          __builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0));
+      out.b = b0 + __builtin_ctzll(__ballot(has && below == r));
+      out.level = lo;
+      return true;
+    }
+    r -= c;
+  }
+  return false;
+}
+
+// Workgroups of a variable-length launch: w = tile * heads + i. Consecutive workgroups
+// take the heads of one tile, which the hardware deals round-robin over the 8 XCDs, so
+// every XCD gets an equal share of each level. With heads % 8 == 0, slot i maps to head
+// (i % 8) * (heads / 8) + i / 8: XCD x then holds heads x*heads/8 .. (x+1)*heads/8 - 1,
+// and a grouped-query group's heads share one L2.
+__device__ __forceinline__ int varlen_head(int w, int heads) {
+  const int i = w % heads;
+  return heads % 8 == 0 ? (i % 8) * (heads / 8) + i / 8 : i;
+}
+
+// Upper bound on the tiles of a variable-length batch: sum_b ceil(n_b / blk) is below
+// total / blk + batch for offsets that partition [0, total], and at most batch * levels.
+inline int64_t varlen_tiles(int64_t batch, int64_t total, int64_t seq, int64_t blk) {
+  const int64_t by_total = (total + blk - 1) / blk + batch;
+  const int64_t by_seq = batch * ((seq + blk - 1) / blk);
+  return by_total < by_seq ? by_total : by_seq;
+}
+
 }  // namespace tk_attn

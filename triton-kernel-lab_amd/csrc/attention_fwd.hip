@@ -41,8 +41,13 @@ using namespace tk_attn;
 constexpr int kThreads = 512;
 
 struct Shape {
-  int heads, seq;
+  int heads, seq;  // seq: the sequence length (varlen: the longest sequence)
   int group;  // query heads per KV head: K/V of head h are those of KV head h / group
+  // Variable-length batches (null for equal lengths): sequence b is the rows
+  // cu[b] .. cu[b+1] of a packed [total][head][dim] layout (the batch strides are 0),
+  // and the LSE is [head][total].
+  const int32_t* cu;
+  int total, batch;
   int64_t q[3], k[3], v[3], o[3];  // batch, head, sequence strides (elements)
   float scale_log2;
   int q_blocks, tiles;
@@ -93,19 +98,37 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
                 STB = G::STB, STAGES = G::STAGES;
   __shared__ __attribute__((aligned(1024))) char lds[STAGES * STB];
 
-  // Workgroup -> (batch*head, query block): XCD-contiguous ranges so a head's blocks share
-  // one L2; causal: the heaviest (last) query block of a head first.
-  int w = blockIdx.x;
-  if (s.tiles % 8 == 0) w = (w % 8) * (s.tiles / 8) + w / 8;
-  const int bh = w / s.q_blocks;
-  const int qb = CAUSAL ? s.q_blocks - 1 - w % s.q_blocks : w % s.q_blocks;
-  const int b = bh / s.heads, h = bh % s.heads;
+  // Workgroup -> (batch*head, query block). Equal lengths: XCD-contiguous ranges so a
+  // head's blocks share one L2; causal: the heaviest (last) query block of a head first.
+  // Varlen: the heavy-first schedule over every sequence's query blocks (level = query
+  // block), heads interleaved over the XCDs.
+  int b, h, qb, start = 0, N = s.seq;
+  uint32_t k_bytes = s.k_bytes, v_bytes = s.v_bytes;
+  if (s.cu != nullptr) {
+    h = varlen_head(blockIdx.x, s.heads);
+    VarlenTile vt;
+    if (!varlen_tile(s.cu, s.batch, s.total, s.seq, BM, blockIdx.x / s.heads, vt)) return;
+    b = vt.b;
+    qb = vt.level;
+    const VarlenRows rows = varlen_rows(s.cu, b, s.total, s.seq);
+    start = rows.start;
+    N = rows.n;
+    if (qb * BM >= N) return;  // uniform: the whole workgroup leaves
+    k_bytes = uint32_t(((N - 1) * s.k[2] + D) * 2);
+    v_bytes = uint32_t(((N - 1) * s.v[2] + D) * 2);
+  } else {
+    int w = blockIdx.x;
+    if (s.tiles % 8 == 0) w = (w % 8) * (s.tiles / 8) + w / 8;
+    const int bh = w / s.q_blocks;
+    qb = CAUSAL ? s.q_blocks - 1 - w % s.q_blocks : w % s.q_blocks;
+    b = bh / s.heads;
+    h = bh % s.heads;
+  }
   const int kvh = h / s.group;
-  const T* Qh = Q + b * s.q[0] + h * s.q[1];
-  const T* Kh = K + b * s.k[0] + kvh * s.k[1];
-  const T* Vh = V + b * s.v[0] + kvh * s.v[1];
-  T* Oh = O + b * s.o[0] + h * s.o[1];
-  const int N = s.seq;
+  const T* Qh = Q + b * s.q[0] + h * s.q[1] + int64_t(start) * s.q[2];
+  const T* Kh = K + b * s.k[0] + kvh * s.k[1] + int64_t(start) * s.k[2];
+  const T* Vh = V + b * s.v[0] + kvh * s.v[1] + int64_t(start) * s.v[2];
+  T* Oh = O + b * s.o[0] + h * s.o[1] + int64_t(start) * s.o[2];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -114,9 +137,9 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
   const int wq0 = q0 + wave * G::QW;
 
   const __amdgpu_buffer_rsrc_t rk =
-      __builtin_amdgcn_make_buffer_rsrc((void*)Kh, (short)0, s.k_bytes, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc((void*)Kh, (short)0, k_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rv =
-      __builtin_amdgcn_make_buffer_rsrc((void*)Vh, (short)0, s.v_bytes, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc((void*)Vh, (short)0, v_bytes, 0x00020000);
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
 
   // DMA sources (bytes from the head's base, block-relative row). Rows past the sequence
@@ -324,7 +347,11 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
         u.y = pack2<T>(acc[dt][g4 * 4 + 2] * inv, acc[dt][g4 * 4 + 3] * inv);
         *reinterpret_cast<uint2*>(orow + d) = u;
       }
-    if (lse != nullptr && hi == 0) lse[static_cast<int64_t>(bh) * N + query] = m_run + __log2f(l);
+    if (lse != nullptr && hi == 0) {
+      const int64_t at = s.cu != nullptr ? int64_t(h) * s.total + start + query
+                                         : (int64_t(b) * s.heads + h) * N + query;
+      lse[at] = m_run + __log2f(l);
+    }
   }
 }
 
@@ -359,11 +386,14 @@ void attn_fwd_dma_launch(int dtype, const void* q, const void* k, const void* v,
                          float* lse, int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
                          int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
                          const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
-                         bool causal, hipStream_t stream) {
+                         bool causal, hipStream_t stream, const int32_t* cu_seqlens,
+                         int64_t total) {
   Shape s{};
   s.heads = (int)heads;
   s.seq = (int)seq;
   s.group = (int)(heads / kv_heads);
+  s.cu = cu_seqlens;
+  s.total = (int)total;
   for (int i = 0; i < 3; ++i) {
     s.q[i] = q_strides[i];
     s.k[i] = k_strides[i];
@@ -371,8 +401,10 @@ void attn_fwd_dma_launch(int dtype, const void* q, const void* k, const void* v,
     s.o[i] = o_strides[i];
   }
   s.scale_log2 = sm_scale * 1.4426950408889634f;
+  s.batch = (int)batch;
   s.q_blocks = (int)cdiv(seq, 256);
-  s.tiles = (int)(s.q_blocks * batch * heads);
+  s.tiles = cu_seqlens != nullptr ? (int)(varlen_tiles(batch, total, seq, 256) * heads)
+                                  : (int)(s.q_blocks * batch * heads);
   s.k_bytes = (uint32_t)head_extent_bytes(seq, head_dim, k_strides[2]);
   s.v_bytes = (uint32_t)head_extent_bytes(seq, head_dim, v_strides[2]);
   const dim3 grid(static_cast<unsigned>(s.tiles));

@@ -70,6 +70,18 @@ _SIGNATURES: dict[str, list[object]] = {
         _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _F32, _I32,
         _P,
     ],
+    "tk_attn_fwd_varlen": [
+        _I32, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _I64P,
+        _F32, _I32, _P,
+    ],
+    "tk_attn_bwd_dkdv_varlen": [
+        _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64P,
+        _I64P, _F32, _I32, _P,
+    ],
+    "tk_attn_bwd_dq_varlen": [
+        _I32, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P,
+        _F32, _I32, _P,
+    ],
     "tk_vector_add": [_I32, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "tk_activation_fwd": [_I32, _I32, _P, _P, _I64, _I64, _I64, _I64, _P],
     "tk_activation_bwd": [_I32, _I32, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P],

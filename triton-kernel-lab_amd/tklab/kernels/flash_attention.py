@@ -15,7 +15,9 @@ The registry keeps the reference's spec shape (batch 1, 16 heads, head_dim
 ``grouped_query_attention(q, k, v, *, causal)`` extends the same kernels to K/V
 with fewer heads than Q (query head ``h`` uses KV head ``h // (heads //
 kv_heads)``), forward and backward; dK/dV sum a KV head's query heads in a fixed
-order, so the backward stays deterministic.
+order, so the backward stays deterministic. ``varlen_attention(q, k, v,
+cu_seqlens, max_seqlen, *, causal)`` runs them on variable-length batches packed
+as ``(total, heads, head_dim)`` with int32 sequence offsets ``cu_seqlens``.
 """
 
 from __future__ import annotations
@@ -368,6 +370,140 @@ def grouped_query_attention(
         _launch_gqa_forward(q, k, v, output, None, causal=causal)
         return output
     return cast(torch.Tensor, _GQAFunction.apply(q, k, v, causal))
+
+
+def _validate_varlen(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int
+) -> None:
+    """Packed variable-length contract: (total, heads, head_dim) tensors and offsets."""
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+        raise ValueError("varlen attention expects Q, K, and V shaped (total, heads, dim)")
+    if k.shape != v.shape:
+        raise ValueError("K and V must have identical shapes")
+    if q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError("Q and K/V must agree on total tokens and head_dim")
+    if 0 in q.shape or 0 in k.shape:
+        raise ValueError("attention does not support empty dimensions")
+    if q.shape[1] % k.shape[1]:
+        raise ValueError("the number of Q heads must be a multiple of the K/V heads")
+    if q.device != k.device or q.device != v.device or cu_seqlens.device != q.device:
+        raise ValueError("Q, K, V and cu_seqlens must be on the same device")
+    if q.device.type != "cuda":
+        raise ValueError("attention requires CUDA (ROCm/HIP) tensors")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError("Q, K, and V must have the same dtype")
+    if q.dtype not in _DTYPES:
+        raise ValueError("attention supports float16 and bfloat16 inputs only")
+    if q.shape[-1] not in _HEAD_DIMS:
+        raise ValueError(f"attention requires head_dim in {_HEAD_DIMS}")
+    if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2 or cu_seqlens.dtype != torch.int32:
+        raise ValueError("cu_seqlens must be an int32 vector of batch + 1 offsets")
+    if not cu_seqlens.is_contiguous():
+        raise ValueError("cu_seqlens must be contiguous")
+    if not 1 <= max_seqlen <= q.shape[0]:
+        raise ValueError("max_seqlen must be in [1, total]")
+    for name, tensor in (("Q", q), ("K", k), ("V", v)):
+        if not tensor.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+        assert_int32_addressable(tensor, name=name)
+
+
+def _launch_varlen_forward(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
+    max_seqlen: int, output: torch.Tensor, softmax_lse: torch.Tensor | None, *, causal: bool,
+) -> None:
+    """Varlen forward into preallocated buffers (``softmax_lse`` [heads, total] or None)."""
+    total, heads, head_dim = q.shape
+    _hip.call(
+        "tk_attn_fwd_varlen", _hip.dtype_code(q.dtype), q.data_ptr(), k.data_ptr(),
+        v.data_ptr(), output.data_ptr(), _hip.ptr(softmax_lse), cu_seqlens.data_ptr(),
+        cu_seqlens.numel() - 1, heads, k.shape[1], max_seqlen, total, head_dim,
+        _hip.int64_array(list(q.stride()[:2])), _hip.int64_array(list(k.stride()[:2])),
+        _hip.int64_array(list(output.stride()[:2])), 1.0 / math.sqrt(head_dim), int(causal),
+        _hip.stream_of(q),
+    )
+
+
+def _launch_varlen_backward(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
+    max_seqlen: int, output: torch.Tensor, softmax_lse: torch.Tensor, do: torch.Tensor,
+    *, causal: bool,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Varlen backward: delta [heads, total], dK/dV per KV head, dQ per query head."""
+    if do.shape != q.shape or do.device != q.device or do.dtype != q.dtype:
+        raise ValueError("attention upstream gradient metadata must match Q")
+    do = do.contiguous()
+    total, heads, head_dim = q.shape
+    batch = cu_seqlens.numel() - 1
+    code = _hip.dtype_code(q.dtype)
+    stream = _hip.stream_of(q)
+    scale = 1.0 / math.sqrt(head_dim)
+    delta = torch.empty((heads, total), dtype=torch.float32, device=q.device)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    # delta as one sequence of `total` rows: index head * total + token.
+    token, head = q.stride(0), q.stride(1)
+    _hip.call("tk_attn_bwd_preprocess", code, output.data_ptr(), do.data_ptr(), delta.data_ptr(),
+              1, heads, total, head_dim, _hip.int64_array([total * token, head, token]), stream)
+    qs = _hip.int64_array([token, head])
+    kvs = _hip.int64_array(list(k.stride()[:2]))
+    _hip.call("tk_attn_bwd_dkdv_varlen", code, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+              do.data_ptr(), dk.data_ptr(), dv.data_ptr(), softmax_lse.data_ptr(),
+              delta.data_ptr(), cu_seqlens.data_ptr(), batch, heads, k.shape[1], max_seqlen,
+              total, head_dim, qs, kvs, scale, int(causal), stream)
+    _hip.call("tk_attn_bwd_dq_varlen", code, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+              do.data_ptr(), dq.data_ptr(), softmax_lse.data_ptr(), delta.data_ptr(),
+              cu_seqlens.data_ptr(), batch, heads, k.shape[1], max_seqlen, total, head_dim, qs,
+              kvs, scale, int(causal), stream)
+    return dq, dk, dv
+
+
+class _VarlenFunction(torch.autograd.Function):
+    """Autograd bridge of varlen attention: saves Q, K, V, O, the offsets and the LSE."""
+
+    @staticmethod
+    def forward(
+        ctx: Any, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
+        max_seqlen: int, causal: bool,
+    ) -> torch.Tensor:
+        output = torch.empty_like(q)
+        softmax_lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32,
+                                  device=q.device)
+        _launch_varlen_forward(q, k, v, cu_seqlens, max_seqlen, output, softmax_lse,
+                               causal=causal)
+        ctx.save_for_backward(q, k, v, cu_seqlens, output, softmax_lse)
+        ctx.max_seqlen = max_seqlen
+        ctx.causal = causal
+        return output
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx: Any, do: torch.Tensor) -> tuple[Any, ...]:
+        q, k, v, cu_seqlens, output, softmax_lse = ctx.saved_tensors
+        dq, dk, dv = _launch_varlen_backward(q, k, v, cu_seqlens, ctx.max_seqlen, output,
+                                             softmax_lse, do, causal=ctx.causal)
+        return dq, dk, dv, None, None, None
+
+
+def varlen_attention(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
+    max_seqlen: int, *, causal: bool,
+) -> torch.Tensor:
+    """Attention over a variable-length batch packed along the token axis.
+
+    ``q`` is ``(total, heads, head_dim)``, ``k`` and ``v`` ``(total, kv_heads,
+    head_dim)`` (``heads % kv_heads == 0``); sequence ``b`` is tokens
+    ``cu_seqlens[b]`` .. ``cu_seqlens[b + 1]`` (int32, on the device) and attends
+    only to itself; ``max_seqlen`` is the longest sequence. Each sequence gets
+    exactly the result :func:`grouped_query_attention` gives it alone, with
+    autograd (first order).
+    """
+    _validate_varlen(q, k, v, cu_seqlens, max_seqlen)
+    needs_grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
+    if not needs_grad:
+        output = torch.empty_like(q)
+        _launch_varlen_forward(q, k, v, cu_seqlens, max_seqlen, output, None, causal=causal)
+        return output
+    return cast(torch.Tensor, _VarlenFunction.apply(q, k, v, cu_seqlens, max_seqlen, causal))
 
 
 def _reference_factory(*, causal: bool) -> TensorFn:
