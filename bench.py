@@ -437,6 +437,33 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
 
     rows[-1]["unfused_ms"] = round(timed(unfused, 5), 4)
     del xm, wgm, wum, ym, gm, um
+    # Config 2 feeding its consumer: residual-RMSNorm then the grouped-query QKV
+    # projection, x, r [16384, 4096] @ W [4096, 6144] (32 query + 2 x 8 KV heads of 128):
+    # statistics pass + row-scaled GEMM on the folded weight (GEMM FLOPs);
+    # `unfused_ms` is tk_rmsnorm_fwd writing s and y, then tk_gemm on y.
+    from tklab.kernels import residual_rms_norm as rrn
+    from tklab.kernels import rms_norm_matmul as rnm
+
+    xq, rq = (torch.randn(16384, 4096, device=device, dtype=bf16, generator=g) for _ in range(2))
+    wn = (1 + 0.02 * torch.randn(4096, device=device, generator=g)).to(bf16)
+    wq = (torch.randn(4096, 6144, device=device, generator=g) * 4096 ** -0.5).to(bf16)
+    wf = rnm.fold_norm_weight(wn, wq)
+    mfma_row("residual_rms_norm_matmul (tk_rmsnorm_fwd stats + tk_gemm_rowscale)",
+             "bf16 16384x6144x4096, residual add + RMSNorm in front",
+             lambda: rnm.residual_rms_norm_matmul(xq, rq, wf, eps=1e-6),
+             2 * 16384 * 6144 * 4096, "bfloat16", reps=5)
+    sq, yq = torch.empty_like(xq), torch.empty_like(xq)
+    rstdq = torch.empty(16384, device=device, dtype=torch.float32)
+    cq = torch.empty(16384, 6144, device=device, dtype=bf16)
+
+    def unfused_norm_gemm():
+        rrn._launch_forward(xq, rq, wn, sq, yq, rstdq, eps=1e-6, store_residual=True,
+                            store_stats=True)
+        mm._launch_fp32acc((yq, wq), cq)
+
+    rows[-1]["unfused_ms"] = round(timed(unfused_norm_gemm, 5), 4)
+    rows[-1]["fold_ms"] = round(timed(lambda: rnm.fold_norm_weight(wn, wq), 5), 4)
+    del xq, rq, wq, wf, sq, yq, cq
     # Config 5: attention.
     for causal, nctx, d in ((True, 8192, 128), (False, 4096, 128), (True, 8192, 64), (False, 4096, 64)):
         shape = (4, 32, nctx, d)

@@ -62,7 +62,9 @@ int tk_softmax_online_fwd(int dtype, const void* x, void* y, float* partials, in
  *   s = residual ? round_dtype(x + residual) : x
  *   rstd = 1 / sqrt(mean(s^2) + eps);  y = s * rstd * weight
  * `residual`, `residual_sum` (written when non-null) and `rstd` (float32[rows],
- * written when non-null) may be NULL.
+ * written when non-null) may be NULL. `y` may be NULL when `rstd` is not
+ * (statistics mode: only s and rstd are written and `weight` is not read; the
+ * statistics pass of tk_gemm_rowscale's normalized GEMM).
  * Replaces `_rms_norm_forward_kernel[(rows,)]`, src/tklab/kernels/rms_norm.py:248-260,
  * and `_residual_rms_norm_forward_kernel[(rows,)]`,
  * src/tklab/kernels/residual_rms_norm.py:149-167. cols * sizeof(dtype) <= 65536. */
@@ -149,6 +151,28 @@ int tk_gemm_swiglu(int dtype, const void* a, const void* b_gate, const void* b_u
                    int64_t m, int64_t n, int64_t k, int64_t stride_am, int64_t stride_ak,
                    int64_t stride_gk, int64_t stride_gn, int64_t stride_uk, int64_t stride_un,
                    int64_t stride_ym, int64_t stride_yn, void* stream);
+
+/* GEMM with a per-row float32 scale in its epilogue:
+ *   c[i, :] = round_dtype(row_scale[i] * (a * b)[i, :])   (float32 accumulation)
+ * The normalized GEMM rms_norm(s; w) * W = diag(rstd) * s * (diag(w) * W): with
+ * row_scale = rstd from tk_rmsnorm_fwd's statistics mode and b = tk_scale_rows(W, w)
+ * (the norm weight folded into the projection once per weight version), the
+ * normalized activations are never written. No reference kernel exists: the
+ * reference lists the residual-RMSNorm -> projection fusion among its next steps
+ * around src/tklab/kernels/residual_rms_norm.py:28-82 and matmul.py:72-164.
+ * Operand requirements are tk_gemm_swiglu's (otherwise non-zero status: compose
+ * tk_rmsnorm_fwd and tk_gemm). dtype TK_DTYPE_F16 or TK_DTYPE_BF16. */
+int tk_gemm_rowscale(int dtype, const void* a, const void* b, const float* row_scale, void* c,
+                     int64_t m, int64_t n, int64_t k, int64_t stride_am, int64_t stride_ak,
+                     int64_t stride_bk, int64_t stride_bn, int64_t stride_cm, int64_t stride_cn,
+                     void* stream);
+
+/* Row scaling y[r, c] = round_dtype(x[r, c] * scale[r]) for x, y [rows, cols]
+ * (unit column stride) and scale[rows] in the same dtype: folds a normalization
+ * weight into the projection that follows it (see tk_gemm_rowscale). Helper of
+ * that fusion; no reference counterpart. */
+int tk_scale_rows(int dtype, const void* x, const void* scale, void* y, int64_t rows,
+                  int64_t cols, int64_t x_row_stride, int64_t y_row_stride, void* stream);
 
 /* Flash attention forward over q/k/v/o[batch][heads][seq][head_dim]
  * (head_dim unit-stride; strides given for batch, head and seq), head_dim in

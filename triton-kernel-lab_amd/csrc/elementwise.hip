@@ -1,5 +1,5 @@
-// Elementwise kernels: SwiGLU forward/backward and rotate-half RoPE
-// forward/backward.
+// Elementwise kernels: SwiGLU forward/backward, rotate-half RoPE forward/backward, and
+// row scaling (folding a normalization weight into a projection).
 //
 // A chunk is VEC contiguous elements (VEC = 16/sizeof(T): one 128-bit access per
 // tensor). A workgroup pass takes kUnroll * kBlock consecutive chunks; each thread
@@ -220,6 +220,37 @@ __global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
   }
 }
 
+// ------------------------------------------------------------------ row scaling
+
+// y[r, c] = x[r, c] * scale[r], one float32 product rounded to T: folds a normalization
+// weight into the rows of the projection that follows it (W'[k, :] = w[k] * W[k, :]).
+template <typename T, int VEC>
+__global__ __launch_bounds__(kBlock) void scale_rows_kernel(
+    const T* __restrict__ x, const T* __restrict__ scale, T* __restrict__ y, int chunks,
+    tk::FastDiv per_row, int64_t xs, int64_t ys) {
+  const int stride = gridDim.x * kBlock * kUnroll;
+  for (int i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
+    float v[kUnroll][VEC], sc[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = i0 + u * kBlock;
+      if (i >= chunks) break;
+      const ChunkPos p = chunk_pos<VEC>(i, per_row);
+      tk::load_vec_stream<T, VEC>(x + p.row * xs + p.col, v[u]);
+      sc[u] = tk::to_f32(scale[p.row]);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int i = i0 + u * kBlock;
+      if (i >= chunks) break;
+      const ChunkPos p = chunk_pos<VEC>(i, per_row);
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) v[u][j] = v[u][j] * sc[u];
+      tk::store_vec_stream<T, VEC>(y + p.row * ys + p.col, v[u]);
+    }
+  }
+}
+
 bool vector_ok(int dtype, int64_t width, std::initializer_list<const void*> ptrs,
                std::initializer_list<int64_t> strides) {
   const int es = tk::elem_size(dtype);
@@ -361,4 +392,24 @@ extern "C" int tk_rope_bwd(int dtype, const void* dy, const void* x, const void*
                          cos_row_stride, sin_row_stride, dx_row_stride, dcos_row_stride,
                          dsin_row_stride)));
   return tk::check_launch("rope_bwd");
+}
+
+extern "C" int tk_scale_rows(int dtype, const void* x, const void* scale, void* y, int64_t rows,
+                             int64_t cols, int64_t x_row_stride, int64_t y_row_stride,
+                             void* stream) {
+  if (x == nullptr || scale == nullptr || y == nullptr) return tk::fail("scale_rows: null pointer");
+  const bool vok = tk::valid_dtype(dtype) &&
+                   vector_ok(dtype, cols, {x, y}, {x_row_stride, y_row_stride});
+  const int vec = vok ? 16 / tk::elem_size(dtype) : 1;
+  int64_t per_row, chunks;
+  if (check_problem("scale_rows", dtype, rows, cols, vec, &per_row, &chunks)) return 1;
+  const tk::FastDiv div(static_cast<uint32_t>(per_row));
+  const Grid1D g = chunk_grid(chunks);
+  hipStream_t s = tk::as_stream(stream);
+  TK_DISPATCH_DTYPE(dtype, T,
+    TK_DISPATCH_VEC(T, vok,
+      hipLaunchKernelGGL((scale_rows_kernel<T, VEC>), dim3(g.blocks), dim3(kBlock), 0, s,
+                         static_cast<const T*>(x), static_cast<const T*>(scale),
+                         static_cast<T*>(y), (int)chunks, div, x_row_stride, y_row_stride)));
+  return tk::check_launch("scale_rows");
 }

@@ -320,3 +320,25 @@ extern "C" int tk_gemm_swiglu(int dtype, const void* a, const void* b_gate, cons
                              stride_ym, stride_yn, tk::as_stream(stream));
   return tk::check_launch("gemm_swiglu");
 }
+
+extern "C" int tk_gemm_rowscale(int dtype, const void* a, const void* b, const float* row_scale,
+                                void* c, int64_t m, int64_t n, int64_t k, int64_t stride_am,
+                                int64_t stride_ak, int64_t stride_bk, int64_t stride_bn,
+                                int64_t stride_cm, int64_t stride_cn, void* stream) {
+  if (dtype != TK_DTYPE_F16 && dtype != TK_DTYPE_BF16)
+    return tk::fail("gemm_rowscale: dtype must be float16 or bfloat16");
+  if (a == nullptr || b == nullptr || row_scale == nullptr || c == nullptr)
+    return tk::fail("gemm_rowscale: null pointer");
+  if (m <= 0 || n <= 0 || k <= 0) return tk::fail("gemm_rowscale: empty problem");
+  if (stride_cm <= 0 || stride_cn <= 0) return tk::fail("gemm_rowscale: strides must be positive");
+  const int64_t lim = INT32_MAX;
+  if (m > lim || n > lim || k > lim || (m - 1) * stride_cm + (n - 1) * stride_cn > lim)
+    return tk::fail("gemm_rowscale: operand exceeds the int32 offset range");
+  if (!tk::gemm_dma_applies(a, b, m, n, k, stride_am, stride_ak, stride_bk, stride_bn))
+    return tk::fail("gemm_rowscale: needs unit inner strides, 16-byte aligned rows, k %% 32 == 0, "
+                    "n %% 8 == 0 and operands below 2 GiB");
+  if (tk::cdiv(m, BM) * tk::cdiv(n, BN) > INT32_MAX) return tk::fail("gemm_rowscale: too many tiles");
+  tk::gemm_dma_launch(dtype, a, b, c, m, n, k, stride_am, stride_bk, stride_cm, stride_cn,
+                      tk::as_stream(stream), row_scale);
+  return tk::check_launch("gemm_rowscale");
+}

@@ -11,10 +11,11 @@ namespace tk {
 bool gemm_dma_applies(const void* a, const void* b, int64_t m, int64_t n, int64_t k,
                       int64_t stride_am, int64_t stride_ak, int64_t stride_bk, int64_t stride_bn);
 
-// Enqueues the DMA kernel; arguments are checked by the caller.
+// Enqueues the DMA kernel; arguments are checked by the caller. With `row_scale`
+// (float32[m]) row m of C is round(row_scale[m] * acc).
 void gemm_dma_launch(int dtype, const void* a, const void* b, void* c, int64_t m, int64_t n,
                      int64_t k, int64_t stride_am, int64_t stride_bk, int64_t stride_cm,
-                     int64_t stride_cn, hipStream_t stream);
+                     int64_t stride_cn, hipStream_t stream, const float* row_scale = nullptr);
 
 // Enqueues the SwiGLU-fused DMA kernel: y = swiglu(value = a * b_up, gate = a * b_gate),
 // both weights [K, N] row-major; each must satisfy gemm_dma_applies with `a`.

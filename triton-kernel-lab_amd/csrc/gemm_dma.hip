@@ -31,6 +31,11 @@
 // Tile order: workgroup w runs on XCD w % 8; tiles are renumbered so each XCD walks a
 // contiguous range in groups of 4 M-tiles, sharing A and B panels in that XCD's L2.
 //
+// Row-scaled variant (kRowScale): C[m, :] = round(s[m] * acc),
+// one float32 multiply before the rounding. With s = rstd of a normalization whose
+// weight is folded into B, this is the normalized GEMM rms_norm(a) * B' without the
+// normalized activations ever being written.
+//
 // SwiGLU variant (kSwiGLU): Y = swiglu(value = A*B_up, gate = A*B_gate) for two weights
 // [K, N]. A block computes 256 x 128 of Y from a 256-column B tile holding the gate
 // columns n0..n0+127 then the same up columns, laid out in LDS as two 128-column blocks
@@ -90,6 +95,7 @@ struct Problem {
   int64_t scm, scn;
   int tiles_m, tiles_n;
   uint32_t a_bytes, b_bytes, b2_bytes;
+  const float* row_scale;  // kRowScale: C[m, :] = round(row_scale[m] * acc)
 };
 
 template <int N>
@@ -161,7 +167,7 @@ __device__ __forceinline__ T swiglu_out(float gate_acc, float up_acc) {
   return tk::from_f32<T>(v * g * tk::stable_sigmoid(g));
 }
 
-template <typename T, bool kSwiGLU>
+template <typename T, bool kSwiGLU, bool kRowScale>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(2, 2))) void
 gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ B2,
@@ -220,6 +226,13 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
   }
   const uint32_t b_tile_bytes = uint32_t(BK * ldb) * 2u;
   const int kt = p.k / BK;
+
+  // Row-scaled variant: thread t < 256 fetches the scale of tile row t (rows past M
+  // clamp to row M - 1 and are never stored) before the first DMA, so the load has
+  // landed long before the epilogue; one register through the main loop.
+  float row_scale = 0.f;
+  if constexpr (kRowScale)
+    if (threadIdx.x < BM) row_scale = p.row_scale[min(m0 + (int)threadIdx.x, p.m - 1)];
 
   // DMA x (0..3: two A loads, two B loads) of K tile `tile` into ring slot `slot`. Tiles past the end reload the
   // last tile into a slot that is never read again, so every step issues the same number
@@ -342,8 +355,27 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
       }
     }
   } else {
+    // Row-scaled variant: the tile's 256 scales go through the (now idle) LDS, thread t
+    // writing the one it fetched at entry; a lane then reads its rows in groups of 4.
+    const float* scales = reinterpret_cast<const float*>(lds);
+    if constexpr (kRowScale) {
+      __syncthreads();  // every wave is done reading the last K tile
+      if (threadIdx.x < BM) reinterpret_cast<float*>(lds)[threadIdx.x] = row_scale;
+      __syncthreads();
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      float sc[16];
+      if constexpr (kRowScale) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const float4 q = *reinterpret_cast<const float4*>(scales + wm + i * 32 + g4 * 8 + lhalf * 4);
+          sc[g4 * 4 + 0] = q.x;
+          sc[g4 * 4 + 1] = q.y;
+          sc[g4 * 4 + 2] = q.z;
+          sc[g4 * 4 + 3] = q.w;
+        }
+      }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int n = n0 + wn + j * 32 + lrow;
@@ -351,7 +383,8 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int m = m0 + wm + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-          if (m < p.m) C[m * p.scm + n * p.scn] = tk::from_f32<T>(acc[i][j][r]);
+          const float v = kRowScale ? acc[i][j][r] * sc[r] : acc[i][j][r];
+          if (m < p.m) C[m * p.scm + n * p.scn] = tk::from_f32<T>(v);
         }
       }
     }
@@ -375,7 +408,7 @@ bool gemm_dma_applies(const void* a, const void* b, int64_t m, int64_t n, int64_
 
 void gemm_dma_launch(int dtype, const void* a, const void* b, void* c, int64_t m, int64_t n,
                      int64_t k, int64_t stride_am, int64_t stride_bk, int64_t stride_cm,
-                     int64_t stride_cn, hipStream_t stream) {
+                     int64_t stride_cn, hipStream_t stream, const float* row_scale) {
   const uint32_t b_bytes = (uint32_t)(((k - 1) * stride_bk + n) * 2);
   Problem p{(int)m,
             (int)n,
@@ -389,16 +422,30 @@ void gemm_dma_launch(int dtype, const void* a, const void* b, void* c, int64_t m
             (int)cdiv(n, BN),
             (uint32_t)(((m - 1) * stride_am + k) * 2),
             b_bytes,
-            b_bytes};
+            b_bytes,
+            row_scale};
   const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
-  if (dtype == TK_DTYPE_F16)
-    hipLaunchKernelGGL((gemm_dma_kernel<_Float16, false>), grid, dim3(kThreads), 0, stream,
-                       static_cast<const _Float16*>(a), static_cast<const _Float16*>(b),
-                       static_cast<const _Float16*>(b), static_cast<_Float16*>(c), p);
-  else
-    hipLaunchKernelGGL((gemm_dma_kernel<__bf16, false>), grid, dim3(kThreads), 0, stream,
-                       static_cast<const __bf16*>(a), static_cast<const __bf16*>(b),
-                       static_cast<const __bf16*>(b), static_cast<__bf16*>(c), p);
+  if (dtype == TK_DTYPE_F16) {
+    using T = _Float16;
+    if (row_scale != nullptr)
+      hipLaunchKernelGGL((gemm_dma_kernel<T, false, true>), grid, dim3(kThreads), 0, stream,
+                         static_cast<const T*>(a), static_cast<const T*>(b),
+                         static_cast<const T*>(b), static_cast<T*>(c), p);
+    else
+      hipLaunchKernelGGL((gemm_dma_kernel<T, false, false>), grid, dim3(kThreads), 0, stream,
+                         static_cast<const T*>(a), static_cast<const T*>(b),
+                         static_cast<const T*>(b), static_cast<T*>(c), p);
+  } else {
+    using T = __bf16;
+    if (row_scale != nullptr)
+      hipLaunchKernelGGL((gemm_dma_kernel<T, false, true>), grid, dim3(kThreads), 0, stream,
+                         static_cast<const T*>(a), static_cast<const T*>(b),
+                         static_cast<const T*>(b), static_cast<T*>(c), p);
+    else
+      hipLaunchKernelGGL((gemm_dma_kernel<T, false, false>), grid, dim3(kThreads), 0, stream,
+                         static_cast<const T*>(a), static_cast<const T*>(b),
+                         static_cast<const T*>(b), static_cast<T*>(c), p);
+  }
 }
 
 void gemm_swiglu_dma_launch(int dtype, const void* a, const void* b_gate, const void* b_up,
@@ -417,14 +464,15 @@ void gemm_swiglu_dma_launch(int dtype, const void* a, const void* b_gate, const 
             (int)cdiv(n, 128),
             (uint32_t)(((m - 1) * stride_am + k) * 2),
             (uint32_t)(((k - 1) * stride_gk + n) * 2),
-            (uint32_t)(((k - 1) * stride_uk + n) * 2)};
+            (uint32_t)(((k - 1) * stride_uk + n) * 2),
+            nullptr};
   const dim3 grid(static_cast<unsigned>(p.tiles_m * p.tiles_n));
   if (dtype == TK_DTYPE_F16)
-    hipLaunchKernelGGL((gemm_dma_kernel<_Float16, true>), grid, dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL((gemm_dma_kernel<_Float16, true, false>), grid, dim3(kThreads), 0, stream,
                        static_cast<const _Float16*>(a), static_cast<const _Float16*>(b_gate),
                        static_cast<const _Float16*>(b_up), static_cast<_Float16*>(y), p);
   else
-    hipLaunchKernelGGL((gemm_dma_kernel<__bf16, true>), grid, dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL((gemm_dma_kernel<__bf16, true, false>), grid, dim3(kThreads), 0, stream,
                        static_cast<const __bf16*>(a), static_cast<const __bf16*>(b_gate),
                        static_cast<const __bf16*>(b_up), static_cast<__bf16*>(y), p);
 }

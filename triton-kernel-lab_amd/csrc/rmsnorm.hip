@@ -68,14 +68,18 @@ __global__ __launch_bounds__(RT >= kNormBlock ? RT : kNormBlock) void rmsnorm_fw
   ss = tk::group_allreduce<RT>(ss, tk::SumOp{}, scratch);
   const float rstd = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
 
-  Row wv;
-  wv.load(weight, cols, lane);
+  // Statistics mode (y null): only s and rstd are produced, for a consumer that applies
+  // rstd and the weight itself (the row-scaled GEMM).
+  if (y != nullptr) {
+    Row wv;
+    wv.load(weight, cols, lane);
 #pragma unroll
-  for (int e = 0; e < VALS; ++e) wv.set(e, sv.get(e) * rstd * wv.get(e));
-  if constexpr (kBuf)
-    wv.template store_buf<tk::kCpolSc1>(y + row * y_stride, cols, lane);
-  else
-    wv.store(y + row * y_stride, cols, lane);
+    for (int e = 0; e < VALS; ++e) wv.set(e, sv.get(e) * rstd * wv.get(e));
+    if constexpr (kBuf)
+      wv.template store_buf<tk::kCpolSc1>(y + row * y_stride, cols, lane);
+    else
+      wv.store(y + row * y_stride, cols, lane);
+  }
   if (rstd_out != nullptr && lane == 0) rstd_out[row] = rstd;
 }
 
@@ -328,7 +332,8 @@ extern "C" int tk_rmsnorm_fwd(int dtype, const void* x, const void* residual, co
                               int64_t x_row_stride, int64_t residual_row_stride,
                               int64_t residual_sum_row_stride, int64_t y_row_stride, float eps,
                               void* stream) {
-  if (x == nullptr || weight == nullptr || y == nullptr) return tk::fail("rmsnorm_fwd: null pointer");
+  if (x == nullptr || (y != nullptr && weight == nullptr) || (y == nullptr && rstd == nullptr))
+    return tk::fail("rmsnorm_fwd: null pointer");
   if (!(eps > 0.f)) return tk::fail("rmsnorm_fwd: eps must be finite and positive");
   const bool vector_ok = tk::valid_dtype(dtype) && rows_vector_ok(
       dtype, cols, {x, residual, weight, residual_sum, y},

@@ -45,6 +45,8 @@ _SIGNATURES: dict[str, list[object]] = {
         _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P,
     ],
     "tk_gemm": [_I32, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P],
+    "tk_gemm_rowscale": [_I32, _P, _P, _P, _P] + [_I64] * 9 + [_P],
+    "tk_scale_rows": [_I32, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "tk_gemm_swiglu": [
         _I32, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P,
     ],
