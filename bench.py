@@ -496,7 +496,24 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
     mfma_row("tk_attn_bwd_gqa (preprocess+dkdv+dq)", tag + ", 2.5x fwd FLOPs",
              lambda: fa._launch_gqa_backward(qq, kk, vv, o, lse, do, causal=True),
              int(2.5 * flops), "bfloat16", reps=5)
-    del qq, kk, vv, do, o, lse
+    # RoPE in the attention prologue: position tables [8192, 64] (base 1e4); Q rotated
+    # as the forward loads it, K rotated once into a workspace. `unfused_ms` is the RoPE
+    # kernel on Q and on K, then the plain forward on the rotated tensors.
+    inv_f = 10000.0 ** (-torch.arange(64, dtype=torch.float32) / 64)
+    ang = torch.arange(8192, dtype=torch.float32)[:, None] * inv_f[None]
+    rcos, rsin = ang.cos().to(bf16).to(device), ang.sin().to(bf16).to(device)
+    kr, qr = torch.empty_like(kk), torch.empty_like(qq)
+    mfma_row("tk_attn_fwd_rope", tag + ", RoPE on Q (prologue) and K",
+             lambda: fa._launch_rope_forward(qq, kk, vv, rcos, rsin, o, lse, kr, causal=True),
+             flops, "bfloat16", reps=5)
+
+    def unfused_rope():
+        fa._rope_positions(qq, rcos, rsin, qr, inverse=False)
+        fa._rope_positions(kk, rcos, rsin, kr, inverse=False)
+        fa._launch_gqa_forward(qr, kr, vv, o, lse, causal=True)
+
+    rows[-1]["unfused_ms"] = round(timed(unfused_rope, 5), 4)
+    del qq, kk, vv, do, o, lse, kr, qr
     # Variable-length causal attention: one packed batch of 32768 tokens in sequences of
     # 8192, 2 x 4096, 4 x 2048 and 8 x 1024 (H32 Hkv8 D128); FLOPs summed per sequence.
     lengths = [8192] + [4096] * 2 + [2048] * 4 + [1024] * 8

@@ -125,6 +125,17 @@ int tk_rope_bwd(int dtype, const void* dy, const void* x, const void* cos, const
                 int64_t sin_row_stride, int64_t dx_row_stride, int64_t dcos_row_stride,
                 int64_t dsin_row_stride, void* stream);
 
+/* Rotate-half RoPE over `rows` rows of [batch, heads, seq, D] (uniform row strides)
+ * with position-indexed tables cos/sin [>= seq][D/2] (row stride table_row_stride):
+ * row r uses table row r mod seq. inverse == 0: tk_rope_fwd's arithmetic; inverse != 0:
+ * the input gradient, tk_rope_bwd's dx (RoPE with -sin). No reference counterpart:
+ * the reference's tables are per row (src/tklab/kernels/rope.py:213-225); this is the
+ * position-indexed form the attention prologue uses (see tk_attn_fwd_rope). */
+int tk_rope_positions(int dtype, const void* x, const void* cos, const void* sin, void* y,
+                      int64_t rows, int64_t seq, int64_t half_dim, int64_t x_row_stride,
+                      int64_t table_row_stride, int64_t y_row_stride, int inverse,
+                      void* stream);
+
 /* GEMM C[M][N] = A[M][K] * B[K][N] on MFMA, float32 accumulation, C stored in
  * `dtype` (TK_DTYPE_F16 or TK_DTYPE_BF16). All strides are element strides
  * and must be positive. `acc_fp16` != 0 requests the reference's FP16
@@ -225,6 +236,22 @@ int tk_attn_fwd_gqa(int dtype, const void* q, const void* k, const void* v, void
                     int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
                     const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
                     int causal, void* stream);
+/* Grouped-query attention forward with rotate-half RoPE applied to Q and K first,
+ * from position-indexed tables cos/sin [table_rows >= seq][head_dim / 2]: query and
+ * key i use row i. Q is rotated in the kernel's prologue as it is loaded (the rotate-half
+ * pairs sit in one lane's MFMA fragments); K is rotated once by tk_rope_positions into
+ * the workspace `k_rot` (contiguous [batch][kv_heads][seq][head_dim]), since every
+ * query block re-reads each K block. Bitwise the composition tk_rope_fwd(q), tk_rope_fwd(k),
+ * tk_attn_fwd_gqa; k_rot holds the rotated K afterwards (the backward needs it). K must be
+ * [batch][kv_heads][seq] rows of one row stride. No reference kernel exists: the
+ * reference lists RoPE in the attention prologue among its next steps around
+ * src/tklab/kernels/rope.py:26-73 and flash_attention.py:120-264. */
+int tk_attn_fwd_rope(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+                     const void* rope_cos, const void* rope_sin, int64_t table_rows,
+                     int64_t table_row_stride, void* k_rot, int64_t batch, int64_t heads,
+                     int64_t kv_heads, int64_t seq, int64_t head_dim, const int64_t* q_strides,
+                     const int64_t* k_strides, const int64_t* v_strides,
+                     const int64_t* o_strides, float sm_scale, int causal, void* stream);
 int tk_attn_bwd_dkdv_gqa(int dtype, const void* q, const void* k, const void* v,
                          const void* dout, void* dk, void* dv, const float* lse,
                          const float* delta, int64_t batch, int64_t heads, int64_t kv_heads,

@@ -915,6 +915,40 @@ extern "C" int tk_attn_fwd_gqa(int dtype, const void* q, const void* k, const vo
   return tk::check_launch("attn_fwd_gqa");
 }
 
+extern "C" int tk_attn_fwd_rope(int dtype, const void* q, const void* k, const void* v, void* o,
+                                float* lse, const void* rope_cos, const void* rope_sin,
+                                int64_t table_rows, int64_t table_row_stride, void* k_rot,
+                                int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
+                                int64_t head_dim, const int64_t* q_strides,
+                                const int64_t* k_strides, const int64_t* v_strides,
+                                const int64_t* o_strides, float sm_scale, int causal,
+                                void* stream) {
+  const void* ptrs[] = {q, k, v, o, rope_cos, rope_sin, k_rot};
+  const int64_t* st[] = {q_strides, k_strides, v_strides, o_strides};
+  const bool kv[] = {false, true, true, false};
+  if (gqa_check("attn_fwd_rope", dtype, ptrs, 7, batch, heads, kv_heads, seq, head_dim, st, kv, 4))
+    return 1;
+  if (table_rows < seq) return tk::fail("attn_fwd_rope: the tables need a row per position");
+  if (table_row_stride < head_dim / 2 || (table_row_stride * 2) % 16 != 0 ||
+      !tk::aligned16(rope_cos) || !tk::aligned16(rope_sin))
+    return tk::fail("attn_fwd_rope: table rows must be 16-byte aligned");
+  if (k_strides[1] != seq * k_strides[2] || k_strides[0] != kv_heads * k_strides[1])
+    return tk::fail("attn_fwd_rope: K must be [batch][kv_heads][seq] rows of one row stride");
+  // K is rotated once into the workspace: every query block re-reads each K block, so a
+  // rotation inside the attention loop would be repeated once per query block.
+  const int64_t rot_strides[3] = {kv_heads * seq * head_dim, seq * head_dim, head_dim};
+  if (!tk::attn_fwd_dma_applies(seq, head_dim, rot_strides, v_strides))
+    return tk::fail("attn_fwd_rope: each head's rows must span less than 2 GiB");
+  if (tk_rope_positions(dtype, k, rope_cos, rope_sin, k_rot, batch * kv_heads * seq, seq,
+                        head_dim / 2, k_strides[2], table_row_stride, head_dim, 0, stream))
+    return 1;
+  tk::attn_fwd_dma_launch(dtype, q, k_rot, v, o, lse, batch, heads, kv_heads, seq, head_dim,
+                          q_strides, rot_strides, v_strides, o_strides, sm_scale, causal != 0,
+                          tk::as_stream(stream), nullptr, 0, rope_cos, rope_sin,
+                          table_row_stride);
+  return tk::check_launch("attn_fwd_rope");
+}
+
 extern "C" int tk_attn_bwd_dkdv_gqa(int dtype, const void* q, const void* k, const void* v,
                                     const void* dout, void* dk, void* dv, const float* lse,
                                     const float* delta, int64_t batch, int64_t heads,

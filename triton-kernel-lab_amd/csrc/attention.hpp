@@ -4,6 +4,8 @@
 // multi-head attention). With `cu_seqlens` (int32[batch + 1]) the batch is variable-length:
 // sequence b is rows cu_seqlens[b] .. cu_seqlens[b + 1] of a packed [total][head][dim]
 // layout (batch strides 0, `seq` the longest length) and LSE / delta are [head][total].
+// With rope tables (forward only) Q is rotated (rotate-half RoPE, tables [pos][D/2]
+// indexed by query position) as it is loaded.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <cstdint>
@@ -20,7 +22,8 @@ void attn_fwd_dma_launch(int dtype, const void* q, const void* k, const void* v,
                          int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
                          const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
                          bool causal, hipStream_t stream, const int32_t* cu_seqlens = nullptr,
-                         int64_t total = 0);
+                         int64_t total = 0, const void* rope_cos = nullptr,
+                         const void* rope_sin = nullptr, int64_t rope_stride = 0);
 
 // True when one query head's rows (layout of q, dO, dQ) and one KV head's rows (layout
 // of k, v, dK, dV) each span less than 2 GiB. The caller has already checked dtype,

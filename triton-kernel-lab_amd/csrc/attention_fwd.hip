@@ -52,7 +52,34 @@ struct Shape {
   float scale_log2;
   int q_blocks, tiles;
   uint32_t k_bytes, v_bytes;  // per-head buffer extents
+  // RoPE applied to Q in the prologue (null: none): position-indexed tables [pos][D/2]
+  // of T with row stride rope_stride; query i uses row i.
+  const void* rope_cos;
+  const void* rope_sin;
+  int64_t rope_stride;
 };
+
+// Rotate-half RoPE of one 16-byte Q fragment pair: x1 holds features f .. f+7 and x2
+// features f + D/2 .. f + D/2 + 7 (f < D/2); c and s hold cos/sin of f .. f+7. The
+// arithmetic is the RoPE kernel's: products rounded separately (no contraction), then
+// each result rounded to T, so the rotated Q is bitwise the one tk_rope_fwd stores.
+template <typename T>
+__device__ __forceinline__ void rope_fragment(i32x4& x1, i32x4& x2, i32x4 c, i32x4 s) {
+#pragma clang fp contract(off)
+  typedef T t8 __attribute__((ext_vector_type(8)));
+  const t8 a = __builtin_bit_cast(t8, x1), b = __builtin_bit_cast(t8, x2);
+  const t8 cv = __builtin_bit_cast(t8, c), sv = __builtin_bit_cast(t8, s);
+  t8 y1, y2;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float xa = static_cast<float>(a[e]), xb = static_cast<float>(b[e]);
+    const float ce = static_cast<float>(cv[e]), se = static_cast<float>(sv[e]);
+    y1[e] = tk::from_f32<T>(xa * ce - xb * se);
+    y2[e] = tk::from_f32<T>(xb * ce + xa * se);
+  }
+  x1 = __builtin_bit_cast(i32x4, y1);
+  x2 = __builtin_bit_cast(i32x4, y2);
+}
 
 template <int D>
 struct Geo {
@@ -167,6 +194,20 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
       qf[kk] = query < N ? *reinterpret_cast<const i32x4*>(Qh + query * s.q[2] + kk * 16 + hi * 8)
                          : i32x4{0, 0, 0, 0};
   }
+  // RoPE tables of this lane's query, loaded with Q; the rotation waits until the first
+  // K/V blocks' DMA has been issued.
+  const bool rope = s.rope_cos != nullptr && wq0 + l32 < N;
+  i32x4 rc[KS / 2], rsn[KS / 2];
+  if (rope) {
+    const int64_t at = int64_t(wq0 + l32) * s.rope_stride + hi * 8;
+    const T* cr = static_cast<const T*>(s.rope_cos) + at;
+    const T* sr = static_cast<const T*>(s.rope_sin) + at;
+#pragma unroll
+    for (int kk = 0; kk < KS / 2; ++kk) {
+      rc[kk] = *reinterpret_cast<const i32x4*>(cr + kk * 16);
+      rsn[kk] = *reinterpret_cast<const i32x4*>(sr + kk * 16);
+    }
+  }
   // Lane read addresses inside a stage: K row l32 (+32 for the second key tile), chunk
   // 2 kk + hi; V rows 4 hi + j (+16 per key step, +8 for k-index 4..7), features
   // 32 dt + 16 g + 4 q .. +3.
@@ -191,6 +232,12 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
 
   dma_block<D>(rk, rv, lds, k_src, v_src, 0, kv_blocks - 1, k_blk, v_blk, wave);
   dma_block<D>(rk, rv, lds + STB, k_src, v_src, 1, kv_blocks - 1, k_blk, v_blk, wave);
+  // Fragments kk and kk + KS/2 hold features 16 kk + 8 hi .. +7 and the same + D/2: the
+  // rotate-half pairs sit in one lane.
+  if (rope) {
+#pragma unroll
+    for (int kk = 0; kk < KS / 2; ++kk) rope_fragment<T>(qf[kk], qf[kk + KS / 2], rc[kk], rsn[kk]);
+  }
   int stage = 0, fill = 2;
   // This wave multiplies a prefix of the workgroup's blocks (causal: those starting at or
   // before its last query) and only helps to load the rest.
@@ -387,8 +434,12 @@ void attn_fwd_dma_launch(int dtype, const void* q, const void* k, const void* v,
                          int64_t head_dim, const int64_t* q_strides, const int64_t* k_strides,
                          const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
                          bool causal, hipStream_t stream, const int32_t* cu_seqlens,
-                         int64_t total) {
+                         int64_t total, const void* rope_cos, const void* rope_sin,
+                         int64_t rope_stride) {
   Shape s{};
+  s.rope_cos = rope_cos;
+  s.rope_sin = rope_sin;
+  s.rope_stride = rope_stride;
   s.heads = (int)heads;
   s.seq = (int)seq;
   s.group = (int)(heads / kv_heads);

@@ -122,11 +122,21 @@ __global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(
 // ------------------------------------------------------------------ RoPE
 
 // y1 = x1*cos - x2*sin; y2 = x2*cos + x1*sin  (src/tklab/kernels/rope.py:44-73)
-template <typename T, int VEC>
+// kPositions: the tables are indexed by position, table row = row mod `positions.d`
+// (rows of [batch, heads, seq, D] with positions 0 .. seq-1); otherwise by row.
+template <bool kPositions>
+__device__ __forceinline__ int table_row(int row, const tk::FastDiv& positions) {
+  if constexpr (kPositions)
+    return row - static_cast<int>(positions.div(row)) * static_cast<int>(positions.d);
+  else
+    return row;
+}
+
+template <typename T, int VEC, bool kPositions = false>
 __global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ cosv, const T* __restrict__ sinv,
     T* __restrict__ y, int chunks, tk::FastDiv per_row, int half, int64_t xs, int64_t cs,
-    int64_t ss, int64_t ys) {
+    int64_t ss, int64_t ys, tk::FastDiv positions = tk::FastDiv()) {
   // A workgroup pass covers kUnroll * kBlock consecutive chunks (one 4 KiB run per
   // wave and tensor), then the grid strides on.
   const int stride = gridDim.x * kBlock * kUnroll;
@@ -138,10 +148,11 @@ __global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       const T* xr = x + p.row * xs;
+      const int tr = table_row<kPositions>(p.row, positions);
       tk::load_vec_stream<T, VEC>(xr + p.col, x1[u]);
       tk::load_vec_stream<T, VEC>(xr + half + p.col, x2[u]);
-      tk::load_vec<T, VEC>(cosv + p.row * cs + p.col, co[u]);
-      tk::load_vec<T, VEC>(sinv + p.row * ss + p.col, si[u]);
+      tk::load_vec<T, VEC>(cosv + tr * cs + p.col, co[u]);
+      tk::load_vec<T, VEC>(sinv + tr * ss + p.col, si[u]);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -163,12 +174,12 @@ __global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
 
 // dx1 = dy1*cos + dy2*sin; dx2 = dy2*cos - dy1*sin;
 // dcos = dy1*x1 + dy2*x2; dsin = -dy1*x2 + dy2*x1  (src/tklab/kernels/rope.py:102-160)
-template <typename T, int VEC>
+template <typename T, int VEC, bool kPositions = false>
 __global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ cosv,
     const T* __restrict__ sinv, T* __restrict__ dx, T* __restrict__ dcos, T* __restrict__ dsin,
     int chunks, tk::FastDiv per_row, int half, int64_t dys, int64_t xs, int64_t cs, int64_t ss,
-    int64_t dxs, int64_t dcs, int64_t dss) {
+    int64_t dxs, int64_t dcs, int64_t dss, tk::FastDiv positions = tk::FastDiv()) {
   const bool need_x = dcos != nullptr || dsin != nullptr;
   // A workgroup pass covers kUnroll * kBlock consecutive chunks (one 4 KiB run per
   // wave and tensor), then the grid strides on.
@@ -181,10 +192,11 @@ __global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       const T* dyr = dy + p.row * dys;
+      const int tr = table_row<kPositions>(p.row, positions);
       tk::load_vec_stream<T, VEC>(dyr + p.col, d1[u]);
       tk::load_vec_stream<T, VEC>(dyr + half + p.col, d2[u]);
-      tk::load_vec<T, VEC>(cosv + p.row * cs + p.col, co[u]);
-      tk::load_vec<T, VEC>(sinv + p.row * ss + p.col, si[u]);
+      tk::load_vec<T, VEC>(cosv + tr * cs + p.col, co[u]);
+      tk::load_vec<T, VEC>(sinv + tr * ss + p.col, si[u]);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -412,4 +424,47 @@ extern "C" int tk_scale_rows(int dtype, const void* x, const void* scale, void* 
                          static_cast<const T*>(x), static_cast<const T*>(scale),
                          static_cast<T*>(y), (int)chunks, div, x_row_stride, y_row_stride)));
   return tk::check_launch("scale_rows");
+}
+
+// RoPE over rows of [batch, heads, seq, D] (row stride x_row_stride / y_row_stride)
+// with position-indexed tables cos/sin [>= seq][D/2]: row r uses table row r mod seq.
+// Forward (inverse = false) or the input gradient (inverse = true: RoPE with -sin).
+extern "C" int tk_rope_positions(int dtype, const void* x, const void* cos, const void* sin,
+                                 void* y, int64_t rows, int64_t seq, int64_t half_dim,
+                                 int64_t x_row_stride, int64_t table_row_stride,
+                                 int64_t y_row_stride, int inverse, void* stream) {
+  if (x == nullptr || cos == nullptr || sin == nullptr || y == nullptr)
+    return tk::fail("rope_positions: null pointer");
+  if (seq <= 0 || seq > rows || rows % seq != 0)
+    return tk::fail("rope_positions: rows must be a positive multiple of seq");
+  const bool vok = tk::valid_dtype(dtype) &&
+                   vector_ok(dtype, half_dim, {x, cos, sin, y},
+                             {x_row_stride, table_row_stride, y_row_stride});
+  const int vec = vok ? 16 / tk::elem_size(dtype) : 1;
+  int64_t per_row, chunks;
+  if (check_problem("rope_positions", dtype, rows, half_dim, vec, &per_row, &chunks)) return 1;
+  const tk::FastDiv div(static_cast<uint32_t>(per_row));
+  const tk::FastDiv positions(static_cast<uint32_t>(seq));
+  const Grid1D g = chunk_grid(chunks);
+  hipStream_t s = tk::as_stream(stream);
+  if (inverse) {
+    TK_DISPATCH_DTYPE(dtype, T,
+      TK_DISPATCH_VEC(T, vok,
+        hipLaunchKernelGGL((rope_bwd_kernel<T, VEC, true>), dim3(g.blocks), dim3(kBlock), 0, s,
+                           static_cast<const T*>(x), static_cast<const T*>(nullptr),
+                           static_cast<const T*>(cos), static_cast<const T*>(sin),
+                           static_cast<T*>(y), static_cast<T*>(nullptr),
+                           static_cast<T*>(nullptr), (int)chunks, div, (int)half_dim,
+                           x_row_stride, 0, table_row_stride, table_row_stride, y_row_stride, 0,
+                           0, positions)));
+  } else {
+    TK_DISPATCH_DTYPE(dtype, T,
+      TK_DISPATCH_VEC(T, vok,
+        hipLaunchKernelGGL((rope_fwd_kernel<T, VEC, true>), dim3(g.blocks), dim3(kBlock), 0, s,
+                           static_cast<const T*>(x), static_cast<const T*>(cos),
+                           static_cast<const T*>(sin), static_cast<T*>(y), (int)chunks, div,
+                           (int)half_dim, x_row_stride, table_row_stride, table_row_stride,
+                           y_row_stride, positions)));
+  }
+  return tk::check_launch("rope_positions");
 }

@@ -44,6 +44,7 @@ _SIGNATURES: dict[str, list[object]] = {
     "tk_rope_bwd": [
         _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P,
     ],
+    "tk_rope_positions": [_I32, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P],
     "tk_gemm": [_I32, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P],
     "tk_gemm_rowscale": [_I32, _P, _P, _P, _P] + [_I64] * 9 + [_P],
     "tk_scale_rows": [_I32, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
@@ -63,6 +64,10 @@ _SIGNATURES: dict[str, list[object]] = {
     "tk_attn_fwd_gqa": [
         _I32, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _I64P, _I64P, _F32,
         _I32, _P,
+    ],
+    "tk_attn_fwd_rope": [
+        _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64P,
+        _I64P, _I64P, _I64P, _F32, _I32, _P,
     ],
     "tk_attn_bwd_dkdv_gqa": [
         _I32, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _F32,

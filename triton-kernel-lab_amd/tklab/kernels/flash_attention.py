@@ -18,6 +18,8 @@ kv_heads)``), forward and backward; dK/dV sum a KV head's query heads in a fixed
 order, so the backward stays deterministic. ``varlen_attention(q, k, v,
 cu_seqlens, max_seqlen, *, causal)`` runs them on variable-length batches packed
 as ``(total, heads, head_dim)`` with int32 sequence offsets ``cu_seqlens``.
+``rope_attention(q, k, v, cos, sin, *, causal)`` applies rotate-half RoPE from
+position-indexed tables to Q (in the forward kernel's prologue) and K first.
 """
 
 from __future__ import annotations
@@ -370,6 +372,102 @@ def grouped_query_attention(
         _launch_gqa_forward(q, k, v, output, None, causal=causal)
         return output
     return cast(torch.Tensor, _GQAFunction.apply(q, k, v, causal))
+
+
+def _validate_rope_tables(q: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> None:
+    """Position-indexed rotate-half tables: (positions >= sequence, head_dim // 2)."""
+    for table in (cos, sin):
+        if table.ndim != 2 or table.shape[1] != q.shape[-1] // 2:
+            raise ValueError("rope tables must be shaped (positions, head_dim // 2)")
+        if table.shape[0] < q.shape[2]:
+            raise ValueError("rope tables need a row per sequence position")
+        if table.dtype != q.dtype or table.device != q.device:
+            raise ValueError("rope tables must match Q's dtype and device")
+        if table.stride(1) != 1:
+            raise ValueError("rope tables require a contiguous final dimension")
+    if cos.stride(0) != sin.stride(0):
+        raise ValueError("rope tables must share one row stride")
+
+
+def _rope_positions(
+    x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, out: torch.Tensor, *, inverse: bool
+) -> None:
+    """RoPE (or its input gradient) of contiguous (batch, heads, sequence, dim) rows."""
+    batch, heads, n_ctx, head_dim = x.shape
+    _hip.call(
+        "tk_rope_positions", _hip.dtype_code(x.dtype), x.data_ptr(), cos.data_ptr(),
+        sin.data_ptr(), out.data_ptr(), batch * heads * n_ctx, n_ctx, head_dim // 2, head_dim,
+        cos.stride(0), head_dim, int(inverse), _hip.stream_of(x),
+    )
+
+
+def _launch_rope_forward(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+    output: torch.Tensor, softmax_lse: torch.Tensor | None, k_rot: torch.Tensor, *, causal: bool,
+) -> None:
+    """RoPE'd grouped-query forward: Q rotated in the kernel prologue, K into ``k_rot``."""
+    batch, heads, n_ctx, head_dim = q.shape
+    _hip.call(
+        "tk_attn_fwd_rope", _hip.dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+        output.data_ptr(), _hip.ptr(softmax_lse), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+        cos.stride(0), k_rot.data_ptr(), batch, heads, k.shape[1], n_ctx, head_dim,
+        _strides(q), _strides(k), _strides(v), _strides(output), 1.0 / math.sqrt(head_dim),
+        int(causal), _hip.stream_of(q),
+    )
+
+
+class _RopeAttentionFunction(torch.autograd.Function):
+    """Autograd bridge: saves Q, the rotated K, V, the tables, O and the LSE."""
+
+    @staticmethod
+    def forward(
+        ctx: Any, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+        sin: torch.Tensor, causal: bool,
+    ) -> torch.Tensor:
+        output, k_rot = torch.empty_like(q), torch.empty_like(k)
+        batch, heads, n_ctx, _ = q.shape
+        softmax_lse = torch.empty((batch, heads, n_ctx), dtype=torch.float32, device=q.device)
+        _launch_rope_forward(q, k, v, cos, sin, output, softmax_lse, k_rot, causal=causal)
+        ctx.save_for_backward(q, k_rot, v, cos, sin, output, softmax_lse)
+        ctx.causal = causal
+        return output
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx: Any, do: torch.Tensor) -> tuple[Any, ...]:
+        q, k_rot, v, cos, sin, output, softmax_lse = ctx.saved_tensors
+        q_rot = torch.empty_like(q)
+        _rope_positions(q, cos, sin, q_rot, inverse=False)
+        dq_rot, dk_rot, dv = _launch_gqa_backward(
+            q_rot, k_rot, v, output, softmax_lse, do, causal=ctx.causal
+        )
+        dq, dk = torch.empty_like(dq_rot), torch.empty_like(dk_rot)
+        _rope_positions(dq_rot, cos, sin, dq, inverse=True)
+        _rope_positions(dk_rot, cos, sin, dk, inverse=True)
+        return dq, dk, dv, None, None, None
+
+
+def rope_attention(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+    *, causal: bool,
+) -> torch.Tensor:
+    """Grouped-query attention on rotate-half RoPE'd Q and K.
+
+    ``attention(rope(q), rope(k), v)`` with position-indexed tables ``cos``/``sin``
+    of shape ``(positions >= sequence, head_dim // 2)`` (query and key ``i`` use row
+    ``i``; the reference's ``rope`` takes per-row tables, ``rope.py:26-73``). Q is
+    rotated in the attention kernel's prologue and never stored rotated; K is rotated
+    once into a workspace (every query block re-reads it). Bitwise the composition of
+    the RoPE and attention kernels; the tables are constants (no gradient).
+    """
+    _validate_gqa(q, k, v)
+    _validate_rope_tables(q, cos, sin)
+    needs_grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
+    if not needs_grad:
+        output, k_rot = torch.empty_like(q), torch.empty_like(k)
+        _launch_rope_forward(q, k, v, cos, sin, output, None, k_rot, causal=causal)
+        return output
+    return cast(torch.Tensor, _RopeAttentionFunction.apply(q, k, v, cos, sin, causal))
 
 
 def _validate_varlen(
