@@ -286,7 +286,17 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
     rows: list[dict] = []
 
     def timed(fn, reps: int) -> float:
+        # The reference's timing (bench.py:98-103): at least 25 ms of warmup, then at
+        # least 100 ms of timed launches; the median single launch.
         fn()
+        torch.cuda.synchronize()
+        t0, warm = time.perf_counter(), 0
+        while time.perf_counter() - t0 < 0.025:
+            fn()
+            torch.cuda.synchronize()
+            warm += 1
+        each = (time.perf_counter() - t0) / max(warm, 1)
+        reps = max(reps, math.ceil(0.1 / max(each, 1e-6)))
         times = []
         for _ in range(reps):
             flush.zero_()
