@@ -211,10 +211,10 @@ def measured_roofs(torch, device) -> dict:
 
     Copy: tk_roof_copy of 1 GiB back to back (2 GiB of HBM traffic per launch),
     beside torch's own device copy; the larger is the copy roof. MFMA: tk_roof_mfma
-    with 8192 waves (8 per SIMD) of dense v_mfma_f32_32x32x16 and no memory
-    traffic, timed like the MFMA rows (1 GiB flush before each launch), at about
-    the length of the 8192^3 GEMM (~1 ms) and of the causal attention forward
-    (~4 ms), since sustained clocks fall with the length of a dense MFMA burst.
+    with 8192 waves (8 per SIMD) of dense v_mfma_f32_16x16x32 (the shape that
+    sustains the most FLOP/s under the power limit) and no memory traffic, timed like
+    the MFMA rows (25 ms of warmup, then a 1 GiB flush before each launch), at about
+    the length of the 8192^3 GEMM (~1 ms) and of the causal attention forward (~4 ms).
     """
     from tklab import _hip
 
@@ -249,6 +249,10 @@ def measured_roofs(torch, device) -> dict:
     for dt_name, code in (("float16", 1), ("bfloat16", 2)):
         mfma[dt_name] = {}
         for label, iters in (("1ms", 1000), ("4ms", 4000)):
+            t0 = time.perf_counter()
+            while time.perf_counter() - t0 < 0.025:
+                _hip.call("tk_roof_mfma", code, out.data_ptr(), waves, iters, stream)
+                torch.cuda.synchronize()
             times = []
             for _ in range(6):
                 flush.zero_()

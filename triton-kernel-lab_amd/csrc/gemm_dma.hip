@@ -3,22 +3,31 @@
 // computes the same product with a Triton tile loop).
 //
 // Block tile 256 x 256, K step 32, 512 threads = 8 wave64s in a 2 (M) x 4 (N) grid, two
-// waves per SIMD; each wave owns 128 x 64 of C as 4 x 2 tiles of v_mfma_f32_32x32x16
+// waves per SIMD; each wave owns 128 x 64 of C as 8 x 4 tiles of v_mfma_f32_16x16x32
 // (128 accumulators). With two waves per SIMD, one wave's LDS reads, DMA issue and
-// barrier waits are covered by the other wave's MFMAs.
+// barrier waits are covered by the other wave's MFMAs. 16x16x32 rather than 32x32x16:
+// the clock is power-limited under dense MFMA load, and the 16x16 shape sustains more
+// FLOP/s (MFMA-only with random operands 1.90 vs 1.78 PFLOP/s bf16; this GEMM 1.39 vs
+// 1.29 PFLOP/s at 8192^3 with the same tiles and LDS traffic).
 //
 // Operands reach LDS by buffer->LDS DMA (buffer_load_dwordx4 ... lds): no VGPR staging.
 // LDS is a ring of kStages stages of 32 KiB (A tile then B tile); K tile t+kAhead is
 // issued while tile t is multiplied, kAhead = kStages - 2, so the stage being refilled
-// was last read two tiles ago and one barrier per K tile orders every reuse.
+// was last read two tiles ago and one barrier per K tile orders every reuse. The
+// barrier sits between the wave's row tiles 0-3 and 4-7: rows 0-3 run while rows 4-7
+// of the same K tile are read and tile t + kAhead is issued; rows 4-7 run while the
+// next tile's rows 0-3 and B fragments (a second register set) are read.
 //
 // Stage layout (bytes), chosen so every LDS read phase touches 64 distinct banks:
 //   A: 256 rows x 64 B; the 16-byte chunk c (k = 8c .. 8c+7) of row r sits at chunk
-//      c ^ ((r >> 2) & 3). Fragment reads are ds_read_b128 (16 lanes per phase).
+//      c ^ ((r >> 2) & 3). A fragment (16 rows, lane group g taking k = 8g .. 8g+7) is
+//      one ds_read_b128 (16 lanes per phase: 16 rows of one chunk).
 //   B: 32 k-rows x 512 B, row-major in n; the 32-byte granule g (n = 16g .. 16g+15) of
-//      k-row k sits at granule g ^ (2 * (k & 3)). Fragments are read with
-//      ds_read_b64_tr_b16 (32 lanes per phase), which transposes 4 k x 16 n blocks into
-//      the MFMA B layout: two reads give one lane its 8 consecutive k of one column.
+//      k-row k sits at granule g ^ (2 * (k & 3) + ((k >> 3) & 1)). Fragments are read
+//      with ds_read_b64_tr_b16, which transposes 4 k x 16 n blocks into the MFMA B
+//      layout: two reads give one lane its 8 consecutive k of one column. One read phase
+//      (32 lanes) covers two lane groups on k-rows 8 apart; the (k >> 3) term puts their
+//      8 granules on distinct banks.
 // A DMA instruction moves 64 lanes x 16 B into 1 KiB of contiguous LDS at M0, so the
 // swizzle is applied on the global side: each lane fetches the chunk that belongs at its
 // LDS slot.
@@ -39,9 +48,9 @@
 // SwiGLU variant (kSwiGLU): Y = swiglu(value = A*B_up, gate = A*B_gate) for two weights
 // [K, N]. A block computes 256 x 128 of Y from a 256-column B tile holding the gate
 // columns n0..n0+127 then the same up columns, laid out in LDS as two 128-column blocks
-// (256-byte k-rows, 32-byte granule g of k-row k at g ^ (2 * (k & 3)): still 64 distinct
-// banks per read phase), so every B DMA instruction reads one weight. Wave (wm, wq)
-// takes gate columns 32wq.. as its N tile 0 and the same up columns as N tile 1, and
+// (256-byte k-rows, same granule swizzle: still 64 distinct banks per read phase), so
+// every B DMA instruction reads one weight. Wave (wm, wq) takes gate columns 32wq ..
+// 32wq+31 as its N tiles 0, 1 and the same up columns as N tiles 2, 3, and
 // the epilogue rounds both to the storage type (as the unfused GEMMs store them) and
 // writes value * gate * sigmoid(gate): the two M x N intermediates never reach HBM and
 // the result is bitwise that of the two GEMMs followed by the SwiGLU kernel.
@@ -67,27 +76,10 @@ constexpr uint32_t kOob = 0x80000000u;  // past every buffer's num_records: read
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <typename T>
-struct Mfma;
-template <>
-struct Mfma<_Float16> {
-  static __device__ __forceinline__ f32x16 run(i32x4 a, i32x4 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma<__bf16> {
-  static __device__ __forceinline__ f32x16 run(i32x4 a, i32x4 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-};
 
 struct Problem {
   int m, n, k;
@@ -127,37 +119,6 @@ __device__ __forceinline__ i32x2 lds_read_tr16(uint32_t addr) {
   return r;
 }
 
-// A fragment of row block i (32 rows = 2 KiB) with i folded into the immediate offset.
-__device__ __forceinline__ i32x4 read_a(int i, uint32_t addr) {
-  switch (i) {
-    case 0: return lds_read_b128<0>(addr);
-    case 1: return lds_read_b128<2048>(addr);
-    case 2: return lds_read_b128<4096>(addr);
-    default: return lds_read_b128<6144>(addr);
-  }
-}
-
-// B fragment for k half KK (16 k-rows of ROWB bytes): k-rows +0..3 and +4..7 of this
-// lane group.
-template <int KK, int ROWB>
-__device__ __forceinline__ i32x4 read_b(uint32_t addr) {
-  const i32x2 lo = lds_read_tr16<kOperandBytes + KK * 16 * ROWB>(addr);
-  const i32x2 hi = lds_read_tr16<kOperandBytes + KK * 16 * ROWB + 4 * ROWB>(addr);
-  return i32x4{lo[0], lo[1], hi[0], hi[1]};
-}
-
-struct Frags {
-  i32x4 a[4], b[2];
-};
-
-// Waits for this wave's LDS reads; the fragments are in/out operands so no use of them
-// can be scheduled above the wait.
-__device__ __forceinline__ void wait_lgkm(Frags& f) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(f.a[0]), "+v"(f.a[1]), "+v"(f.a[2]), "+v"(f.a[3]), "+v"(f.b[0]),
-                 "+v"(f.b[1]));
-}
-
 // Y = value * gate * sigmoid(gate) on values already rounded to T, in the SwiGLU
 // kernel's operation order (contraction off: each product rounded separately).
 template <typename T>
@@ -167,19 +128,66 @@ __device__ __forceinline__ T swiglu_out(float gate_acc, float up_acc) {
   return tk::from_f32<T>(v * g * tk::stable_sigmoid(g));
 }
 
+// v_mfma_f32_16x16x32: A lane l holds row l % 16, k = 8 (l / 16) .. +7; B lane l holds
+// column l % 16, the same k; D lane l holds column l % 16, rows 4 (l / 16) .. +3.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<_Float16> {
+  static __device__ __forceinline__ f32x4 run(i32x4 a, i32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<__bf16> {
+  static __device__ __forceinline__ f32x4 run(i32x4 a, i32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+// B k-row swizzle: 32-byte granule g of k-row k sits at g ^ b_swz(k). A 16x16x32 B
+// fragment read phase covers two 16-lane groups reading k-rows 8 apart, so the swizzle
+// carries bit 3 of k besides the (k & 3) term that separates the 4 rows of one read.
+__device__ __forceinline__ int b_swz(int k) { return 2 * (k & 3) + ((k >> 3) & 1); }
+
+// A fragment of row tile I (16 rows = 1 KiB of the stage).
+template <int I>
+__device__ __forceinline__ i32x4 read_a(uint32_t addr) {
+  return lds_read_b128<I * 1024>(addr);
+}
+
+// B fragment: k-rows +0..3 and +4..7 of this lane group (ROWB bytes per k-row).
+template <int ROWB>
+__device__ __forceinline__ i32x4 read_b(uint32_t addr) {
+  const i32x2 lo = lds_read_tr16<kOperandBytes>(addr);
+  const i32x2 hi = lds_read_tr16<kOperandBytes + 4 * ROWB>(addr);
+  return i32x4{lo[0], lo[1], hi[0], hi[1]};
+}
+
+template <int N>
+__device__ __forceinline__ void wait_lgkm_pin(i32x4 (&f)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(f[i]));
+}
+
 template <typename T, bool kSwiGLU, bool kRowScale>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(2, 2))) void
 gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __restrict__ B2,
-                T* __restrict__ C, Problem p) {
-  constexpr int kTileN = kSwiGLU ? 128 : BN;  // output columns per block
-  constexpr int kRowB = kSwiGLU ? 256 : 512;  // bytes per B k-row in LDS
+                  T* __restrict__ C, Problem p) {
+  constexpr int kTileN = kSwiGLU ? 128 : BN;
+  constexpr int kRowB = kSwiGLU ? 256 : 512;
   __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
 
   const int total = p.tiles_m * p.tiles_n;
   int w = blockIdx.x;
   if (total % kXcds == 0) w = (w % kXcds) * (total / kXcds) + w / kXcds;
-  const int per_group = kGroupM * p.tiles_n;  // p.tiles_n counts kTileN-column tiles
+  const int per_group = kGroupM * p.tiles_n;
   const int first_m = (w / per_group) * kGroupM;
   const int group_m = min(p.tiles_m - first_m, kGroupM);
   const int tile_m = first_m + (w % per_group) % group_m;
@@ -189,11 +197,9 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
-  const int lrow = lane & 31;
-  const int lhalf = lane >> 5;
+  const int l16 = lane & 15, lg = lane >> 4;
   const __amdgpu_buffer_rsrc_t ra =
       __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, p.a_bytes, 0x00020000);
-  // SwiGLU: waves 0-3 fill the gate block, waves 4-7 the up block.
   const bool up_half = kSwiGLU && wave >= 4;
   const __amdgpu_buffer_rsrc_t rb =
       up_half ? __builtin_amdgcn_make_buffer_rsrc((void*)B2, (short)0, p.b2_bytes, 0x00020000)
@@ -201,9 +207,6 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
   const int ldb = up_half ? p.ldb2 : p.ldb;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
 
-  // DMA sources for K tile 0 (bytes). Wave w fills A rows 32w .. 32w+31 (2 loads of 16
-  // rows) and B k-rows 4w .. 4w+3 (2 loads of 2 k-rows). Rows past M and columns past N
-  // read as zero; K is a multiple of BK on this path.
   uint32_t a_src[2], b_src[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -211,32 +214,25 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
     const int c = (lane & 3) ^ ((r >> 2) & 3);
     a_src[i] = (m0 + r < p.m) ? uint32_t((m0 + r) * p.lda + c * 8) * 2u : kOob;
     if constexpr (kSwiGLU) {
-      // Load L = 2*wave + i: block L / 8 (gate, up), k-rows 4*(L % 8) .. +3 of 256 B.
       const int L = wave * 2 + i;
       const int kr = 4 * (L & 7) + (lane >> 4);
       const int slot = lane & 15;
-      const int chunk = (((slot >> 1) ^ (2 * (kr & 3))) << 1) | (slot & 1);
+      const int chunk = (((slot >> 1) ^ b_swz(kr)) << 1) | (slot & 1);
       b_src[i] = (n0 + chunk * 8 < p.n) ? uint32_t(kr * ldb + n0 + chunk * 8) * 2u : kOob;
     } else {
       const int kr = (wave * 2 + i) * 2 + (lane >> 5);
       const int slot = lane & 31;
-      const int chunk = (((slot >> 1) ^ (2 * (kr & 3))) << 1) | (slot & 1);
+      const int chunk = (((slot >> 1) ^ b_swz(kr)) << 1) | (slot & 1);
       b_src[i] = (n0 + chunk * 8 < p.n) ? uint32_t(kr * ldb + n0 + chunk * 8) * 2u : kOob;
     }
   }
   const uint32_t b_tile_bytes = uint32_t(BK * ldb) * 2u;
   const int kt = p.k / BK;
 
-  // Row-scaled variant: thread t < 256 fetches the scale of tile row t (rows past M
-  // clamp to row M - 1 and are never stored) before the first DMA, so the load has
-  // landed long before the epilogue; one register through the main loop.
   float row_scale = 0.f;
   if constexpr (kRowScale)
     if (threadIdx.x < BM) row_scale = p.row_scale[min(m0 + (int)threadIdx.x, p.m - 1)];
 
-  // DMA x (0..3: two A loads, two B loads) of K tile `tile` into ring slot `slot`. Tiles past the end reload the
-  // last tile into a slot that is never read again, so every step issues the same number
-  // of loads and the vmcnt arithmetic stays constant.
   auto dma = [&](int x, int tile, int slot) {
     tile = min(tile, kt - 1);
     char* stage = lds + slot * kStageBytes;
@@ -249,35 +245,33 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
           tile * b_tile_bytes, 0, 0);
   };
 
-  // Lane read addresses inside a stage: A row wm + lrow, chunk (2*kk + lhalf) swizzled;
-  // B k-row 8*(g>>1) + jj (+16*kk, +4), columns wn + 32j + 16*(g&1) + 4q.
-  uint32_t a_addr[2], b_addr[2];
+  // A: row wm + l16 (+16 per row tile), chunk lg swizzled ((row >> 2) & 3 is the same
+  // for every row tile). B: k-rows 8 lg + (l16 >> 2) (+4), columns of N tile j starting
+  // at 4 (l16 & 3).
+  const uint32_t a_addr = (wm + l16) * 64 + ((lg ^ ((l16 >> 2) & 3)) * 16);
+  uint32_t b_addr[4];
   {
-    const int sa = (lrow >> 2) & 3;
+    const int jj = l16 >> 2, q = l16 & 3;
+    const int kr = 8 * lg + jj;
+    const int sw = b_swz(kr);
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) a_addr[kk] = (wm + lrow) * 64 + (((kk * 2 + lhalf) ^ sa) * 16);
-    const int g = lane >> 4, jj = (lane & 15) >> 2, q = lane & 3;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < 4; ++j) {
       if constexpr (kSwiGLU) {
-        // N tile j is block j (gate, up), columns 32 * (wave & 3) ..
-        const int n = (wave & 3) * 32 + (g & 1) * 16 + 4 * q;
-        b_addr[j] = j * 8192 +
-                    (((g >> 1) * 8 + jj) * 128 + (((n >> 4) ^ (2 * jj)) * 16) + (n & 15)) * 2;
+        // N tiles 0, 1: gate columns 32 (wave & 3) + 16 j; tiles 2, 3: the same up columns.
+        const int g = 2 * (wave & 3) + (j & 1);
+        b_addr[j] = (j >> 1) * 8192 + kr * 256 + ((g ^ sw) * 32) + q * 8;
       } else {
-        const int n = wn + j * 32 + (g & 1) * 16 + 4 * q;
-        b_addr[j] = (((g >> 1) * 8 + jj) * 256 + (((n >> 4) ^ (2 * jj)) * 16) + (n & 15)) * 2;
+        const int g = wn / 16 + j;
+        b_addr[j] = kr * 512 + ((g ^ sw) * 32) + q * 8;
       }
     }
   }
 
-  f32x16 acc[4][2];
+  f32x4 acc[8][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
   for (int t = 0; t < kAhead; ++t)
@@ -286,110 +280,114 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
   wait_vmcnt<(kAhead - 1) * 4>();
   barrier_no_fence();
 
-  Frags f0, f1;
+  i32x4 a_lo[4], a_hi[4], b0[4], b1[4];
+  a_lo[0] = read_a<0>(lds_base + a_addr);
+  a_lo[1] = read_a<1>(lds_base + a_addr);
+  a_lo[2] = read_a<2>(lds_base + a_addr);
+  a_lo[3] = read_a<3>(lds_base + a_addr);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) f0.a[i] = read_a(i, lds_base + a_addr[0]);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) f0.b[j] = read_b<0, kRowB>(lds_base + b_addr[j]);
+  for (int j = 0; j < 4; ++j) b0[j] = read_b<kRowB>(lds_base + b_addr[j]);
 
-  int stage = 0, fill = kAhead;
-  for (int t = 0; t < kt; ++t) {
+  // One K tile; B is this tile's B fragments, Bn receives the next tile's.
+  auto step = [&](int t, int stage, int fill, i32x4 (&Bc)[4], i32x4 (&Bn)[4]) {
     const uint32_t base = lds_base + stage * kStageBytes;
     const int next = stage + 1 == kStages ? 0 : stage + 1;
     const uint32_t next_base = lds_base + next * kStageBytes;
-
-    // First k half of tile t; meanwhile read the second half and issue tile t + kAhead.
-    wait_lgkm(f0);
+    wait_lgkm_pin(a_lo);
+    wait_lgkm_pin(Bc);
     sched_fence();
+    // Rows 0-3; read rows 4-7 of this tile, issue tile t + kAhead.
 #pragma unroll
-    for (int x = 0; x < 8; ++x) {
-      acc[x >> 1][x & 1] = Mfma<T>::run(f0.a[x >> 1], f0.b[x & 1], acc[x >> 1][x & 1]);
+    for (int x = 0; x < 16; ++x) {
+      const int i = x >> 2, j = x & 3;
+      acc[i][j] = Mfma<T>::run(a_lo[i], Bc[j], acc[i][j]);
       sched_fence();
-      if (x < 4) {
-        f1.a[x] = read_a(x, base + a_addr[1]);
-      } else if (x < 6) {
-        if (x == 4) f1.b[0] = read_b<1, kRowB>(base + b_addr[0]);
-        else f1.b[1] = read_b<1, kRowB>(base + b_addr[1]);
+      if (j == 0) {
+        if (i == 0) a_hi[0] = read_a<4>(base + a_addr);
+        if (i == 1) a_hi[1] = read_a<5>(base + a_addr);
+        if (i == 2) a_hi[2] = read_a<6>(base + a_addr);
+        if (i == 3) a_hi[3] = read_a<7>(base + a_addr);
       }
-      if (x >= 4) dma(x - 4, t + kAhead, fill);
+      if (j == 2) dma(i, t + kAhead, fill);
       sched_fence();
     }
-
-    // Tile t+1 has landed for this wave once only the later tiles' loads are pending;
-    // the barrier makes every wave's share visible (and retires all reads of tile t-1).
     wait_vmcnt<(kAhead - 1) * 4>();
     barrier_no_fence();
-
-    // Second k half of tile t; meanwhile read the first half of tile t+1.
-    wait_lgkm(f1);
+    wait_lgkm_pin(a_hi);
     sched_fence();
+    // Rows 4-7; read rows 0-3 and B of tile t+1.
 #pragma unroll
-    for (int x = 0; x < 8; ++x) {
-      acc[x >> 1][x & 1] = Mfma<T>::run(f1.a[x >> 1], f1.b[x & 1], acc[x >> 1][x & 1]);
+    for (int x = 0; x < 16; ++x) {
+      const int i = x >> 2, j = x & 3;
+      acc[4 + i][j] = Mfma<T>::run(a_hi[i], Bc[j], acc[4 + i][j]);
       sched_fence();
-      if (x < 4) {
-        f0.a[x] = read_a(x, next_base + a_addr[0]);
-      } else if (x < 6) {
-        if (x == 4) f0.b[0] = read_b<0, kRowB>(next_base + b_addr[0]);
-        else f0.b[1] = read_b<0, kRowB>(next_base + b_addr[1]);
+      if (j == 0) {
+        if (i == 0) a_lo[0] = read_a<0>(next_base + a_addr);
+        if (i == 1) a_lo[1] = read_a<1>(next_base + a_addr);
+        if (i == 2) a_lo[2] = read_a<2>(next_base + a_addr);
+        if (i == 3) a_lo[3] = read_a<3>(next_base + a_addr);
       }
+      if (j == 2) Bn[i] = read_b<kRowB>(next_base + b_addr[i]);
       sched_fence();
     }
-    stage = next;
+  };
+
+  int stage = 0, fill = kAhead;
+  auto advance = [&]() {
+    stage = stage + 1 == kStages ? 0 : stage + 1;
     fill = fill + 1 == kStages ? 0 : fill + 1;
+  };
+  int t = 0;
+  for (; t + 1 < kt; t += 2) {
+    step(t, stage, fill, b0, b1);
+    advance();
+    step(t + 1, stage, fill, b1, b0);
+    advance();
   }
-  // No DMA may still be writing when the workgroup's LDS is released.
+  if (t < kt) step(t, stage, fill, b0, b1);
   wait_vmcnt<0>();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
   if constexpr (kSwiGLU) {
-    const int n = n0 + (wave & 3) * 32 + lrow;
-    if (n < p.n) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+    for (int jj = 0; jj < 2; ++jj) {
+      const int n = n0 + (wave & 3) * 32 + jj * 16 + l16;
+      if (n >= p.n) continue;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-          if (m < p.m) C[m * p.scm + n * p.scn] = swiglu_out<T>(acc[i][0][r], acc[i][1][r]);
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm + i * 16 + lg * 4 + r;
+          if (m < p.m) C[m * p.scm + n * p.scn] = swiglu_out<T>(acc[i][jj][r], acc[i][jj + 2][r]);
         }
-      }
     }
   } else {
-    // Row-scaled variant: the tile's 256 scales go through the (now idle) LDS, thread t
-    // writing the one it fetched at entry; a lane then reads its rows in groups of 4.
     const float* scales = reinterpret_cast<const float*>(lds);
     if constexpr (kRowScale) {
-      __syncthreads();  // every wave is done reading the last K tile
+      __syncthreads();
       if (threadIdx.x < BM) reinterpret_cast<float*>(lds)[threadIdx.x] = row_scale;
       __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float sc[16];
-      if constexpr (kRowScale) {
+    for (int i = 0; i < 8; ++i) {
+      float4 sc = {1.f, 1.f, 1.f, 1.f};
+      if constexpr (kRowScale) sc = *reinterpret_cast<const float4*>(scales + wm + i * 16 + lg * 4);
+      const float scv[4] = {sc.x, sc.y, sc.z, sc.w};
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const float4 q = *reinterpret_cast<const float4*>(scales + wm + i * 32 + g4 * 8 + lhalf * 4);
-          sc[g4 * 4 + 0] = q.x;
-          sc[g4 * 4 + 1] = q.y;
-          sc[g4 * 4 + 2] = q.z;
-          sc[g4 * 4 + 3] = q.w;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int n = n0 + wn + j * 32 + lrow;
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + wn + j * 16 + l16;
         if (n >= p.n) continue;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm + i * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-          const float v = kRowScale ? acc[i][j][r] * sc[r] : acc[i][j][r];
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + wm + i * 16 + lg * 4 + r;
+          const float v = kRowScale ? acc[i][j][r] * scv[r] : acc[i][j][r];
           if (m < p.m) C[m * p.scm + n * p.scn] = tk::from_f32<T>(v);
         }
       }
     }
   }
 }
+
 
 }  // namespace
 
