@@ -5,7 +5,10 @@
 // written by exactly one workgroup, so both passes are deterministic).
 //
 // dK/dV pass: a workgroup owns 128 keys (4 wave64s x 32, one wave per SIMD) and walks the
-// query blocks of 64. K and V fragments stay in registers. Per query block each wave
+// query blocks of 64. With head_dim 64 the kernel is held to 256 registers (it fits
+// without spills), so two workgroups share a CU and each SIMD has a second wave to cover
+// the first one's LDS and MFMA latencies (+13-16% over one wave per SIMD); head_dim 128
+// needs ~400 registers and ~98 KiB of LDS, one workgroup per CU. K and V fragments stay in registers. Per query block each wave
 // computes S = Q K^T and dP = dO V^T (accumulator lane = one key, so P and dS feed the
 // next MFMAs as B operands straight from registers), then dV^T += dO^T P and
 // dK^T += Q^T dS with dO^T / Q^T read transposed (ds_read_b64_tr_b16) from the same
@@ -26,7 +29,7 @@ namespace {
 
 using namespace tk_attn;
 
-constexpr int kThreads = 256;  // 4 waves, one per SIMD
+constexpr int kThreads = 256;  // 4 waves, one per SIMD of the CU
 
 template <int N>
 __device__ __forceinline__ void wait_lgkm_n() {
@@ -230,7 +233,7 @@ __device__ __forceinline__ void pin_sub_rows(SubRows& r) {
 
 template <typename T, int D, bool CAUSAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(1, 1))) void
+                          amdgpu_waves_per_eu(D == 64 ? 2 : 1, D == 64 ? 2 : 1))) void
 attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
                          const T* __restrict__ V, const T* __restrict__ dO, T* __restrict__ dK,
                          T* __restrict__ dV, const float* __restrict__ lse,
