@@ -15,6 +15,13 @@ import math
 MAX_FEATURE_BYTES = 65_536
 EPS = 1e-5
 
+# Tile of the dweight stage-2 reduction (reference ``_norm_common.py:21-22`` names the
+# Triton block): a workgroup owns STAGE2_BLOCK_N columns and reads the partial rows in
+# STAGE2_BLOCK_M interleaved slices (``kStage2Slices`` x ``kStage2Cols`` in
+# csrc/rmsnorm.hip), folding the slices in a fixed order.
+STAGE2_BLOCK_M = 32
+STAGE2_BLOCK_N = 32
+
 # Groups of the backward dweight reduction: one workgroup per group. 512 groups
 # keep two 4-wave workgroups per compute unit (256 CUs) streaming rows, while the
 # float32 partial buffer stays at 512 x columns.
