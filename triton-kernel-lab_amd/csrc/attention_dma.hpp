@@ -11,6 +11,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -32,6 +33,36 @@ struct Mma<__bf16> {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
 };
+
+// v_mfma_f32_16x16x32: A lane l holds row l % 16, k = 8 (l / 16) .. +7; B lane l holds
+// column l % 16, the same k; D lane l holds column l % 16, rows 4 (l / 16) .. +3.
+template <typename T>
+struct Mma16;
+template <>
+struct Mma16<_Float16> {
+  static __device__ __forceinline__ f32x4 run(i32x4 a, i32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+template <>
+struct Mma16<__bf16> {
+  static __device__ __forceinline__ f32x4 run(i32x4 a, i32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+// Two 16x16 accumulators (4 registers each) rounded (RNE) to T: one MFMA operand whose
+// k-indices 0..3 are lo's registers and 4..7 hi's.
+template <typename T>
+__device__ __forceinline__ i32x4 acc_frag2(const f32x4& lo, const f32x4& hi) {
+  const f32x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  if constexpr (__is_same(T, __bf16))
+    return __builtin_bit_cast(i32x4, __builtin_convertvector(v, bf16x8));
+  else
+    return __builtin_bit_cast(i32x4, __builtin_convertvector(v, f16x8));
+}
 
 // Registers 8g .. 8g+7 of an accumulator rounded (RNE) to T: an MFMA operand.
 template <typename T>
@@ -67,6 +98,7 @@ __device__ __forceinline__ void wait_lgkm() {
 // Keeps every use of an LDS-read result below the preceding wait (volatile asm
 // statements stay in program order; this one redefines the value).
 __device__ __forceinline__ void pin(i32x4& f) { asm volatile("" : "+v"(f)); }
+__device__ __forceinline__ void pin(f32x4& f) { asm volatile("" : "+v"(f)); }
 
 // Barrier without __syncthreads()'s fence, which would wait for every outstanding DMA.
 __device__ __forceinline__ void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
@@ -103,6 +135,24 @@ __device__ __forceinline__ float max_with_partner(float x) {
 
 __device__ __forceinline__ float sum_with_partner(float x) {
   const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                   false, false);
+  return __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
+}
+
+// Maximum / sum over the four lanes l % 16 + 16 {0..3} (a 16x16 accumulator column):
+// a permlane32 swap pairs l with l ^ 32, a permlane16 swap then l with l ^ 16. Both
+// swaps return the lane's own and its partner's value (in either order), so every lane
+// of a column ends with the same result.
+__device__ __forceinline__ float max_over_column(float x) {
+  x = max_with_partner(x);
+  const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
+                                                   false, false);
+  return fmaxf(__uint_as_float(pr[0]), __uint_as_float(pr[1]));
+}
+
+__device__ __forceinline__ float sum_over_column(float x) {
+  x = sum_with_partner(x);
+  const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x),
                                                    false, false);
   return __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
 }

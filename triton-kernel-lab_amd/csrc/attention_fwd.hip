@@ -3,30 +3,38 @@
 // replaces: base-2 online softmax on scores * scale * log2(e) in _attention_inner
 // (:55-121), O = acc / l and log-sum-exp m + log2(l) (:248-264)).
 //
-// Workgroup: 256 queries, 8 wave64s of 32 queries, two waves per SIMD, so one wave's
-// softmax (VALU, transcendental) runs while the other wave's MFMAs occupy the matrix
-// pipe. Key/value blocks of 64.
+// Workgroup: 256 queries, 8 wave64s of 32 queries (two 16-query tiles), two waves per SIMD.
+// Key/value blocks of 64 (four 16-key tiles). All products are v_mfma_f32_16x16x32.
 //
-// Per wave and key block:
-//   S^T = K Q^T   2 key tiles (32 x 32) over D/16 k-steps: an accumulator lane owns one
-//                 query (column lane % 32) and 16 keys of each tile; the partner lane
-//                 lane ^ 32 holds the other keys, so row max/sum need one permlane32 swap.
-//   softmax       masked only on diagonal / ragged blocks; the O rescale is skipped when
-//                 no row max of the wave moved (alpha == 1 exactly).
-//   O^T += V^T P^T  D/32 feature tiles over 4 steps of 16 keys; P^T comes straight from
-//                 the S^T registers (registers 8g..8g+7 of a lane hold keys
-//                 16g + 4 hi + {0..3} and 16g + 8 + 4 hi + {0..3}), and V^T fragments
-//                 are read with ds_read_b64_tr_b16 from row-major V using exactly those
-//                 two 4-key row groups, so no data permutation is needed anywhere.
+// Per wave and key block j:
+//   S^T = K Q^T     4 key tiles x 2 query tiles over D/32 k-steps: lane l holds query
+//                   16 qt + l % 16 and keys 16 kt + 4 (l / 16) + {0..3}, so a query's
+//                   maximum and sum span the four lanes l % 16 + 16 {0..3} (permlane32 and
+//                   permlane16 swaps).
+//   softmax         masked only on diagonal / ragged blocks. The reference maximum only
+//                   moves when a block's maximum exceeds it by more than 2^8 (exponentials
+//                   stay <= 256), so O is rescaled in a few blocks rather than most, and
+//                   the cross-lane maximum is only formed when some lane's own maximum
+//                   would move it.
+//   O^T += V^T P^T  D/16 feature tiles x 2 query tiles over two 32-key steps; P^T comes
+//                   straight from the S^T registers (key tiles 2s and 2s + 1 give k-index
+//                   0..3 and 4..7 of lane group l / 16), and V^T fragments are read with
+//                   ds_read_b64_tr_b16 from row-major V rows in exactly that key order.
 // Q fragments stay in registers for the whole key loop.
 //
-// K and V blocks reach LDS by buffer->LDS DMA (no VGPR staging) into a 3-stage ring,
-// two blocks ahead; one barrier per block orders every reuse. LDS layouts keep every read
-// phase on 64 distinct banks:
+// Ping-pong: the barrier-separated phases alternate an MFMA phase M(j) (O^T += V_{j-1}^T
+// P_{j-1}^T, then S^T_j) and a softmax phase V(j); the two waves of each SIMD (found from
+// the hardware SIMD id) run opposite phases, so one wave's exponentials overlap the other's
+// MFMAs. Each phase's register results are pinned before its barrier so the compiler
+// cannot sink them into the next phase.
+//
+// K and V blocks reach LDS by buffer->LDS DMA (no VGPR staging) into a 4-stage ring; block
+// j is read in phases 2j .. 2j+3 and its stage is refilled at phase 2j+4. LDS layouts keep
+// every read phase on 64 distinct banks:
 //   K [64 keys][D]: 16-byte chunk c of row r at slot c ^ kswz(r) (ds_read_b128, 16 lanes
-//                   per phase read 16 rows of one chunk);
+//                   per phase read one chunk of 16 rows);
 //   V [64 keys][D]: 32-byte granule g of row r at granule g ^ vswz(r) (ds_read_b64_tr_b16,
-//                   32 lanes per phase read 4 rows x 2 granules).
+//                   32 lanes per phase read one granule of 8 rows).
 // The DMA writes 1 KiB contiguous per instruction, so the swizzle is applied on the global
 // side (each lane fetches the chunk that belongs in its LDS slot). LDS reads are inline
 // asm ordered by explicit waits: the compiler would otherwise wait for every outstanding
@@ -39,6 +47,7 @@ namespace {
 using namespace tk_attn;
 
 constexpr int kThreads = 512;
+constexpr float kLazyRescale = 8.f;
 
 struct Shape {
   int heads, seq;  // seq: the sequence length (varlen: the longest sequence)
@@ -84,27 +93,35 @@ __device__ __forceinline__ void rope_fragment(i32x4& x1, i32x4& x2, i32x4 c, i32
 template <int D>
 struct Geo {
   static constexpr int BM = 256, BN = 64, WAVES = 8, QW = 32;
-  static constexpr int KS = D / 16, DT = D / 32;
+  static constexpr int KS = D / 32;             // k-steps of S^T (32 features each)
+  static constexpr int KH = KS / 2;             // k-steps per half of the feature range
+  static constexpr int FT = D / 16;             // 16-feature tiles of O^T
   static constexpr int RB = D * 2;              // bytes per K/V row
   static constexpr int OPB = BN * RB;           // bytes per operand per stage
   static constexpr int STB = 2 * OPB;           // stage: K tile then V tile
-  static constexpr int STAGES = 3;
+  static constexpr int STAGES = 4;
   static constexpr int ROWS_PER_DMA = 1024 / RB;
   static constexpr int DMA_PER_OP = OPB / 1024 / WAVES;  // per wave, per operand
   static constexpr int DMA_PER_BLOCK = 2 * DMA_PER_OP;
   static constexpr int SLOTS = RB / 16;         // 16-byte slots per row
+  // K: 16-byte chunk c of row r at slot c ^ kswz(r). A read phase (16 lanes) takes one
+  // chunk of 16 consecutive rows.
   static __device__ __forceinline__ int kswz(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
-  static __device__ __forceinline__ int vswz(int r) { return D == 128 ? 2 * (r & 3) : 2 * ((r >> 1) & 1); }
+  // V: 32-byte granule g of row r at granule g ^ vswz(r). A transposed read phase (32
+  // lanes) takes one granule of 8 consecutive rows.
+  static __device__ __forceinline__ int vswz(int r) { return D == 128 ? (r & 7) : ((r >> 1) & 3); }
 };
 
-// DMA of key/value block `blk` (clamped to `last`: blocks past the end reload the last
-// one into a stage that is never read, keeping the per-block load count constant).
+// DMA of key/value block `blk` into its ring stage (clamped to `last`: blocks past the end
+// reload the last one into a stage that is never read, keeping the per-phase load count
+// constant).
 template <int D>
 __device__ __forceinline__ void dma_block(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
-                                          char* stage, const uint32_t* k_src,
+                                          char* lds, const uint32_t* k_src,
                                           const uint32_t* v_src, int blk, int last,
                                           uint32_t k_blk, uint32_t v_blk, int wave) {
   using G = Geo<D>;
+  char* stage = lds + (blk % G::STAGES) * G::STB;
   blk = min(blk, last);
 #pragma unroll
   for (int x = 0; x < G::DMA_PER_OP; ++x) {
@@ -116,14 +133,127 @@ __device__ __forceinline__ void dma_block(__amdgpu_buffer_rsrc_t rk, __amdgpu_bu
   }
 }
 
+// V^T fragment of the 32-key step starting at row ROW0 of a stage's V tile: rows
+// ROW0 + 4g .. +3 (k-index 0..3 of lane group g) and ROW0 + 16 + 4g .. +3 (k-index 4..7),
+// the key order of the P^T fragment built from key tiles 2s and 2s + 1.
+template <int ROW0, int RB>
+__device__ __forceinline__ i32x4 read_v16(uint32_t addr) {
+  const i32x2 a = lds_read_tr16<ROW0 * RB>(addr);
+  const i32x2 b = lds_read_tr16<(ROW0 + 16) * RB>(addr);
+  return i32x4{a[0], a[1], b[0], b[1]};
+}
+
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// The MFMA phase of one wave: O^T += V_{j-1}^T P^T from the previous softmax phase's pf
+// (DO_PV), then S^T(j) = K_j Q^T into st (DO_S). kb / vb: LDS addresses of the K tile of block j
+// and the V tile of block j-1. LDS reads are issued in groups, each awaited just before
+// the MFMAs that use it while the next group is in flight.
+// V fragments of one half-step (FT reads): vf[s][h][f] is 32-key step s, feature tile
+// h * FH + f of the V tile at vb.
+template <int D>
+__device__ __forceinline__ void read_v_group(i32x4 (&vf)[2][2][Geo<D>::FT / 2], uint32_t vb,
+                                             const uint32_t (&va)[Geo<D>::FT], int s, int h) {
+  constexpr int FH = Geo<D>::FT / 2, RB = Geo<D>::RB;
+#pragma unroll
+  for (int f = 0; f < FH; ++f)
+    vf[s][h][f] = s == 0 ? read_v16<0, RB>(vb + va[h * FH + f]) : read_v16<32, RB>(vb + va[h * FH + f]);
+}
+
+template <typename T, int D, bool DO_S, bool DO_PV>
+__device__ __forceinline__ void mfma_phase(uint32_t kb, uint32_t vb, const uint32_t (&ka)[Geo<D>::KS],
+                                           const uint32_t (&va)[Geo<D>::FT],
+                                           const i32x4 (&qf)[2][Geo<D>::KS], f32x4 (&st)[2][4],
+                                           const i32x4 (&pf)[2][2], f32x4 (&acc)[Geo<D>::FT][2],
+                                           i32x4 (&vf)[2][2][Geo<D>::FT / 2]) {
+  using G = Geo<D>;
+  constexpr int KS = G::KS, FT = G::FT, RB = G::RB, FH = FT / 2;
+  // K fragments: kf[kk][kt] is key tile kt (rows 16 kt + c), k-step kk (4 reads).
+  i32x4 kf[KS][4];
+  auto read_k = [&](int kk) {
+    const uint32_t a = kb + ka[kk];
+    kf[kk][0] = lds_read_b128<0>(a);
+    kf[kk][1] = lds_read_b128<16 * RB>(a);
+    kf[kk][2] = lds_read_b128<32 * RB>(a);
+    kf[kk][3] = lds_read_b128<48 * RB>(a);
+  };
+  auto read_v = [&](int s, int h) { read_v_group<D>(vf, vb, va, s, h); };
+  auto s_mfma = [&](int kk) {
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) pin(kf[kk][kt]);
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+        st[qt][kt] = Mma16<T>::run(kf[kk][kt], qf[qt][kk],
+                                   kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[qt][kt]);
+    sched_fence();
+  };
+  auto pv_mfma = [&](int s, int h) {
+#pragma unroll
+    for (int f = 0; f < FH; ++f) pin(vf[s][h][f]);
+#pragma unroll
+    for (int f = 0; f < FH; ++f)
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+        acc[h * FH + f][qt] = Mma16<T>::run(vf[s][h][f], pf[qt][s], acc[h * FH + f][qt]);
+    sched_fence();
+  };
+  // O^T += V^T P^T first, so the P^T fragments are dead before S^T is produced. Two or
+  // three read groups are in flight: the V half-steps (the first two were issued at the
+  // end of the preceding softmax phase), then the K k-steps (the first K groups are
+  // issued during the last V half-steps' MFMAs).
+  if constexpr (DO_PV) {
+    wait_lgkm<FT>();
+    pv_mfma(0, 0);
+    read_v(1, 0);
+    sched_fence();
+    wait_lgkm<FT>();
+    pv_mfma(0, 1);
+    read_v(1, 1);
+    sched_fence();
+    wait_lgkm<FT>();
+    pv_mfma(1, 0);
+    if constexpr (DO_S) read_k(0);
+    sched_fence();
+    wait_lgkm<DO_S ? 4 : 0>();
+    pv_mfma(1, 1);
+    if constexpr (DO_S) read_k(1);
+    sched_fence();
+  }
+  if constexpr (DO_S) {
+    if constexpr (!DO_PV) {
+      read_k(0);
+      read_k(1);
+      sched_fence();
+    }
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      if (kk + 1 < KS)
+        wait_lgkm<4>();
+      else
+        wait_lgkm<0>();
+      s_mfma(kk);
+      if (kk + 2 < KS) read_k(kk + 2);
+      sched_fence();
+    }
+  }
+}
+
+// SIMD of the executing wave (HW_ID bits 5:4).
+__device__ __forceinline__ int simd_id() {
+  return __builtin_amdgcn_s_getreg((1 << 11) | (4 << 6) | 4);
+}
+
 template <typename T, int D, bool CAUSAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads))) void
 attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                     T* __restrict__ O, float* __restrict__ lse, Shape s) {
   using G = Geo<D>;
-  constexpr int BM = G::BM, BN = G::BN, KS = G::KS, DT = G::DT, RB = G::RB, OPB = G::OPB,
-                STB = G::STB, STAGES = G::STAGES;
+  constexpr int BM = G::BM, BN = G::BN, KS = G::KS, FT = G::FT, RB = G::RB, OPB = G::OPB,
+                STB = G::STB, STAGES = G::STAGES, DPB = G::DMA_PER_BLOCK;
   __shared__ __attribute__((aligned(1024))) char lds[STAGES * STB];
+  __shared__ int simd_of[G::WAVES];
 
   // Workgroup -> (batch*head, query block). Equal lengths: XCD-contiguous ranges so a
   // head's blocks share one L2; causal: the heaviest (last) query block of a head first.
@@ -159,9 +289,10 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int l32 = lane & 31, hi = lane >> 5;
+  const int c = lane & 15, g = lane >> 4;
   const int q0 = qb * BM;
   const int wq0 = q0 + wave * G::QW;
+  if (lane == 0) simd_of[wave] = simd_id();
 
   const __amdgpu_buffer_rsrc_t rk =
       __builtin_amdgcn_make_buffer_rsrc((void*)Kh, (short)0, k_bytes, 0x00020000);
@@ -183,221 +314,233 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
   }
   const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
   const int kv_blocks = (kv_end + BN - 1) / BN;
+  const int last = kv_blocks - 1;
   const uint32_t k_blk = uint32_t(BN * s.k[2]) * 2u, v_blk = uint32_t(BN * s.v[2]) * 2u;
+  // The first STAGES - 1 blocks are fetched before anything else.
+#pragma unroll
+  for (int blk = 0; blk < STAGES - 1; ++blk)
+    dma_block<D>(rk, rv, lds, k_src, v_src, blk, last, k_blk, v_blk, wave);
 
-  // Q fragments (B operand of S^T): query wq0 + l32, features 16 kk + 8 hi .. +7.
-  i32x4 qf[KS];
-  {
-    const int query = wq0 + l32;
+  // Q fragments (B operand of S^T): query tile qt holds query wq0 + 16 qt + c, k-step kk
+  // features 32 kk + 8 g .. +7.
+  i32x4 qf[2][KS];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int query = wq0 + 16 * qt + c;
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk)
-      qf[kk] = query < N ? *reinterpret_cast<const i32x4*>(Qh + query * s.q[2] + kk * 16 + hi * 8)
-                         : i32x4{0, 0, 0, 0};
+      qf[qt][kk] = query < N
+                       ? *reinterpret_cast<const i32x4*>(Qh + query * s.q[2] + kk * 32 + g * 8)
+                       : i32x4{0, 0, 0, 0};
   }
-  // RoPE tables of this lane's query, loaded with Q; the rotation waits until the first
-  // K/V blocks' DMA has been issued.
-  const bool rope = s.rope_cos != nullptr && wq0 + l32 < N;
-  i32x4 rc[KS / 2], rsn[KS / 2];
-  if (rope) {
-    const int64_t at = int64_t(wq0 + l32) * s.rope_stride + hi * 8;
-    const T* cr = static_cast<const T*>(s.rope_cos) + at;
-    const T* sr = static_cast<const T*>(s.rope_sin) + at;
+  // RoPE: fragments kk and kk + KS/2 hold features 32 kk + 8 g .. +7 and the same + D/2,
+  // so the rotate-half pairs sit in one lane. Queries past the end keep zero tables (their
+  // Q is 0).
+  if (s.rope_cos != nullptr) {
 #pragma unroll
-    for (int kk = 0; kk < KS / 2; ++kk) {
-      rc[kk] = *reinterpret_cast<const i32x4*>(cr + kk * 16);
-      rsn[kk] = *reinterpret_cast<const i32x4*>(sr + kk * 16);
+    for (int qt = 0; qt < 2; ++qt) {
+      const int query = wq0 + 16 * qt + c;
+      const int64_t at = int64_t(query) * s.rope_stride + g * 8;
+      const T* cr = static_cast<const T*>(s.rope_cos) + at;
+      const T* sr = static_cast<const T*>(s.rope_sin) + at;
+#pragma unroll
+      for (int kk = 0; kk < KS / 2; ++kk) {
+        const i32x4 cv = query < N ? *reinterpret_cast<const i32x4*>(cr + kk * 32) : i32x4{0, 0, 0, 0};
+        const i32x4 sv = query < N ? *reinterpret_cast<const i32x4*>(sr + kk * 32) : i32x4{0, 0, 0, 0};
+        rope_fragment<T>(qf[qt][kk], qf[qt][kk + KS / 2], cv, sv);
+      }
     }
   }
-  // Lane read addresses inside a stage: K row l32 (+32 for the second key tile), chunk
-  // 2 kk + hi; V rows 4 hi + j (+16 per key step, +8 for k-index 4..7), features
-  // 32 dt + 16 g + 4 q .. +3.
-  uint32_t ka[KS], va[DT];
+  // Lane read addresses inside a stage: K row c of key tile kt (+16 kt rows), chunk
+  // 4 kk + g; V rows 4 g + j (+32 per key step, +16 for k-index 4..7), features
+  // 16 ft + 4 q .. +3, with j = c / 4, q = c % 4.
+  uint32_t ka[KS], va[FT];
 #pragma unroll
-  for (int kk = 0; kk < KS; ++kk) ka[kk] = l32 * RB + (((2 * kk + hi) ^ G::kswz(l32)) * 16);
+  for (int kk = 0; kk < KS; ++kk) ka[kk] = c * RB + (((4 * kk + g) ^ G::kswz(c)) * 16);
   {
-    const int g = (lane >> 4) & 1, j = (lane & 15) >> 2, q = lane & 3;
-    const int row = 4 * hi + j;
+    const int row = 4 * g + (c >> 2), q = c & 3;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      va[dt] = OPB + row * RB + (((2 * dt + g) ^ G::vswz(row)) * 32) + q * 8;
+    for (int ft = 0; ft < FT; ++ft) va[ft] = OPB + row * RB + ((ft ^ G::vswz(row)) * 32) + q * 8;
   }
 
-  f32x16 acc[DT];
+  // O^T accumulators: acc[ft][qt] register r is feature 16 ft + 4 g + r of query
+  // wq0 + 16 qt + c. st[qt][kt] register r: score of key n0 + 16 kt + 4 g + r.
+  f32x4 acc[FT][2], st[2][4];
+  i32x4 pf[2][2], vf[2][2][FT / 2];
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
+  for (int ft = 0; ft < FT; ++ft)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
-  float m_run = kNegInf, l_part = 0.f;
+    for (int qt = 0; qt < 2; ++qt) acc[ft][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {kNegInf, kNegInf}, l_part[2] = {0.f, 0.f};
   const float sl2 = s.scale_log2;
 
-  dma_block<D>(rk, rv, lds, k_src, v_src, 0, kv_blocks - 1, k_blk, v_blk, wave);
-  dma_block<D>(rk, rv, lds + STB, k_src, v_src, 1, kv_blocks - 1, k_blk, v_blk, wave);
-  // Fragments kk and kk + KS/2 hold features 16 kk + 8 hi .. +7 and the same + D/2: the
-  // rotate-half pairs sit in one lane.
-  if (rope) {
+  // Block 0 landed; simd_of visible.
+  wait_lgkm<0>();
+  wait_vmcnt<(STAGES - 2) * DPB>();
+  barrier_no_fence();
+  // Ping-pong: the two waves that share a SIMD take opposite phases. The workgroup runs
+  // phases t = 0, 1, ... separated by barriers; a wave alternates an MFMA phase M(j)
+  // (S^T of block j, O^T += V^T P^T of block j-1) and a softmax phase V(j), the second
+  // wave of each SIMD one phase behind the first, so one wave's exponentials run while
+  // the other's MFMAs occupy the matrix pipe. Block j is read in phases 2j .. 2j+3; at
+  // the start of phase 2m (m >= 1) its stage's next block m + STAGES - 2 is fetched,
+  // and block m must have landed before phase 2m begins.
+  int grp = 0;
 #pragma unroll
-    for (int kk = 0; kk < KS / 2; ++kk) rope_fragment<T>(qf[kk], qf[kk + KS / 2], rc[kk], rsn[kk]);
-  }
-  int stage = 0, fill = 2;
-  // This wave multiplies a prefix of the workgroup's blocks (causal: those starting at or
-  // before its last query) and only helps to load the rest.
-  const int wave_blocks = CAUSAL ? min(kv_blocks, (wq0 + G::QW - 1) / BN + 1) : kv_blocks;
-  int j = 0;
-  for (; j < wave_blocks; ++j) {
-    // Block j has landed once only block j+1's loads are pending; the barrier makes every
-    // wave's share visible and retires all reads of block j-1, whose stage is refilled.
-    wait_vmcnt<G::DMA_PER_BLOCK>();
+  for (int w = 0; w < G::WAVES; ++w) grp += (w < wave && simd_of[w] == simd_of[wave]) ? 1 : 0;
+  grp = __builtin_amdgcn_readfirstlane(grp) & 1;
+  const int phases = 2 * kv_blocks + 2;
+  int t = 0;
+  auto end_phase = [&]() {
+    if (t & 1) wait_vmcnt<(STAGES - 3) * DPB>();
     barrier_no_fence();
-    dma_block<D>(rk, rv, lds + fill * STB, k_src, v_src, j + 2, kv_blocks - 1, k_blk, v_blk,
-                 wave);
+    ++t;
+    if (!(t & 1))
+      dma_block<D>(rk, rv, lds, k_src, v_src, (t >> 1) + STAGES - 2, last, k_blk, v_blk, wave);
+  };
+  auto kbase = [&](int j) { return lds_base + (j % STAGES) * STB; };
+
+  // Softmax phase of block j: P = exp2(S * scale * log2(e) - m) into pf, the running
+  // statistics updated. The reference maximum m_run only moves when the block's maximum
+  // exceeds it by more than kLazyRescale (log2 units): exponentials stay
+  // <= 2^kLazyRescale, and O and l are rescaled in few blocks instead of whenever one of
+  // the wave's 32 maxima grows. O = acc / l and the log-sum-exp m_run + log2(l) do not
+  // depend on which reference is used.
+  auto softmax_phase = [&](int j) {
     const int n0 = j * BN;
-    const uint32_t base = lds_base + stage * STB;
-
-    // S^T = K Q^T; the second half of the feature range is read during the first's MFMAs.
-    i32x4 kf[2][2][KS / 2];
-#pragma unroll
-    for (int half = 0; half < 2; ++half)
-#pragma unroll
-      for (int i = 0; i < KS / 2; ++i) {
-        kf[half][0][i] = lds_read_b128<0>(base + ka[half * (KS / 2) + i]);
-        kf[half][1][i] = lds_read_b128<32 * RB>(base + ka[half * (KS / 2) + i]);
-      }
-    f32x16 st[2];
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      if (half == 0)
-        wait_lgkm<KS>();  // the KS reads of the second half may still be in flight
-      else
-        wait_lgkm<0>();
-#pragma unroll
-      for (int i = 0; i < KS / 2; ++i) {
-        pin(kf[half][0][i]);
-        pin(kf[half][1][i]);
-      }
-#pragma unroll
-      for (int i = 0; i < KS / 2; ++i) {
-        const int kk = half * (KS / 2) + i;
-        if (kk == 0) {
-          const f32x16 z = {};
-          st[0] = Mma<T>::run(kf[0][0][0], qf[0], z);
-          st[1] = Mma<T>::run(kf[0][1][0], qf[0], z);
-        } else {
-          st[0] = Mma<T>::run(kf[half][0][i], qf[kk], st[0]);
-          st[1] = Mma<T>::run(kf[half][1][i], qf[kk], st[1]);
-        }
-      }
-    }
-
-    // Online softmax for query wq0 + l32. Register r of key tile nt holds key
-    // n0 + 32 nt + 4 hi + 8 (r / 4) + r % 4.
-    const int query = wq0 + l32;
     const bool need_mask = n0 + BN > N || (CAUSAL && n0 + BN - 1 > wq0);
     if (__builtin_expect(need_mask, 0)) {
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        int lim = N - 1 - (n0 + nt * 32 + 4 * hi);  // last valid offset from the lane's first key
-        if (CAUSAL) lim = min(lim, query - (n0 + nt * 32 + 4 * hi));
+      for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (((r >> 2) << 3) + (r & 3) > lim) st[nt][r] = kNegInf;
+        for (int kt = 0; kt < 4; ++kt) {
+          const int k0 = n0 + 16 * kt + 4 * g;  // the lane's first key of this tile
+          int lim = N - 1 - k0;                 // last valid offset from k0
+          if (CAUSAL) lim = min(lim, wq0 + 16 * qt + c - k0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (r > lim) st[qt][kt][r] = kNegInf;
+        }
+    }
+    // A column's maximum exceeds the threshold only if one of its four lanes' does: the
+    // cross-lane reduction runs only when some lane of the wave sees such a maximum.
+    float mx[2];
+    bool move[2];
+    float m_new[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      mx[qt] = kNegInf;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx[qt] = fmaxf(mx[qt], st[qt][kt][r]);
+      move[qt] = mx[qt] * sl2 > m_run[qt] + kLazyRescale;
+      m_new[qt] = m_run[qt];
+    }
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(move[0] || move[1]) != 0, 0)) {
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const float bm = max_over_column(mx[qt]) * sl2;
+        move[qt] = bm > m_run[qt] + kLazyRescale;
+        m_new[qt] = move[qt] ? bm : m_run[qt];
       }
     }
-    float mx = kNegInf;
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int qt = 0; qt < 2; ++qt) {
+      const float neg = -m_new[qt];
+      float sum = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[nt][r]);
-    mx = max_with_partner(mx);
-    const float m_new = fmaxf(m_run, mx * sl2);
-
-    // First two 16-key steps of V^T, read while the exponentials run.
-    i32x4 vf[2][DT];
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      vf[0][dt] = read_v<0, RB>(base + va[dt]);
-      vf[1][dt] = read_v<16, RB>(base + va[dt]);
-    }
-    const float neg = -m_new;
-    float sum = 0.f;
+        for (int r = 0; r < 4; ++r) {
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qt][kt][r], sl2, neg));
+          st[qt][kt][r] = p;
+          sum += p;
+        }
+      if (__builtin_amdgcn_ballot_w64(move[qt])) {
+        const float alpha = move[qt] ? __builtin_amdgcn_exp2f(m_run[qt] - m_new[qt]) : 1.f;
+        l_part[qt] *= alpha;
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[nt][r], sl2, neg));
-        st[nt][r] = p;
-        sum += p;
+        for (int ft = 0; ft < FT; ++ft) acc[ft][qt] *= alpha;
       }
-    const float alpha = m_new == kNegInf ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-    l_part = l_part * alpha + sum;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+      l_part[qt] += sum;
+      m_run[qt] = m_new[qt];
+      pf[qt][0] = acc_frag2<T>(st[qt][0], st[qt][1]);
+      pf[qt][1] = acc_frag2<T>(st[qt][2], st[qt][3]);
     }
-    m_run = m_new;
-    const i32x4 pf[4] = {acc_frag<T>(st[0], 0), acc_frag<T>(st[0], 1), acc_frag<T>(st[1], 0),
-                         acc_frag<T>(st[1], 1)};
+  };
 
-    // O^T += V^T P^T; the last two key steps are read during the first two's MFMAs.
-    wait_lgkm<0>();
+  // This wave multiplies a prefix of the workgroup's blocks (causal: those starting at or
+  // before its last query); every wave takes part in every phase's barrier and loads.
+  const int n = CAUSAL ? min(kv_blocks, (wq0 + G::QW - 1) / BN + 1) : kv_blocks;
+  // The loop is entered after M(0) and leaves before V(n-1) (with the softmax phase first
+  // in the body the compiler keeps one copy of the O accumulators across the back edge).
+  // A phase's results are pinned before its closing barrier: the barrier orders memory
+  // only, and the compiler would otherwise sink register work (the exponentials, the
+  // MFMA chains) into the next phase, where it runs beside the partner wave's same kind
+  // of work.
+  auto pin_mfma = [&]() {
 #pragma unroll
-    for (int g = 0; g < 2; ++g)
+    for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) pin(vf[g][dt]);
-    i32x4 vf2[2][DT];
+      for (int kt = 0; kt < 4; ++kt) pin(st[qt][kt]);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      vf2[0][dt] = read_v<32, RB>(base + va[dt]);
-      vf2[1][dt] = read_v<48, RB>(base + va[dt]);
+    for (int ft = 0; ft < FT; ++ft)
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) pin(acc[ft][qt]);
+  };
+  // The softmax phase ends by issuing the first two V half-steps of the next MFMA phase
+  // (block j's V tile has landed since phase 2j).
+  auto pin_softmax = [&](int j) {
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      pin(pf[qt][0]);
+      pin(pf[qt][1]);
+      asm volatile("" : "+v"(l_part[qt]), "+v"(m_run[qt]));
     }
-#pragma unroll
-    for (int g = 0; g < 2; ++g)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt] = Mma<T>::run(vf[g][dt], pf[g], acc[dt]);
-    wait_lgkm<0>();
-#pragma unroll
-    for (int g = 0; g < 2; ++g)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) pin(vf2[g][dt]);
-#pragma unroll
-    for (int g = 0; g < 2; ++g)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt] = Mma<T>::run(vf2[g][dt], pf[2 + g], acc[dt]);
-
-    stage = stage + 1 == STAGES ? 0 : stage + 1;
-    fill = fill + 1 == STAGES ? 0 : fill + 1;
+    read_v_group<D>(vf, kbase(j), va, 0, 0);
+    read_v_group<D>(vf, kbase(j), va, 0, 1);
+  };
+  if (grp) end_phase();
+  mfma_phase<T, D, true, false>(kbase(0), 0, ka, va, qf, st, pf, acc, vf);
+  pin_mfma();
+  end_phase();
+  for (int j = 1; j < n; ++j) {
+    softmax_phase(j - 1);
+    pin_softmax(j - 1);
+    end_phase();
+    mfma_phase<T, D, true, true>(kbase(j), kbase(j - 1), ka, va, qf, st, pf, acc, vf);
+    pin_mfma();
+    end_phase();
   }
-  for (; j < kv_blocks; ++j) {
-    wait_vmcnt<G::DMA_PER_BLOCK>();
-    barrier_no_fence();
-    dma_block<D>(rk, rv, lds + fill * STB, k_src, v_src, j + 2, kv_blocks - 1, k_blk, v_blk,
-                 wave);
-    fill = fill + 1 == STAGES ? 0 : fill + 1;
-  }
+  softmax_phase(n - 1);
+  pin_softmax(n - 1);
+  end_phase();
+  mfma_phase<T, D, false, true>(0, kbase(n - 1), ka, va, qf, st, pf, acc, vf);
+  while (t < phases - 1) end_phase();
   // No DMA may still be writing when the workgroup's LDS is released.
   wait_vmcnt<0>();
 
-  // O = O^T / l: register r of tile dt is feature 32 dt + 8 (r / 4) + 4 hi + r % 4.
-  const float l = sum_with_partner(l_part);
-  const float inv = 1.0f / l;
-  const int query = wq0 + l32;
-  if (query < N) {
-    T* orow = Oh + query * s.o[2];
+  // O = O^T / l: acc[ft][qt] register r is feature 16 ft + 4 g + r.
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int qt = 0; qt < 2; ++qt) {
+    const float l = sum_over_column(l_part[qt]);
+    const float inv = 1.0f / l;
+    const int query = wq0 + 16 * qt + c;
+    if (query < N) {
+      T* orow = Oh + query * s.o[2];
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int d = dt * 32 + g4 * 8 + hi * 4;
+      for (int ft = 0; ft < FT; ++ft) {
         uint2 u;
-        u.x = pack2<T>(acc[dt][g4 * 4 + 0] * inv, acc[dt][g4 * 4 + 1] * inv);
-        u.y = pack2<T>(acc[dt][g4 * 4 + 2] * inv, acc[dt][g4 * 4 + 3] * inv);
-        *reinterpret_cast<uint2*>(orow + d) = u;
+        u.x = pack2<T>(acc[ft][qt][0] * inv, acc[ft][qt][1] * inv);
+        u.y = pack2<T>(acc[ft][qt][2] * inv, acc[ft][qt][3] * inv);
+        *reinterpret_cast<uint2*>(orow + ft * 16 + g * 4) = u;
       }
-    if (lse != nullptr && hi == 0) {
-      const int64_t at = s.cu != nullptr ? int64_t(h) * s.total + start + query
-                                         : (int64_t(b) * s.heads + h) * N + query;
-      lse[at] = m_run + __log2f(l);
+      if (lse != nullptr && g == 0) {
+        const int64_t at = s.cu != nullptr ? int64_t(h) * s.total + start + query
+                                           : (int64_t(b) * s.heads + h) * N + query;
+        lse[at] = m_run[qt] + __log2f(l);
+      }
     }
   }
 }
