@@ -149,94 +149,98 @@ __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0
 // (DO_PV), then S^T(j) = K_j Q^T into st (DO_S). kb / vb: LDS addresses of the K tile of block j
 // and the V tile of block j-1. LDS reads are issued in groups, each awaited just before
 // the MFMAs that use it while the next group is in flight.
-// V fragments of one half-step (FT reads): vf[s][h][f] is 32-key step s, feature tile
-// h * FH + f of the V tile at vb.
+// The MFMA phase as a pipeline of read units of four LDS instructions each: V units
+// (u < NV) hold 32-key step s = u / (FT/2) of feature tiles 2p and 2p+1 (p = u % (FT/2)),
+// K units (u >= NV) k-step kk = u - NV of the four key tiles. Unit u's MFMAs run while
+// units u+1 .. u+DEPTH-1 are in flight.
 template <int D>
-__device__ __forceinline__ void read_v_group(i32x4 (&vf)[2][2][Geo<D>::FT / 2], uint32_t vb,
-                                             const uint32_t (&va)[Geo<D>::FT], int s, int h) {
-  constexpr int FH = Geo<D>::FT / 2, RB = Geo<D>::RB;
+struct Units {
+  static constexpr int FP = Geo<D>::FT / 2;  // feature-tile pairs per 32-key step
+  static constexpr int NV = 2 * FP;          // V units of a block
+  // Units in flight, and V units issued at the end of the softmax phase (at most 15 LDS
+  // reads may be in flight before a wave's issue stalls). head_dim 64 keeps fewer in
+  // flight to stay within 128 registers.
+  static constexpr int DEPTH = D == 64 ? 3 : 4;
+  static constexpr int PREFETCH = D == 64 ? 2 : 3;
+};
+
+// Issues V unit u of the V tile at vb into vu[u].
+template <int D>
+__device__ __forceinline__ void read_v_unit(i32x4 (&vu)[Units<D>::NV][2], uint32_t vb,
+                                            const uint32_t (&va)[Geo<D>::FT], int u) {
+  constexpr int FP = Units<D>::FP, RB = Geo<D>::RB;
+  const int s = u / FP, p = u % FP;
 #pragma unroll
-  for (int f = 0; f < FH; ++f)
-    vf[s][h][f] = s == 0 ? read_v16<0, RB>(vb + va[h * FH + f]) : read_v16<32, RB>(vb + va[h * FH + f]);
+  for (int i = 0; i < 2; ++i)
+    vu[u][i] = s == 0 ? read_v16<0, RB>(vb + va[2 * p + i]) : read_v16<32, RB>(vb + va[2 * p + i]);
 }
 
+// The MFMA phase of one wave: O^T += V_{j-1}^T P^T from the previous softmax phase's pf
+// (DO_PV; P^T is dead before S^T is produced), then S^T(j) = K_j Q^T into st (DO_S).
+// kb / vb: LDS addresses of the K tile of block j and the V tile of block j-1. With DO_PV
+// the first PREFETCH V units were issued by the preceding softmax phase.
 template <typename T, int D, bool DO_S, bool DO_PV>
 __device__ __forceinline__ void mfma_phase(uint32_t kb, uint32_t vb, const uint32_t (&ka)[Geo<D>::KS],
                                            const uint32_t (&va)[Geo<D>::FT],
                                            const i32x4 (&qf)[2][Geo<D>::KS], f32x4 (&st)[2][4],
                                            const i32x4 (&pf)[2][2], f32x4 (&acc)[Geo<D>::FT][2],
-                                           i32x4 (&vf)[2][2][Geo<D>::FT / 2]) {
+                                           i32x4 (&vu)[Units<D>::NV][2]) {
   using G = Geo<D>;
-  constexpr int KS = G::KS, FT = G::FT, RB = G::RB, FH = FT / 2;
-  // K fragments: kf[kk][kt] is key tile kt (rows 16 kt + c), k-step kk (4 reads).
+  constexpr int KS = G::KS, RB = G::RB, FP = Units<D>::FP;
+  constexpr int NV = DO_PV ? Units<D>::NV : 0, NU = NV + (DO_S ? KS : 0);
+  constexpr int DEPTH = Units<D>::DEPTH;
+  constexpr int PRE = DO_PV ? Units<D>::PREFETCH : 0;  // units issued before the phase
+  static_assert(!DO_PV || Units<D>::NV >= PRE, "the prefetched units are V units");
   i32x4 kf[KS][4];
-  auto read_k = [&](int kk) {
-    const uint32_t a = kb + ka[kk];
-    kf[kk][0] = lds_read_b128<0>(a);
-    kf[kk][1] = lds_read_b128<16 * RB>(a);
-    kf[kk][2] = lds_read_b128<32 * RB>(a);
-    kf[kk][3] = lds_read_b128<48 * RB>(a);
-  };
-  auto read_v = [&](int s, int h) { read_v_group<D>(vf, vb, va, s, h); };
-  auto s_mfma = [&](int kk) {
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) pin(kf[kk][kt]);
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
-        st[qt][kt] = Mma16<T>::run(kf[kk][kt], qf[qt][kk],
-                                   kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[qt][kt]);
-    sched_fence();
-  };
-  auto pv_mfma = [&](int s, int h) {
-#pragma unroll
-    for (int f = 0; f < FH; ++f) pin(vf[s][h][f]);
-#pragma unroll
-    for (int f = 0; f < FH; ++f)
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
-        acc[h * FH + f][qt] = Mma16<T>::run(vf[s][h][f], pf[qt][s], acc[h * FH + f][qt]);
-    sched_fence();
-  };
-  // O^T += V^T P^T first, so the P^T fragments are dead before S^T is produced. Two or
-  // three read groups are in flight: the V half-steps (the first two were issued at the
-  // end of the preceding softmax phase), then the K k-steps (the first K groups are
-  // issued during the last V half-steps' MFMAs).
-  if constexpr (DO_PV) {
-    wait_lgkm<FT>();
-    pv_mfma(0, 0);
-    read_v(1, 0);
-    sched_fence();
-    wait_lgkm<FT>();
-    pv_mfma(0, 1);
-    read_v(1, 1);
-    sched_fence();
-    wait_lgkm<FT>();
-    pv_mfma(1, 0);
-    if constexpr (DO_S) read_k(0);
-    sched_fence();
-    wait_lgkm<DO_S ? 4 : 0>();
-    pv_mfma(1, 1);
-    if constexpr (DO_S) read_k(1);
-    sched_fence();
-  }
-  if constexpr (DO_S) {
-    if constexpr (!DO_PV) {
-      read_k(0);
-      read_k(1);
-      sched_fence();
+  auto issue = [&](int u) {
+    if (u < NV) {
+      read_v_unit<D>(vu, vb, va, u);
+    } else {
+      const int kk = u - NV;
+      const uint32_t a = kb + ka[kk];
+      kf[kk][0] = lds_read_b128<0>(a);
+      kf[kk][1] = lds_read_b128<16 * RB>(a);
+      kf[kk][2] = lds_read_b128<32 * RB>(a);
+      kf[kk][3] = lds_read_b128<48 * RB>(a);
     }
+  };
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      if (kk + 1 < KS)
-        wait_lgkm<4>();
-      else
-        wait_lgkm<0>();
-      s_mfma(kk);
-      if (kk + 2 < KS) read_k(kk + 2);
-      sched_fence();
+  for (int u = PRE; u < DEPTH && u < NU; ++u) issue(u);
+  sched_fence();
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    // Units u+1 .. min(u+DEPTH, NU)-1 may still be in flight (four instructions each).
+    const int after = (u + DEPTH < NU ? u + DEPTH : NU) - (u + 1);
+    if (after >= 3)
+      wait_lgkm<12>();
+    else if (after == 2)
+      wait_lgkm<8>();
+    else if (after == 1)
+      wait_lgkm<4>();
+    else
+      wait_lgkm<0>();
+    if (u < NV) {
+      const int s = u / FP, p = u % FP;
+      pin(vu[u][0]);
+      pin(vu[u][1]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+          acc[2 * p + i][qt] = Mma16<T>::run(vu[u][i], pf[qt][s], acc[2 * p + i][qt]);
+    } else {
+      const int kk = u - NV;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) pin(kf[kk][kt]);
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+          st[qt][kt] = Mma16<T>::run(kf[kk][kt], qf[qt][kk],
+                                     kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[qt][kt]);
     }
+    if (u + DEPTH < NU) issue(u + DEPTH);
+    sched_fence();
   }
 }
 
@@ -245,8 +249,11 @@ __device__ __forceinline__ int simd_id() {
   return __builtin_amdgcn_s_getreg((1 << 11) | (4 << 6) | 4);
 }
 
+// head_dim 64 uses 64 KiB of LDS per workgroup: held to 128 registers, two workgroups
+// share a CU (four waves per SIMD).
 template <typename T, int D, bool CAUSAL>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads))) void
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(D == 64 ? 4 : 2))) void
 attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
                     T* __restrict__ O, float* __restrict__ lse, Shape s) {
   using G = Geo<D>;
@@ -366,7 +373,7 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
   // O^T accumulators: acc[ft][qt] register r is feature 16 ft + 4 g + r of query
   // wq0 + 16 qt + c. st[qt][kt] register r: score of key n0 + 16 kt + 4 g + r.
   f32x4 acc[FT][2], st[2][4];
-  i32x4 pf[2][2], vf[2][2][FT / 2];
+  i32x4 pf[2][2], vu[Units<D>::NV][2];
 #pragma unroll
   for (int ft = 0; ft < FT; ++ft)
 #pragma unroll
@@ -489,7 +496,7 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) pin(acc[ft][qt]);
   };
-  // The softmax phase ends by issuing the first two V half-steps of the next MFMA phase
+  // The softmax phase ends by issuing the first PREFETCH V units of the next MFMA phase
   // (block j's V tile has landed since phase 2j).
   auto pin_softmax = [&](int j) {
 #pragma unroll
@@ -498,25 +505,25 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
       pin(pf[qt][1]);
       asm volatile("" : "+v"(l_part[qt]), "+v"(m_run[qt]));
     }
-    read_v_group<D>(vf, kbase(j), va, 0, 0);
-    read_v_group<D>(vf, kbase(j), va, 0, 1);
+#pragma unroll
+    for (int u = 0; u < Units<D>::PREFETCH; ++u) read_v_unit<D>(vu, kbase(j), va, u);
   };
   if (grp) end_phase();
-  mfma_phase<T, D, true, false>(kbase(0), 0, ka, va, qf, st, pf, acc, vf);
+  mfma_phase<T, D, true, false>(kbase(0), 0, ka, va, qf, st, pf, acc, vu);
   pin_mfma();
   end_phase();
   for (int j = 1; j < n; ++j) {
     softmax_phase(j - 1);
     pin_softmax(j - 1);
     end_phase();
-    mfma_phase<T, D, true, true>(kbase(j), kbase(j - 1), ka, va, qf, st, pf, acc, vf);
+    mfma_phase<T, D, true, true>(kbase(j), kbase(j - 1), ka, va, qf, st, pf, acc, vu);
     pin_mfma();
     end_phase();
   }
   softmax_phase(n - 1);
   pin_softmax(n - 1);
   end_phase();
-  mfma_phase<T, D, false, true>(0, kbase(n - 1), ka, va, qf, st, pf, acc, vf);
+  mfma_phase<T, D, false, true>(0, kbase(n - 1), ka, va, qf, st, pf, acc, vu);
   while (t < phases - 1) end_phase();
   // No DMA may still be writing when the workgroup's LDS is released.
   wait_vmcnt<0>();
