@@ -80,6 +80,35 @@ def test_matches_the_oracle(dtype, d, causal, n) -> None:
     torch.testing.assert_close(lse, dev(lse_ref, lse), rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("kind", ["ramp", "large"])
+def test_running_maximum_moves_often(dtype, d, causal, kind) -> None:
+    """Scores that grow along the keys (each 64-key block's maximum exceeds the previous
+    block's by far more than 2^8 in base 2) and large random logits: the kernel's reference
+    maximum moves in most blocks, and the result still matches the oracle."""
+    torch.manual_seed(17 + d + int(causal))
+    n = 300
+    shape = (1, 2, n, d)
+    if kind == "ramp":
+        q = 1 + 0.1 * torch.randn(shape, device="cuda")
+        ramp = (0.1 * torch.arange(n, device="cuda", dtype=torch.float32))[:, None]
+        k = ramp + 0.1 * torch.randn(shape, device="cuda")
+    else:
+        q = 6 * torch.randn(shape, device="cuda")
+        k = torch.randn(shape, device="cuda")
+    q, k = q.to(dtype), k.to(dtype)
+    v = torch.randn(shape, device="cuda", dtype=dtype)
+    out = torch.empty_like(q)
+    lse = torch.empty(shape[:-1], device="cuda", dtype=torch.float32)
+    _launch_forward(q, k, v, out, lse, causal=causal, store_lse=True)
+    o_ref, lse_ref = oracle.attn_fwd(host(q), host(k), host(v), d ** -0.5, causal, name(dtype))
+    assert torch.isfinite(out).all()
+    assert_close(out, dev(o_ref, out))
+    torch.testing.assert_close(lse, dev(lse_ref, lse), rtol=1e-5, atol=1e-5)
+
+
 def test_inference_and_training_forward_agree_bitwise() -> None:
     torch.manual_seed(5)
     q, k, v = (torch.randn(1, 4, 700, 128, device="cuda", dtype=torch.bfloat16) for _ in range(3))

@@ -429,51 +429,106 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
             if (r > lim) st[qt][kt][r] = kNegInf;
         }
     }
-    // A column's maximum exceeds the threshold only if one of its four lanes' does: the
-    // cross-lane reduction runs only when some lane of the wave sees such a maximum.
-    float mx[2];
-    bool move[2];
-    float m_new[2];
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      mx[qt] = kNegInf;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mx[qt] = fmaxf(mx[qt], st[qt][kt][r]);
-      move[qt] = mx[qt] * sl2 > m_run[qt] + kLazyRescale;
-      m_new[qt] = m_run[qt];
-    }
-    if (__builtin_expect(__builtin_amdgcn_ballot_w64(move[0] || move[1]) != 0, 0)) {
+    if constexpr (D == 128) {
+      // Exponentials against the current reference first. A lane whose 16 exponentials of a
+      // query sum to at most 2^kLazyRescale has none above it, so when no lane of the wave
+      // exceeds that sum no reference moves and no maximum is needed. Otherwise the column
+      // maxima are formed from the scores, which are still intact, and the queries whose
+      // reference moves are recomputed.
+      f32x4 p[2][4];
+      float sum[2];
+      auto exps = [&](int qt) {
+        const float neg = -m_run[qt];
+  #pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+          for (int r = 0; r < 4; ++r)
+            p[qt][kt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qt][kt][r], sl2, neg));
+        float s0 = p[qt][0][0];
+  #pragma unroll
+        for (int i = 1; i < 16; ++i) s0 += p[qt][i / 4][i % 4];
+        sum[qt] = s0;
+      };
+      exps(0);
+      exps(1);
+      constexpr float kLazyLimit = 256.f;  // 2^kLazyRescale
+      if (__builtin_expect(
+              __builtin_amdgcn_ballot_w64(!(sum[0] <= kLazyLimit) || !(sum[1] <= kLazyLimit)) != 0,
+              0)) {
+  #pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+          float mx = kNegInf;
+  #pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[qt][kt][r]);
+          const float bm = max_over_column(mx) * sl2;
+          const bool move = bm > m_run[qt] + kLazyRescale;
+          if (__builtin_amdgcn_ballot_w64(move)) {
+            const float m_new = move ? bm : m_run[qt];
+            const float alpha = move ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.f;
+            l_part[qt] *= alpha;
+  #pragma unroll
+            for (int ft = 0; ft < FT; ++ft) acc[ft][qt] *= alpha;
+            m_run[qt] = m_new;
+            exps(qt);
+          }
+        }
+      }
+  #pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        l_part[qt] += sum[qt];
+        pf[qt][0] = acc_frag2<T>(p[qt][0], p[qt][1]);
+        pf[qt][1] = acc_frag2<T>(p[qt][2], p[qt][3]);
+      }
+    } else {
+      // head_dim 64 (128 registers): the exponentials overwrite the scores, so the maximum
+      // comes first. A column's maximum exceeds the threshold only if one of its four
+      // lanes' does: the cross-lane reduction runs only when some lane of the wave sees
+      // such a maximum.
+      float mx[2], m_new[2];
+      bool move[2];
 #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
-        const float bm = max_over_column(mx[qt]) * sl2;
-        move[qt] = bm > m_run[qt] + kLazyRescale;
-        m_new[qt] = move[qt] ? bm : m_run[qt];
+        mx[qt] = kNegInf;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mx[qt] = fmaxf(mx[qt], st[qt][kt][r]);
+        move[qt] = mx[qt] * sl2 > m_run[qt] + kLazyRescale;
+        m_new[qt] = m_run[qt];
       }
-    }
+      if (__builtin_expect(__builtin_amdgcn_ballot_w64(move[0] || move[1]) != 0, 0)) {
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      const float neg = -m_new[qt];
-      float sum = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qt][kt][r], sl2, neg));
-          st[qt][kt][r] = p;
-          sum += p;
+        for (int qt = 0; qt < 2; ++qt) {
+          const float bm = max_over_column(mx[qt]) * sl2;
+          move[qt] = bm > m_run[qt] + kLazyRescale;
+          m_new[qt] = move[qt] ? bm : m_run[qt];
         }
-      if (__builtin_amdgcn_ballot_w64(move[qt])) {
-        const float alpha = move[qt] ? __builtin_amdgcn_exp2f(m_run[qt] - m_new[qt]) : 1.f;
-        l_part[qt] *= alpha;
-#pragma unroll
-        for (int ft = 0; ft < FT; ++ft) acc[ft][qt] *= alpha;
       }
-      l_part[qt] += sum;
-      m_run[qt] = m_new[qt];
-      pf[qt][0] = acc_frag2<T>(st[qt][0], st[qt][1]);
-      pf[qt][1] = acc_frag2<T>(st[qt][2], st[qt][3]);
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const float neg = -m_new[qt];
+        float sum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qt][kt][r], sl2, neg));
+            st[qt][kt][r] = pv;
+            sum += pv;
+          }
+        if (__builtin_amdgcn_ballot_w64(move[qt])) {
+          const float alpha = move[qt] ? __builtin_amdgcn_exp2f(m_run[qt] - m_new[qt]) : 1.f;
+          l_part[qt] *= alpha;
+#pragma unroll
+          for (int ft = 0; ft < FT; ++ft) acc[ft][qt] *= alpha;
+        }
+        l_part[qt] += sum;
+        m_run[qt] = m_new[qt];
+        pf[qt][0] = acc_frag2<T>(st[qt][0], st[qt][1]);
+        pf[qt][1] = acc_frag2<T>(st[qt][2], st[qt][3]);
+      }
     }
   };
 
