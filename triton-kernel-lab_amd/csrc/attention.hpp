@@ -1,5 +1,5 @@
 // Internal interface between the attention entry points (attention.hip) and the
-// buffer->LDS DMA kernels (attention_fwd.hip, attention_bwd.hip). `kv_heads` divides
+// buffer->LDS DMA kernels (attention_fwd.hip, attention_bwd.hip, attention_bwd_dq.hip). `kv_heads` divides
 // `heads`: query head h reads K/V head h / (heads / kv_heads) (kv_heads == heads is
 // multi-head attention). With `cu_seqlens` (int32[batch + 1]) the batch is variable-length:
 // sequence b is rows cu_seqlens[b] .. cu_seqlens[b + 1] of a packed [total][head][dim]
@@ -40,6 +40,7 @@ void attn_bwd_dkdv_dma_launch(int dtype, const void* q, const void* k, const voi
                               float sm_scale, bool causal, hipStream_t stream,
                               const int32_t* cu_seqlens = nullptr, int64_t total = 0);
 
+// dQ per query head (attention_bwd_dq.hip); each row has a single writer.
 void attn_bwd_dq_dma_launch(int dtype, const void* q, const void* k, const void* v,
                             const void* dout, void* dq, const float* lse, const float* delta,
                             int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,

@@ -1,27 +1,23 @@
 // Flash attention recompute backward for head_dim 64/128 (f16/bf16) on CDNA4 MFMA: the
-// dK/dV and dQ passes behind tk_attn_bwd_dkdv / tk_attn_bwd_dq
-// (src/tklab/kernels/flash_attention.py:383-533: P = exp2(S * scale * log2(e) - lse),
-// dS = P (dP - delta), dV = P^T dO, dK = scale dS^T Q, dQ = scale dS K; each output is
-// written by exactly one workgroup, so both passes are deterministic).
+// dK/dV pass behind tk_attn_bwd_dkdv (src/tklab/kernels/flash_attention.py:383-491:
+// P = exp2(S * scale * log2(e) - lse), dS = P (dP - delta), dV = P^T dO, dK = scale dS^T Q;
+// each output is written by exactly one workgroup, so the pass is deterministic). The dQ
+// pass is attention_bwd_dq.hip.
 //
 // dK/dV pass: a workgroup owns 128 keys (4 wave64s x 32, one wave per SIMD) and walks the
 // query blocks of 64. With head_dim 64 the kernel is held to 256 registers (it fits
 // without spills), so two workgroups share a CU and each SIMD has a second wave to cover
 // the first one's LDS and MFMA latencies (+13-16% over one wave per SIMD); head_dim 128
-// needs ~400 registers and ~98 KiB of LDS, one workgroup per CU. K and V fragments stay in registers. Per query block each wave
-// computes S = Q K^T and dP = dO V^T (accumulator lane = one key, so P and dS feed the
-// next MFMAs as B operands straight from registers), then dV^T += dO^T P and
-// dK^T += Q^T dS with dO^T / Q^T read transposed (ds_read_b64_tr_b16) from the same
-// row-major tiles that S and dP read with ds_read_b128.
+// needs ~400 registers and ~98 KiB of LDS, one workgroup per CU. K and V fragments stay in
+// registers. Per query block each wave computes S = Q K^T and dP = dO V^T (accumulator
+// lane = one key, so P and dS feed the next MFMAs as B operands straight from registers),
+// then dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T read transposed
+// (ds_read_b64_tr_b16) from the same row-major tiles that S and dP read with ds_read_b128.
 //
-// dQ pass: a workgroup owns 128 queries (4 waves x 32) and walks the key blocks of 64,
-// like the forward: S^T = K Q^T and dP^T = V dO^T (lane = one query, so lse and delta
-// are one value per lane), dQ^T += K^T dS^T with K^T read transposed.
-//
-// Tiles reach LDS by buffer->LDS DMA into 3-stage rings, two blocks ahead, one barrier
-// per block. Tiles read both ways (Q, dO in the dK/dV pass; K in the dQ pass) store the
-// 16-byte chunk c of row r at slot c ^ dual_swz(r), which keeps both the 16-row
-// ds_read_b128 phases and the 4-row x 64-byte transposed phases on 64 distinct banks.
+// Tiles reach LDS by buffer->LDS DMA into a 3-stage ring, two blocks ahead, one barrier
+// per block. Tiles read both ways (Q, dO) store the 16-byte chunk c of row r at slot
+// c ^ dual_swz(r), which keeps both the 16-row ds_read_b128 phases and the 4-row x
+// 64-byte transposed phases on 64 distinct banks.
 #include "attention.hpp"
 #include "attention_dma.hpp"
 
@@ -181,7 +177,6 @@ __device__ __forceinline__ void dma_stats(__amdgpu_buffer_rsrc_t rs, char* dst, 
 __device__ __forceinline__ int acc_row(int r, int hi) { return ((r >> 2) << 3) + (hi << 2) + (r & 3); }
 
 
-__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 // Row operands of one 32-query sub-block of the dK/dV pass: Q and dO fragments
 // (ds_read_b128, features 16 kk + 8 hi .. +7 of query lane % 32) and the lse / delta of
@@ -481,236 +476,6 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   }
 }
 
-// ---------------------------------------------------------------- dQ
-
-template <typename T, int D, bool CAUSAL>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(1, 1))) void
-attn_bwd_dq_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
-                       const T* __restrict__ V, const T* __restrict__ dO, T* __restrict__ dQ,
-                       const float* __restrict__ lse, const float* __restrict__ delta,
-                       BwdShape s) {
-  using G = BwdGeo<D>;
-  constexpr int BB = G::BB, KS = G::KS, DT = G::DT, RB = G::RB, TILE = G::TILE;
-  constexpr int STB = 2 * TILE;                // stage: K, V
-  constexpr int NDMA = 2 * G::DMA_PER_TILE;
-  __shared__ __attribute__((aligned(1024))) char lds[G::STAGES * STB];
-
-  // Varlen: the heavy-first schedule over every sequence's query blocks (level = query
-  // block), heads interleaved over the XCDs.
-  int b, h, qblk;
-  if (s.cu != nullptr) {
-    h = varlen_head(blockIdx.x, s.heads);
-    VarlenTile vt;
-    if (!varlen_tile(s.cu, s.batch, s.total, s.seq, G::BW, blockIdx.x / s.heads, vt)) return;
-    b = vt.b;
-    qblk = vt.level;
-  } else {
-    int w = blockIdx.x;
-    if (s.tiles % 8 == 0) w = (w % 8) * (s.tiles / 8) + w / 8;
-    const int bh = w / s.blocks_per_head;
-    qblk = CAUSAL ? s.blocks_per_head - 1 - w % s.blocks_per_head : w % s.blocks_per_head;
-    b = bh / s.heads;
-    h = bh % s.heads;
-  }
-  const SeqSpan sp = seq_span<D>(s, b);
-  const int N = sp.n;
-  const int64_t sn = s.st[2], kn = s.kst[2];
-  const int64_t base = b * s.st[0] + h * s.st[1] + int64_t(sp.start) * sn;
-  const int64_t kvbase =
-      b * s.kst[0] + (h / s.group) * s.kst[1] + int64_t(sp.start) * kn;  // KV head h / group
-  const int64_t stat = s.cu != nullptr ? int64_t(h) * s.total + sp.start
-                                       : (int64_t(b) * s.heads + h) * N;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int l32 = lane & 31, hi = lane >> 5;
-  const int q0 = qblk * G::BW;
-  if (q0 >= N) return;  // varlen: past this sequence's end (uniform)
-  const int wq0 = q0 + wave * G::LW;
-  const int query = wq0 + l32;
-
-  // Q and dO fragments of this wave's queries (B operands of S^T and dP^T).
-  i32x4 qf[KS], of[KS];
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) {
-    const int64_t off = base + int64_t(query) * sn + kk * 16 + hi * 8;
-    qf[kk] = query < N ? *reinterpret_cast<const i32x4*>(Q + off) : i32x4{0, 0, 0, 0};
-    of[kk] = query < N ? *reinterpret_cast<const i32x4*>(dO + off) : i32x4{0, 0, 0, 0};
-  }
-  const float lse_q = query < N ? lse[stat + query] : 0.f;
-  const float delta_q = query < N ? delta[stat + query] : 0.f;
-
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(K + kvbase), (short)0, sp.kv_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(V + kvbase), (short)0, sp.kv_bytes, 0x00020000);
-  const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
-  uint32_t k_src[G::DMA_PER_TILE], v_src[G::DMA_PER_TILE];
-#pragma unroll
-  for (int x = 0; x < G::DMA_PER_TILE; ++x) {
-    k_src[x] = tile_src<D, true>(wave, x, lane, kn);
-    v_src[x] = tile_src<D, false>(wave, x, lane, kn);
-  }
-  const uint32_t blk_bytes = uint32_t(BB * kn) * 2u;
-  const int kv_end = CAUSAL ? min(N, q0 + G::BW) : N;
-  const int nblk = (kv_end + BB - 1) / BB;
-
-#define TK_BWD_DQ_DMA(J, ST) \
-  dma_tiles<D>(rk, rv, lds + (ST) * STB, k_src, v_src, min((J), nblk - 1) * blk_bytes, wave);
-
-  f32x16 acc[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
-
-  uint32_t ka[KS], va[KS], ta0[DT], ta8[DT];
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) {
-    ka[kk] = frag_addr<D, true>(lane, kk);
-    va[kk] = frag_addr<D, false>(lane, kk);
-  }
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    ta0[dt] = tr_addr<D>(lane, dt, 0);
-    ta8[dt] = tr_addr<D>(lane, dt, 8);
-  }
-  const float sl2 = s.scale_log2;
-
-  TK_BWD_DQ_DMA(0, 0)
-  TK_BWD_DQ_DMA(1, 1)
-  int stage = 0, fill = 2;
-  const int wave_blocks = CAUSAL ? min(nblk, (wq0 + G::LW - 1) / BB + 1) : nblk;
-  int j = 0;
-  for (; j < wave_blocks; ++j) {
-    wait_vmcnt<NDMA>();
-    barrier_no_fence();
-    TK_BWD_DQ_DMA(j + 2, fill)
-    const int n0 = j * BB;
-    // Lane addresses for this stage; the V tile and the 16-row steps are immediates.
-    const uint32_t kbase = lds_base + stage * STB;
-    uint32_t k_a[KS], v_a[KS], t0[DT], t8[DT];
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      k_a[kk] = kbase + ka[kk];
-      v_a[kk] = kbase + va[kk];
-    }
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      t0[dt] = kbase + ta0[dt];
-      t8[dt] = kbase + ta8[dt];
-    }
-
-    // S^T = K Q^T and dP^T = V dO^T: 2 key tiles of 32.
-    f32x16 sc[2], dp[2];
-    {
-      i32x4 fk[2][KS];
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        fk[0][kk] = read_row<RB>(0, k_a[kk]);
-        fk[1][kk] = read_row<RB>(1, k_a[kk]);
-      }
-      wait_lgkm_n<0>();
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        pin(fk[0][kk]);
-        pin(fk[1][kk]);
-      }
-      const f32x16 z = {};
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        sc[0] = Mma<T>::run(fk[0][kk], qf[kk], kk == 0 ? z : sc[0]);
-        sc[1] = Mma<T>::run(fk[1][kk], qf[kk], kk == 0 ? z : sc[1]);
-      }
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        fk[0][kk] = read_row<RB, TILE>(0, v_a[kk]);
-        fk[1][kk] = read_row<RB, TILE>(1, v_a[kk]);
-      }
-      wait_lgkm_n<0>();
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        pin(fk[0][kk]);
-        pin(fk[1][kk]);
-      }
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        dp[0] = Mma<T>::run(fk[0][kk], of[kk], kk == 0 ? z : dp[0]);
-        dp[1] = Mma<T>::run(fk[1][kk], of[kk], kk == 0 ? z : dp[1]);
-      }
-    }
-
-    // Masked keys (past the sequence end, or after this lane's query) get S^T = -inf;
-    // only ragged and diagonal blocks. Register r of key tile nt holds key
-    // n0 + 32 nt + 8 (r / 4) + 4 hi + r % 4.
-    const bool need_mask = n0 + BB > N || (CAUSAL && n0 + BB - 1 > wq0);
-    if (__builtin_expect(need_mask, 0)) {
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        int lim = N - 1 - (n0 + nt * 32 + 4 * hi);  // last valid offset from the lane's first key
-        if (CAUSAL) lim = min(lim, query - (n0 + nt * 32 + 4 * hi));
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (acc_row(r, 0) > lim) sc[nt][r] = kNegInf;
-      }
-    }
-    // P^T = exp2(S^T c - lse), dS^T = P^T (dP^T - delta).
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[nt][r], sl2, -lse_q));
-        dp[nt][r] = pv * (dp[nt][r] - delta_q);
-      }
-    const i32x4 df[4] = {acc_frag<T>(dp[0], 0), acc_frag<T>(dp[0], 1), acc_frag<T>(dp[1], 0),
-                         acc_frag<T>(dp[1], 1)};
-
-    // dQ^T += K^T dS^T over 4 steps of 16 keys.
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      i32x4 tk[2][DT];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) tk[i][dt] = read_tr_step<RB>(2 * half + i, t0[dt], t8[dt]);
-      wait_lgkm_n<0>();
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) pin(tk[i][dt]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] = Mma<T>::run(tk[i][dt], df[2 * half + i], acc[dt]);
-    }
-    stage = stage + 1 == G::STAGES ? 0 : stage + 1;
-    fill = fill + 1 == G::STAGES ? 0 : fill + 1;
-  }
-  for (; j < nblk; ++j) {
-    wait_vmcnt<NDMA>();
-    barrier_no_fence();
-    TK_BWD_DQ_DMA(j + 2, fill)
-    fill = fill + 1 == G::STAGES ? 0 : fill + 1;
-  }
-#undef TK_BWD_DQ_DMA
-  wait_vmcnt<0>();
-
-  if (query < N) {
-    T* row = dQ + base + int64_t(query) * sn;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int d = dt * 32 + g4 * 8 + hi * 4;
-        uint2 u;
-        u.x = pack2<T>(acc[dt][g4 * 4 + 0] * s.scale, acc[dt][g4 * 4 + 1] * s.scale);
-        u.y = pack2<T>(acc[dt][g4 * 4 + 2] * s.scale, acc[dt][g4 * 4 + 3] * s.scale);
-        *reinterpret_cast<uint2*>(row + d) = u;
-      }
-  }
-}
-
 BwdShape make_shape(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
                     int64_t head_dim, const int64_t* q_strides, const int64_t* kv_strides,
                     float sm_scale, const int32_t* cu_seqlens, int64_t total) {
@@ -784,18 +549,6 @@ void attn_bwd_dkdv_dma_launch(int dtype, const void* q, const void* k, const voi
                                 sm_scale, cu_seqlens, total);
   TK_BWD_LAUNCH(s.kv_tiles, attn_bwd_dkdv_dma_kernel, (const T*)q, (const T*)k, (const T*)v,
                 (const T*)dout, (T*)dk, (T*)dv, lse, delta, s);
-}
-
-void attn_bwd_dq_dma_launch(int dtype, const void* q, const void* k, const void* v,
-                            const void* dout, void* dq, const float* lse, const float* delta,
-                            int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
-                            int64_t head_dim, const int64_t* q_strides,
-                            const int64_t* kv_strides, float sm_scale, bool causal,
-                            hipStream_t stream, const int32_t* cu_seqlens, int64_t total) {
-  const BwdShape s = make_shape(batch, heads, kv_heads, seq, head_dim, q_strides, kv_strides,
-                                sm_scale, cu_seqlens, total);
-  TK_BWD_LAUNCH(s.tiles, attn_bwd_dq_dma_kernel, (const T*)q, (const T*)k, (const T*)v,
-                (const T*)dout, (T*)dq, lse, delta, s);
 }
 
 }  // namespace tk

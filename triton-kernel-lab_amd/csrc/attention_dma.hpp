@@ -126,6 +126,25 @@ __device__ __forceinline__ i32x4 read_v(uint32_t addr) {
   return i32x4{a[0], a[1], b[0], b[1]};
 }
 
+// Transposed fragment of a 32-key step starting at row ROW0 of a row-major [keys][D] tile:
+// rows ROW0 + 4g .. +3 (k-index 0..3 of lane group g = lane / 16) and ROW0 + 16 + 4g .. +3
+// (k-index 4..7), the key order of an operand built from two 16x16 accumulators (key
+// tiles 2s and 2s + 1). The lane supplies the address of row ROW0 + 4g + (lane % 16) / 4,
+// features 4 (lane % 4) .. +3 of its 16-feature tile.
+template <int ROW0, int RB>
+__device__ __forceinline__ i32x4 read_v16(uint32_t addr) {
+  const i32x2 a = lds_read_tr16<ROW0 * RB>(addr);
+  const i32x2 b = lds_read_tr16<(ROW0 + 16) * RB>(addr);
+  return i32x4{a[0], a[1], b[0], b[1]};
+}
+
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// SIMD of the executing wave (HW_ID bits 5:4).
+__device__ __forceinline__ int simd_id() {
+  return __builtin_amdgcn_s_getreg((1 << 11) | (4 << 6) | 4);
+}
+
 // Lane maximum over itself and lane ^ 32 (the swap returns both values, in either order).
 __device__ __forceinline__ float max_with_partner(float x) {
   const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),

@@ -133,22 +133,6 @@ __device__ __forceinline__ void dma_block(__amdgpu_buffer_rsrc_t rk, __amdgpu_bu
   }
 }
 
-// V^T fragment of the 32-key step starting at row ROW0 of a stage's V tile: rows
-// ROW0 + 4g .. +3 (k-index 0..3 of lane group g) and ROW0 + 16 + 4g .. +3 (k-index 4..7),
-// the key order of the P^T fragment built from key tiles 2s and 2s + 1.
-template <int ROW0, int RB>
-__device__ __forceinline__ i32x4 read_v16(uint32_t addr) {
-  const i32x2 a = lds_read_tr16<ROW0 * RB>(addr);
-  const i32x2 b = lds_read_tr16<(ROW0 + 16) * RB>(addr);
-  return i32x4{a[0], a[1], b[0], b[1]};
-}
-
-__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
-
-// The MFMA phase of one wave: O^T += V_{j-1}^T P^T from the previous softmax phase's pf
-// (DO_PV), then S^T(j) = K_j Q^T into st (DO_S). kb / vb: LDS addresses of the K tile of block j
-// and the V tile of block j-1. LDS reads are issued in groups, each awaited just before
-// the MFMAs that use it while the next group is in flight.
 // The MFMA phase as a pipeline of read units of four LDS instructions each: V units
 // (u < NV) hold 32-key step s = u / (FT/2) of feature tiles 2p and 2p+1 (p = u % (FT/2)),
 // K units (u >= NV) k-step kk = u - NV of the four key tiles. Unit u's MFMAs run while
@@ -242,11 +226,6 @@ __device__ __forceinline__ void mfma_phase(uint32_t kb, uint32_t vb, const uint3
     if (u + DEPTH < NU) issue(u + DEPTH);
     sched_fence();
   }
-}
-
-// SIMD of the executing wave (HW_ID bits 5:4).
-__device__ __forceinline__ int simd_id() {
-  return __builtin_amdgcn_s_getreg((1 << 11) | (4 << 6) | 4);
 }
 
 // head_dim 64 uses 64 KiB of LDS per workgroup: held to 128 registers, two workgroups
