@@ -8,7 +8,9 @@
 // barrier waits are covered by the other wave's MFMAs. 16x16x32 rather than 32x32x16:
 // the clock is power-limited under dense MFMA load, and the 16x16 shape sustains more
 // FLOP/s (MFMA-only with random operands 1.90 vs 1.78 PFLOP/s bf16; this GEMM 1.39 vs
-// 1.29 PFLOP/s at 8192^3 with the same tiles and LDS traffic).
+// 1.29 PFLOP/s at 8192^3 with the same tiles and LDS traffic). The MFMAs compute C^T
+// tiles (the B fragment as the first operand), so a lane's four accumulator registers
+// are four consecutive columns of one row and leave as one 8-byte store.
 //
 // Operands reach LDS by buffer->LDS DMA (buffer_load_dwordx4 ... lds): no VGPR staging.
 // LDS is a ring of kStages stages of 32 KiB (A tile then B tile); K tile t+kAhead is
@@ -20,8 +22,11 @@
 //
 // Stage layout (bytes), chosen so every LDS read phase touches 64 distinct banks:
 //   A: 256 rows x 64 B; the 16-byte chunk c (k = 8c .. 8c+7) of row r sits at chunk
-//      c ^ ((r >> 2) & 3). A fragment (16 rows, lane group g taking k = 8g .. 8g+7) is
-//      one ds_read_b128 (16 lanes per phase: 16 rows of one chunk).
+//      c ^ a_swz(r), a_swz(r) = bit 0 of r | bit 2 of r << 1. A fragment (16 rows, lane
+//      group g taking k = 8g .. 8g+7) is one ds_read_b128. Measured on gfx950, an
+//      isolated stream of these reads sustains 256 B/clock/CU with this swizzle and
+//      155 B/clock/CU (four bank-conflict cycles per read) with c ^ ((r >> 2) & 3)
+//      or with none.
 //   B: 32 k-rows x 512 B, row-major in n; the 32-byte granule g (n = 16g .. 16g+15) of
 //      k-row k sits at granule g ^ (2 * (k & 3) + ((k >> 3) & 1)). Fragments are read
 //      with ds_read_b64_tr_b16, which transposes 4 k x 16 n blocks into the MFMA B
@@ -149,6 +154,9 @@ struct Mfma<__bf16> {
   }
 };
 
+// A row swizzle: 16-byte chunk c of row r sits at c ^ a_swz(r).
+__device__ __forceinline__ int a_swz(int r) { return (r & 1) | ((r >> 1) & 2); }
+
 // B k-row swizzle: 32-byte granule g of k-row k sits at g ^ b_swz(k). A 16x16x32 B
 // fragment read phase covers two 16-lane groups reading k-rows 8 apart, so the swizzle
 // carries bit 3 of k besides the (k & 3) term that separates the 4 rows of one read.
@@ -211,7 +219,7 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int r = (wave * 2 + i) * 16 + (lane >> 2);
-    const int c = (lane & 3) ^ ((r >> 2) & 3);
+    const int c = (lane & 3) ^ a_swz(r);
     a_src[i] = (m0 + r < p.m) ? uint32_t((m0 + r) * p.lda + c * 8) * 2u : kOob;
     if constexpr (kSwiGLU) {
       const int L = wave * 2 + i;
@@ -245,10 +253,10 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
           tile * b_tile_bytes, 0, 0);
   };
 
-  // A: row wm + l16 (+16 per row tile), chunk lg swizzled ((row >> 2) & 3 is the same
-  // for every row tile). B: k-rows 8 lg + (l16 >> 2) (+4), columns of N tile j starting
+  // A: row wm + l16 (+16 per row tile), chunk lg swizzled (a_swz reads only the row's
+  // low four bits, the same for every row tile). B: k-rows 8 lg + (l16 >> 2) (+4), columns of N tile j starting
   // at 4 (l16 & 3).
-  const uint32_t a_addr = (wm + l16) * 64 + ((lg ^ ((l16 >> 2) & 3)) * 16);
+  const uint32_t a_addr = (wm + l16) * 64 + ((lg ^ a_swz(l16)) * 16);
   uint32_t b_addr[4];
   {
     const int jj = l16 >> 2, q = l16 & 3;
@@ -300,7 +308,7 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
       const int i = x >> 2, j = x & 3;
-      acc[i][j] = Mfma<T>::run(a_lo[i], Bc[j], acc[i][j]);
+      acc[i][j] = Mfma<T>::run(Bc[j], a_lo[i], acc[i][j]);
       sched_fence();
       if (j == 0) {
         if (i == 0) a_hi[0] = read_a<4>(base + a_addr);
@@ -319,7 +327,7 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
       const int i = x >> 2, j = x & 3;
-      acc[4 + i][j] = Mfma<T>::run(a_hi[i], Bc[j], acc[4 + i][j]);
+      acc[4 + i][j] = Mfma<T>::run(Bc[j], a_hi[i], acc[4 + i][j]);
       sched_fence();
       if (j == 0) {
         if (i == 0) a_lo[0] = read_a<0>(next_base + a_addr);
@@ -348,18 +356,38 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
   wait_vmcnt<0>();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
+  // acc[i][j] holds C^T: register r of lane l is C[m][n] with m = m0 + wm + 16 i + l % 16 and
+  // n = n0 + (N tile j's first column) + 4 (l / 16) + r, so a lane stores 4 consecutive
+  // columns of one row: one 8-byte store when C rows are contiguous and 8-byte aligned.
+  const bool vec = p.scn == 1 && (p.scm & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 7) == 0;
+  auto store4 = [&](int m, int n, const float (&v)[4]) {
+    if (m >= p.m || n >= p.n) return;
+    T* dst = C + m * p.scm + n * p.scn;
+    if (vec) {  // p.n % 8 == 0, so n .. n+3 are in range
+      const uint32_t lo = uint32_t(__builtin_bit_cast(uint16_t, tk::from_f32<T>(v[0]))) |
+                          (uint32_t(__builtin_bit_cast(uint16_t, tk::from_f32<T>(v[1]))) << 16);
+      const uint32_t hi = uint32_t(__builtin_bit_cast(uint16_t, tk::from_f32<T>(v[2]))) |
+                          (uint32_t(__builtin_bit_cast(uint16_t, tk::from_f32<T>(v[3]))) << 16);
+      *reinterpret_cast<uint2*>(dst) = uint2{lo, hi};
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (n + r < p.n) dst[r * p.scn] = tk::from_f32<T>(v[r]);
+    }
+  };
   if constexpr (kSwiGLU) {
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
-      const int n = n0 + (wave & 3) * 32 + jj * 16 + l16;
-      if (n >= p.n) continue;
+      const int n = n0 + (wave & 3) * 32 + jj * 16 + lg * 4;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < 8; ++i) {
+        const int m = m0 + wm + i * 16 + l16;
+        float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = m0 + wm + i * 16 + lg * 4 + r;
-          if (m < p.m) C[m * p.scm + n * p.scn] = swiglu_out<T>(acc[i][jj][r], acc[i][jj + 2][r]);
-        }
+        for (int r = 0; r < 4; ++r)
+          v[r] = static_cast<float>(swiglu_out<T>(acc[i][jj][r], acc[i][jj + 2][r]));
+        store4(m, n, v);
+      }
     }
   } else {
     const float* scales = reinterpret_cast<const float*>(lds);
@@ -370,19 +398,15 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float4 sc = {1.f, 1.f, 1.f, 1.f};
-      if constexpr (kRowScale) sc = *reinterpret_cast<const float4*>(scales + wm + i * 16 + lg * 4);
-      const float scv[4] = {sc.x, sc.y, sc.z, sc.w};
+      const int m = m0 + wm + i * 16 + l16;
+      const float sc = kRowScale ? scales[wm + i * 16 + l16] : 1.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int n = n0 + wn + j * 16 + l16;
-        if (n >= p.n) continue;
+        const int n = n0 + wn + j * 16 + lg * 4;
+        float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = m0 + wm + i * 16 + lg * 4 + r;
-          const float v = kRowScale ? acc[i][j][r] * scv[r] : acc[i][j][r];
-          if (m < p.m) C[m * p.scm + n * p.scn] = tk::from_f32<T>(v);
-        }
+        for (int r = 0; r < 4; ++r) v[r] = kRowScale ? acc[i][j][r] * sc : acc[i][j][r];
+        store4(m, n, v);
       }
     }
   }
