@@ -4,20 +4,33 @@
 // each output is written by exactly one workgroup, so the pass is deterministic). The dQ
 // pass is attention_bwd_dq.hip.
 //
-// dK/dV pass: a workgroup owns 128 keys (4 wave64s x 32, one wave per SIMD) and walks the
-// query blocks of 64. With head_dim 64 the kernel is held to 256 registers (it fits
-// without spills), so two workgroups share a CU and each SIMD has a second wave to cover
-// the first one's LDS and MFMA latencies (+13-16% over one wave per SIMD); head_dim 128
-// needs ~400 registers and ~98 KiB of LDS, one workgroup per CU. K and V fragments stay in
-// registers. Per query block each wave computes S = Q K^T and dP = dO V^T (accumulator
-// lane = one key, so P and dS feed the next MFMAs as B operands straight from registers),
-// then dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T read transposed
-// (ds_read_b64_tr_b16) from the same row-major tiles that S and dP read with ds_read_b128.
+// head_dim 128, attn_bwd_dkdv_pp_kernel. Workgroup: 128 keys, 8 wave64s in 4
+// producer/consumer pairs of 32 keys (waves w and w + 4, which share a SIMD), streaming the
+// query blocks of 64; all products are v_mfma_f32_16x16x32. Per pair and query block:
+//   producer  S = Q K^T, dP = dO V^T (Q / dO rows as A operands, ds_read_b128; K and V
+//             fragments in registers), then P = exp2(S c - lse), dS = P (dP - delta),
+//             written to LDS as the consumer's B-operand fragments (lane = key);
+//   consumer  dV^T += dO^T P, dK^T += Q^T dS with dO^T / Q^T read transposed
+//             (ds_read_b64_tr_b16) from the same tiles, accumulators in registers.
+// Barrier-separated phases: producer MFMA (block v) | producer elementwise (v) with the
+// consumer's MFMAs (v - 1) | ..., so the exponentials of one wave run beside the other
+// wave's MFMAs, and each wave holds only half of the state (K/V and S/dP, or the dK/dV
+// accumulators). The consumer reads the exchange fragments in the producer's MFMA phase,
+// so one 8 KiB buffer per pair suffices. Q/dO tiles reach LDS by buffer->LDS DMA into a
+// ring (block v is read in phases 2v - 1 .. 2v+3); tiles read both ways store the 16-byte
+// chunk c of row r at slot c ^ swz(r), which keeps the 16-row ds_read_b128 phases and the
+// transposed phases on distinct banks.
 //
-// Tiles reach LDS by buffer->LDS DMA into a 3-stage ring, two blocks ahead, one barrier
-// per block. Tiles read both ways (Q, dO) store the 16-byte chunk c of row r at slot
-// c ^ dual_swz(r), which keeps both the 16-row ds_read_b128 phases and the 4-row x
-// 64-byte transposed phases on 64 distinct banks.
+// head_dim 64, attn_bwd_dkdv_dma_kernel: a workgroup owns 128 keys (4 wave64s x 32, one
+// wave per SIMD) and walks the query blocks of 64. It is held to 256 registers, so two
+// workgroups share a CU and each SIMD has a second wave to cover the first one's LDS and
+// MFMA latencies (at head_dim 64 the pair kernel's elementwise phase, the same work as at
+// 128, outlasts the consumer's halved MFMA phase). K and V fragments stay in registers.
+// Per query block each wave computes S = Q K^T and dP = dO V^T (32x32x16 MFMAs,
+// accumulator lane = one key, so P and dS feed the next MFMAs as B operands straight from
+// registers), then dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T read transposed from
+// the same row-major tiles that S and dP read with ds_read_b128. Tiles reach LDS by
+// buffer->LDS DMA into a 3-stage ring, two blocks ahead, one barrier per block.
 #include "attention.hpp"
 #include "attention_dma.hpp"
 
@@ -25,12 +38,8 @@ namespace {
 
 using namespace tk_attn;
 
-constexpr int kThreads = 256;  // 4 waves, one per SIMD of the CU
-
-template <int N>
-__device__ __forceinline__ void wait_lgkm_n() {
-  asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
-}
+constexpr int kThreads = 512;   // producer/consumer kernel (head_dim 128)
+constexpr int kThreads1 = 256;  // one-wave-per-SIMD kernel (head_dim 64)
 
 struct BwdShape {
   int heads, seq;       // query heads
@@ -227,7 +236,7 @@ __device__ __forceinline__ void pin_sub_rows(SubRows& r) {
 // ---------------------------------------------------------------- dK / dV
 
 template <typename T, int D, bool CAUSAL>
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads1, kThreads1),
                           amdgpu_waves_per_eu(D == 64 ? 2 : 1, D == 64 ? 2 : 1))) void
 attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
                          const T* __restrict__ V, const T* __restrict__ dO, T* __restrict__ dK,
@@ -392,7 +401,7 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
     for (int mt = 0; mt < 2; ++mt) {
       SubRows rows;
       read_sub_rows<D>(rows, mt, qs_a, st_a);
-      wait_lgkm_n<0>();
+      wait_lgkm<0>();
       pin_sub_rows<D>(rows);
       // S = Q K^T and dP = dO V^T for 32 queries x this wave's 32 keys.
       f32x16 sc, dp;
@@ -431,7 +440,7 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
       }
       const i32x4 pf[2] = {acc_frag<T>(sc, 0), acc_frag<T>(sc, 1)};
       const i32x4 df[2] = {acc_frag<T>(dp, 0), acc_frag<T>(dp, 1)};
-      wait_lgkm_n<0>();
+      wait_lgkm<0>();
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -476,6 +485,541 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   }
 }
 
+template <int D>
+struct KvGeo {
+  static constexpr int PAIRS = 4, LK = 32;       // wave pairs, keys per pair
+  static constexpr int BW = PAIRS * LK;          // keys per workgroup: 128
+  static constexpr int BB = 64;                  // queries per streamed block
+  static constexpr int KS = D / 32;              // k-steps of S and dP
+  static constexpr int FT = D / 16;              // 16-feature tiles of dK^T / dV^T
+  static constexpr int FP = FT / 2;
+  static constexpr int RB = D * 2;               // bytes per row
+  static constexpr int OPB = BB * RB;            // bytes per operand tile
+  static constexpr int STAT = 2 * BB * 4;        // lse[64] then delta[64]
+  static constexpr int STB = 2 * OPB + STAT;     // stage: Q, dO, statistics
+  static constexpr int STAGES = D == 128 ? 3 : 4;
+  static constexpr int XB = 8 * 1024;            // exchange bytes per pair: 8 fragments
+  static constexpr int LDS = STAGES * STB + PAIRS * XB;
+  static constexpr int ROWS_PER_DMA = 1024 / RB;
+  static constexpr int DMA_PER_OP = OPB / 1024 / 8;
+  static constexpr int DMA_PER_BLOCK = 2 * DMA_PER_OP + 1;  // Q, dO, statistics
+  static constexpr int SLOTS = RB / 16;
+  // Read units (four LDS instructions each). Producer: KS Q-row units then KS dO-row
+  // units (query tiles 0..3 of one k-step). Consumer: 2 FP transposed-dO units (32-query
+  // step s = v / FP, feature tiles 2p, 2p + 1), then 2 FP transposed-Q units. DEPTH units
+  // are in flight; the first PREFETCH units of an MFMA phase are issued at the end of the
+  // wave's preceding phase.
+  static constexpr int NA = 2 * KS, NB = 4 * FP;
+  static constexpr int DEPTH_A = 3, PREFETCH_A = 2, DEPTH_B = 3, PREFETCH_B = 3;
+  // Tiles read both as rows (ds_read_b128: 16 rows of one chunk) and transposed
+  // (ds_read_b64_tr_b16: 8 rows x 32 bytes per 32-lane phase). The transposed phases need
+  // bits 1..3 of the swizzle distinct over rows 0..7 and over rows 8..15; for the row reads
+  // gfx950's bank mapping was measured rather than derived: with these swizzles a stream of
+  // either read sustains 236-256 B/clock/CU, while the swizzle ((r & 7) << 1) | r3 (a
+  // bijection on 16 rows) held the row reads to 155 B/clock/CU.
+  static __device__ __forceinline__ int swz(int r) {
+    return D == 128 ? (((r >> 3) & 1) | ((r & 3) << 1) | ((((r >> 2) ^ (r >> 3)) & 1) << 3))
+                    : (r & 7);
+  }
+};
+
+// Two transposed reads of 16 rows each, OFF and OFF + 16 rows past the lane address: a
+// 32-query A operand in the query order of an operand built from two 16x16 accumulators.
+template <int OFF, int RB>
+__device__ __forceinline__ i32x4 read_t16(uint32_t addr) {
+  const i32x2 a = lds_read_tr16<OFF>(addr);
+  const i32x2 b = lds_read_tr16<OFF + 16 * RB>(addr);
+  return i32x4{a[0], a[1], b[0], b[1]};
+}
+
+__device__ __forceinline__ void lds_write_b128(uint32_t addr, i32x4 v) {
+  asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+
+// Stream of query blocks, in order: the KV head's `group` query heads one after another,
+// blocks first .. first + nblk - 1 of each; past the end the last block is reloaded.
+// Blocks are fetched strictly in order, so a cursor replaces a division, and the head's
+// buffer resources are rebuilt only when the cursor moves to the next head.
+template <typename T>
+struct QStream {
+  const T* q0;
+  const T* o0;
+  const float* st0;     // lse (waves 0-3) or delta (waves 4-7) of the group's first head
+  int64_t head, st_head;  // element strides between the group's heads
+  uint32_t q_bytes, st_bytes, blk_bytes;
+  int group, nblk, first;
+  int dg, dj, fill;  // cursor
+};
+
+// Buffer resources of the cursor's head (Q, dO, statistics).
+template <typename T>
+__device__ __forceinline__ void qstream_open(const QStream<T>& c, __amdgpu_buffer_rsrc_t& rq,
+                                             __amdgpu_buffer_rsrc_t& rdo,
+                                             __amdgpu_buffer_rsrc_t& rst) {
+  rq = __builtin_amdgcn_make_buffer_rsrc((void*)(c.q0 + c.dg * c.head), (short)0, c.q_bytes,
+                                         0x00020000);
+  rdo = __builtin_amdgcn_make_buffer_rsrc((void*)(c.o0 + c.dg * c.head), (short)0, c.q_bytes,
+                                          0x00020000);
+  rst = __builtin_amdgcn_make_buffer_rsrc((void*)(c.st0 + c.dg * c.st_head), (short)0,
+                                          c.st_bytes, 0x00020000);
+}
+
+// DMA of the next block of the stream into its stage: this wave's DMA_PER_OP loads of the
+// Q and dO tiles and 16 statistics floats (wave w: lse rows 16 w .. (waves 0-3), delta
+// rows 16 (w - 4) .. (waves 4-7)).
+template <typename T, int D>
+__device__ __forceinline__ void qstream_dma(QStream<T>& c, __amdgpu_buffer_rsrc_t& rq,
+                                            __amdgpu_buffer_rsrc_t& rdo,
+                                            __amdgpu_buffer_rsrc_t& rst, char* lds,
+                                            const uint32_t* src, uint32_t st_src, int wave,
+                                            int lane) {
+  using G = KvGeo<D>;
+  char* stage = lds + c.fill * G::STB;
+  const uint32_t off = uint32_t(c.first + (c.dg >= c.group ? c.nblk - 1 : c.dj)) * c.blk_bytes;
+#pragma unroll
+  for (int x = 0; x < G::DMA_PER_OP; ++x) {
+    const int id = wave * G::DMA_PER_OP + x;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(stage + id * 1024), 16, src[x], off,
+                                             0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rdo, (lds_void*)(stage + G::OPB + id * 1024), 16,
+                                             src[x], off, 0, 0);
+  }
+  const uint32_t st_off =
+      uint32_t(c.first + (c.dg >= c.group ? c.nblk - 1 : c.dj)) * uint32_t(G::BB * 4);
+  if (lane < 16)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rst, (lds_void*)(stage + 2 * G::OPB + wave * 64), 4,
+                                             st_src, st_off, 0, 0);
+  c.fill = c.fill + 1 == G::STAGES ? 0 : c.fill + 1;
+  if (c.dg < c.group && ++c.dj == c.nblk) {
+    c.dj = 0;
+    if (++c.dg < c.group) qstream_open(c, rq, rdo, rst);
+  }
+}
+
+// Producer read unit u (Q rows for u < KS, else dO rows; k-step u % KS, query tiles
+// 0..3 at +16 rows each) of the stage at sb.
+template <int D>
+__device__ __forceinline__ void producer_unit(i32x4 (&rf)[KvGeo<D>::NA][4], uint32_t sb,
+                                              const uint32_t (&qa)[KvGeo<D>::KS], int u) {
+  constexpr int KS = KvGeo<D>::KS, RB = KvGeo<D>::RB, OPB = KvGeo<D>::OPB;
+  const uint32_t a = sb + qa[u % KS];
+  if (u < KS) {
+    rf[u][0] = lds_read_b128<0>(a);
+    rf[u][1] = lds_read_b128<16 * RB>(a);
+    rf[u][2] = lds_read_b128<32 * RB>(a);
+    rf[u][3] = lds_read_b128<48 * RB>(a);
+  } else {
+    rf[u][0] = lds_read_b128<OPB>(a);
+    rf[u][1] = lds_read_b128<OPB + 16 * RB>(a);
+    rf[u][2] = lds_read_b128<OPB + 32 * RB>(a);
+    rf[u][3] = lds_read_b128<OPB + 48 * RB>(a);
+  }
+}
+
+// Producer MFMA phase: S = Q K^T and dP = dO V^T for the block's 64 queries and the pair's
+// 32 keys (st / dp [qt][kt] register r: query 16 qt + 4 g + r, key 16 kt + c). Its first
+// PREFETCH_A units were issued by the preceding phase.
+template <typename T, int D>
+__device__ __forceinline__ void producer_mfma(uint32_t sb, const uint32_t (&qa)[KvGeo<D>::KS],
+                                              const i32x4 (&kf)[2][KvGeo<D>::KS],
+                                              const i32x4 (&vf)[2][KvGeo<D>::KS],
+                                              f32x4 (&st)[4][2], f32x4 (&dp)[4][2],
+                                              i32x4 (&rf)[KvGeo<D>::NA][4]) {
+  using G = KvGeo<D>;
+  constexpr int KS = G::KS, NU = G::NA, DEPTH = G::DEPTH_A, PRE = G::PREFETCH_A;
+#pragma unroll
+  for (int u = PRE; u < DEPTH && u < NU; ++u) producer_unit<D>(rf, sb, qa, u);
+  sched_fence();
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int after = (u + DEPTH < NU ? u + DEPTH : NU) - (u + 1);
+    if (after >= 2)
+      wait_lgkm<8>();
+    else if (after == 1)
+      wait_lgkm<4>();
+    else
+      wait_lgkm<0>();
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) pin(rf[u][qt]);
+    const int kk = u % KS;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        if (u < KS)
+          st[qt][kt] = Mma16<T>::run(rf[u][qt], kf[kt][kk], kk == 0 ? z : st[qt][kt]);
+        else
+          dp[qt][kt] = Mma16<T>::run(rf[u][qt], vf[kt][kk], kk == 0 ? z : dp[qt][kt]);
+      }
+    if (u + DEPTH < NU) producer_unit<D>(rf, sb, qa, u + DEPTH);
+    sched_fence();
+  }
+}
+
+// Consumer read unit u (transposed dO for u < 2 FP, else transposed Q) of the stage at sb.
+template <int D>
+__device__ __forceinline__ void consumer_unit(i32x4 (&tu)[KvGeo<D>::NB][2], uint32_t sb,
+                                              const uint32_t (&ta)[KvGeo<D>::FT], int u) {
+  using G = KvGeo<D>;
+  constexpr int FP = G::FP, RB = G::RB, OPB = G::OPB;
+  const int v = u < 2 * FP ? u : u - 2 * FP;
+  const int s = v / FP, p = v % FP;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t a = sb + ta[2 * p + i];
+    if (u < 2 * FP)
+      tu[u][i] = s == 0 ? read_t16<OPB, RB>(a) : read_t16<OPB + 32 * RB, RB>(a);
+    else
+      tu[u][i] = s == 0 ? read_t16<0, RB>(a) : read_t16<32 * RB, RB>(a);
+  }
+}
+
+// Consumer MFMA phase: dV^T += dO^T P and dK^T += Q^T dS over the block's 64 queries
+// (adv / adk [ft][kt] register r: feature 16 ft + 4 g + r, key 16 kt + c). Its first
+// PREFETCH_B units were issued by the preceding phase.
+template <typename T, int D>
+__device__ __forceinline__ void consumer_mfma(uint32_t sb, const uint32_t (&ta)[KvGeo<D>::FT],
+                                              const i32x4 (&pf)[2][2], const i32x4 (&df)[2][2],
+                                              f32x4 (&adv)[KvGeo<D>::FT][2],
+                                              f32x4 (&adk)[KvGeo<D>::FT][2],
+                                              i32x4 (&tu)[KvGeo<D>::NB][2]) {
+  using G = KvGeo<D>;
+  constexpr int FP = G::FP, NU = G::NB, DEPTH = G::DEPTH_B, PRE = G::PREFETCH_B;
+#pragma unroll
+  for (int u = PRE; u < DEPTH && u < NU; ++u) consumer_unit<D>(tu, sb, ta, u);
+  sched_fence();
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int after = (u + DEPTH < NU ? u + DEPTH : NU) - (u + 1);
+    if (after >= 3)
+      wait_lgkm<12>();
+    else if (after == 2)
+      wait_lgkm<8>();
+    else if (after == 1)
+      wait_lgkm<4>();
+    else
+      wait_lgkm<0>();
+    pin(tu[u][0]);
+    pin(tu[u][1]);
+    const int v = u < 2 * FP ? u : u - 2 * FP;
+    const int s = v / FP, p = v % FP;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        if (u < 2 * FP)
+          adv[2 * p + i][kt] = Mma16<T>::run(tu[u][i], pf[s][kt], adv[2 * p + i][kt]);
+        else
+          adk[2 * p + i][kt] = Mma16<T>::run(tu[u][i], df[s][kt], adk[2 * p + i][kt]);
+      }
+    if (u + DEPTH < NU) consumer_unit<D>(tu, sb, ta, u + DEPTH);
+    sched_fence();
+  }
+}
+
+// ---------------------------------------------------------------- dK / dV
+
+template <typename T, int D, bool CAUSAL>
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(2))) void
+attn_bwd_dkdv_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K,
+                        const T* __restrict__ V, const T* __restrict__ dO, T* __restrict__ dK,
+                        T* __restrict__ dV, const float* __restrict__ lse,
+                        const float* __restrict__ delta, BwdShape s) {
+  using G = KvGeo<D>;
+  constexpr int BB = G::BB, KS = G::KS, FT = G::FT, RB = G::RB, STB = G::STB;
+  constexpr int STAGES = G::STAGES, DPB = G::DMA_PER_BLOCK;
+  __shared__ __attribute__((aligned(1024))) char lds[G::LDS];
+
+  // Workgroup -> (batch, KV head, key block). The KV head's `group` query heads are
+  // streamed one after another as one sequence of query blocks, so dK and dV sum over
+  // the group in a fixed order with a single writer. Key block 0 (the most causal work)
+  // comes first. Varlen: the heavy-first schedule over every sequence's key blocks
+  // (level = blocks after this one), KV heads interleaved over the XCDs.
+  const int kv_heads = s.heads / s.group;
+  int b, kvh, kblk;
+  if (s.cu != nullptr) {
+    kvh = varlen_head(blockIdx.x, kv_heads);
+    VarlenTile vt;
+    if (!varlen_tile(s.cu, s.batch, s.total, s.seq, G::BW, blockIdx.x / kv_heads, vt)) return;
+    b = vt.b;
+    const int nb = (varlen_rows(s.cu, b, s.total, s.seq).n + G::BW - 1) / G::BW;
+    kblk = nb - 1 - vt.level;
+  } else {
+    int w = blockIdx.x;
+    if (s.kv_tiles % 8 == 0) w = (w % 8) * (s.kv_tiles / 8) + w / 8;
+    const int bkv = w / s.blocks_per_head;
+    kblk = w % s.blocks_per_head;
+    b = bkv / kv_heads;
+    kvh = bkv % kv_heads;
+  }
+  const SeqSpan sp = seq_span<D>(s, b);
+  const int N = sp.n;
+  const int64_t sn = s.st[2], kn = s.kst[2];
+  const int64_t kvbase = b * s.kst[0] + kvh * s.kst[1] + int64_t(sp.start) * kn;
+  const int64_t qbase = b * s.st[0] + int64_t(kvh) * s.group * s.st[1] + int64_t(sp.start) * sn;
+  // Statistics of the group's first query head; head g of the group is g heads later.
+  const int64_t stat_head = s.cu != nullptr ? s.total : N;
+  const int64_t stat0 = s.cu != nullptr
+                            ? int64_t(kvh) * s.group * s.total + sp.start
+                            : (int64_t(b) * s.heads + int64_t(kvh) * s.group) * N;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int kb0 = kblk * G::BW;
+  if (kb0 >= N) return;  // varlen: past this sequence's end (uniform)
+  // Wave w < 4 produces P and dS for keys pk0 .. pk0 + 31; wave w + 4 consumes them.
+  const bool producer = wave < G::PAIRS;
+  const int pair = producer ? wave : wave - G::PAIRS;
+  const int pk0 = kb0 + pair * G::LK;
+
+  const int first = CAUSAL ? kb0 / BB : 0;  // first query block with a query >= kb0
+  const int nblk = (N + BB - 1) / BB - first;
+  const int nv = s.group * nblk;            // blocks in the stream
+
+  QStream<T> qs;
+  qs.q0 = Q + qbase;
+  qs.o0 = dO + qbase;
+  qs.st0 = (wave < 4 ? lse : delta) + stat0;
+  qs.head = s.st[1];
+  qs.st_head = stat_head;
+  qs.q_bytes = sp.q_bytes;
+  qs.st_bytes = uint32_t(N) * 4u;
+  qs.blk_bytes = uint32_t(BB * sn) * 2u;
+  qs.group = s.group;
+  qs.nblk = nblk;
+  qs.first = first;
+  qs.dg = qs.dj = qs.fill = 0;
+  __amdgpu_buffer_rsrc_t rq, rdo, rst;
+  qstream_open(qs, rq, rdo, rst);
+  uint32_t src[G::DMA_PER_OP];
+#pragma unroll
+  for (int x = 0; x < G::DMA_PER_OP; ++x) {
+    const int id = wave * G::DMA_PER_OP + x;
+    const int row = id * G::ROWS_PER_DMA + lane / G::SLOTS;
+    const int slot = lane % G::SLOTS;
+    src[x] = uint32_t(row * sn + (slot ^ G::swz(row)) * 8) * 2u;
+  }
+  const uint32_t st_src = uint32_t((wave & 3) * 16 + lane) * 4u;
+#pragma unroll
+  for (int i = 0; i < STAGES - 1; ++i)
+    qstream_dma<T, D>(qs, rq, rdo, rst, lds, src, st_src, wave, lane);
+
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
+  const uint32_t xb = lds_base + STAGES * STB + pair * G::XB + lane * 16;
+  const float sl2 = s.scale_log2;
+  int t = 0;
+  // Block v is DMA'd at the start of phase 2v - 2 (STAGES - 2) blocks ahead and waited
+  // for at the end of phase 2v - 2, so the producer can prefetch its first units at the
+  // end of phase 2v - 1.
+  auto end_phase = [&]() {
+    if (!(t & 1)) wait_vmcnt<(STAGES - 3) * DPB>();
+    barrier_no_fence();
+    ++t;
+    if (!(t & 1)) qstream_dma<T, D>(qs, rq, rdo, rst, lds, src, st_src, wave, lane);
+  };
+  // Causal: a block whose last query precedes the pair's first key contributes nothing.
+  auto active = [&](int j) { return !CAUSAL || (first + j) * BB + BB - 1 >= pk0; };
+
+  wait_vmcnt<(STAGES - 2) * DPB>();
+  barrier_no_fence();
+
+  if (producer) {
+    // K and V fragments (B operands): key tile kt holds key pk0 + 16 kt + c, k-step kk
+    // features 32 kk + 8 g .. +7.
+    i32x4 kf[2][KS], vf[2][KS];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int key = pk0 + 16 * kt + c;
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        const int64_t off = kvbase + int64_t(key) * kn + kk * 32 + g * 8;
+        kf[kt][kk] = key < N ? *reinterpret_cast<const i32x4*>(K + off) : i32x4{0, 0, 0, 0};
+        vf[kt][kk] = key < N ? *reinterpret_cast<const i32x4*>(V + off) : i32x4{0, 0, 0, 0};
+      }
+    }
+    // Row reads: row c of query tile qt (+16 qt rows, an immediate), chunk 4 kk + g.
+    uint32_t qa[KS];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) qa[kk] = c * RB + (((4 * kk + g) ^ G::swz(c)) * 16);
+    const uint32_t sa = 2 * G::OPB + 16 * g;  // statistics of queries 16 qt + 4 g .. +3
+    i32x4 rf[G::NA][4];
+    if (active(0)) {
+#pragma unroll
+      for (int u = 0; u < G::PREFETCH_A; ++u) producer_unit<D>(rf, lds_base, qa, u);
+    }
+    int stage = 0, j = 0;
+    for (int v = 0; v < nv; ++v) {
+      const bool act = active(j);
+      const int jn = j + 1 == nblk ? 0 : j + 1;
+      const int sn = stage + 1 == STAGES ? 0 : stage + 1;
+      const uint32_t sb = lds_base + stage * STB;
+      f32x4 st[4][2], dp[4][2];
+      i32x4 lq[4], dq[4];
+      if (act) {
+        producer_mfma<T, D>(sb, qa, kf, vf, st, dp, rf);
+        // lse / delta of the lane's 16 queries, waited for in the next phase.
+        lq[0] = lds_read_b128<0>(sb + sa);
+        lq[1] = lds_read_b128<64>(sb + sa);
+        lq[2] = lds_read_b128<128>(sb + sa);
+        lq[3] = lds_read_b128<192>(sb + sa);
+        dq[0] = lds_read_b128<256>(sb + sa);
+        dq[1] = lds_read_b128<320>(sb + sa);
+        dq[2] = lds_read_b128<384>(sb + sa);
+        dq[3] = lds_read_b128<448>(sb + sa);
+        // Results pinned before the barrier (it orders memory only; the compiler would
+        // sink register work into the next phase).
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) {
+            pin(st[qt][kt]);
+            pin(dp[qt][kt]);
+          }
+      }
+      end_phase();
+      if (act) {
+        wait_lgkm<0>();
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) {
+          pin(lq[qt]);
+          pin(dq[qt]);
+        }
+        // P = exp2(S c - lse), dS = P (dP - delta); keys after the query are masked
+        // (causal diagonal blocks only).
+        const int q0 = (first + j) * BB;
+        if (CAUSAL && q0 < pk0 + G::LK - 1) {
+#pragma unroll
+          for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+              const int lim = q0 + 16 * qt + 4 * g - (pk0 + 16 * kt + c);
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (r + lim < 0) st[qt][kt][r] = kNegInf;
+            }
+        }
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float l = __int_as_float(lq[qt][r]), dl = __int_as_float(dq[qt][r]);
+              const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qt][kt][r], sl2, -l));
+              st[qt][kt][r] = p;
+              dp[qt][kt][r] = p * (dp[qt][kt][r] - dl);
+            }
+        // Fragments of the consumer's B operands: 32-query step s (query tiles 2s, 2s + 1),
+        // key tile kt; P at 1 KiB * (2 s + kt), dS 4 KiB further.
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) {
+            lds_write_b128(xb + (2 * s2 + kt) * 1024,
+                           acc_frag2<T>(st[2 * s2][kt], st[2 * s2 + 1][kt]));
+            lds_write_b128(xb + 4096 + (2 * s2 + kt) * 1024,
+                           acc_frag2<T>(dp[2 * s2][kt], dp[2 * s2 + 1][kt]));
+          }
+        wait_lgkm<0>();
+      }
+      // First units of the next block's MFMA phase (its tile landed by the end of the
+      // previous phase).
+      if (v + 1 < nv && active(jn)) {
+#pragma unroll
+        for (int u = 0; u < G::PREFETCH_A; ++u)
+          producer_unit<D>(rf, lds_base + sn * STB, qa, u);
+      }
+      end_phase();
+      stage = sn;
+      j = jn;
+    }
+    end_phase();
+  } else {
+    // Transposed reads: row 4 g + c / 4 (+16 for k-index 4..7, +32 per 32-query step),
+    // features 16 ft + 4 (c % 4) .. +3: chunk 2 ft + (c % 4) / 2, half (c % 4) % 2.
+    uint32_t ta[FT];
+    {
+      const int row = 4 * g + (c >> 2), q = c & 3;
+#pragma unroll
+      for (int ft = 0; ft < FT; ++ft)
+        ta[ft] = row * RB + (((2 * ft + (q >> 1)) ^ G::swz(row)) * 16) + (q & 1) * 8;
+    }
+    f32x4 adv[FT][2], adk[FT][2];
+#pragma unroll
+    for (int ft = 0; ft < FT; ++ft)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) adv[ft][kt] = adk[ft][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    i32x4 tu[G::NB][2];
+    end_phase();
+    end_phase();
+    int stage = 0, j = 0;
+    for (int v = 0; v < nv; ++v, j = j + 1 == nblk ? 0 : j + 1) {
+      const bool act = active(j);
+      const uint32_t sb = lds_base + stage * STB;
+      i32x4 pf[2][2], df[2][2];
+      if (act) {
+        // The producer's fragments of block v, then the first transposed units; the
+        // exchange reads have completed once only the prefetched units are outstanding.
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) {
+            pf[s2][kt] = lds_read_b128<0>(xb + (2 * s2 + kt) * 1024);
+            df[s2][kt] = lds_read_b128<4096>(xb + (2 * s2 + kt) * 1024);
+          }
+#pragma unroll
+        for (int u = 0; u < G::PREFETCH_B; ++u) consumer_unit<D>(tu, sb, ta, u);
+        wait_lgkm<4 * G::PREFETCH_B>();
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) {
+            pin(pf[s2][kt]);
+            pin(df[s2][kt]);
+          }
+      }
+      end_phase();
+      if (act) consumer_mfma<T, D>(sb, ta, pf, df, adv, adk, tu);
+#pragma unroll
+      for (int ft = 0; ft < FT; ++ft)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          pin(adv[ft][kt]);
+          pin(adk[ft][kt]);
+        }
+      if (v + 1 < nv) end_phase();
+      stage = stage + 1 == STAGES ? 0 : stage + 1;
+    }
+    wait_vmcnt<0>();
+    // dK = scale (dK^T)^T, dV = (dV^T)^T: register r of adk / adv [ft][kt] is feature
+    // 16 ft + 4 g + r of key pk0 + 16 kt + c.
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int key = pk0 + 16 * kt + c;
+      if (key < N) {
+        T* dkr = dK + kvbase + int64_t(key) * kn;
+        T* dvr = dV + kvbase + int64_t(key) * kn;
+#pragma unroll
+        for (int ft = 0; ft < FT; ++ft) {
+          const int d = 16 * ft + 4 * g;
+          uint2 u;
+          u.x = pack2<T>(adk[ft][kt][0] * s.scale, adk[ft][kt][1] * s.scale);
+          u.y = pack2<T>(adk[ft][kt][2] * s.scale, adk[ft][kt][3] * s.scale);
+          *reinterpret_cast<uint2*>(dkr + d) = u;
+          u.x = pack2<T>(adv[ft][kt][0], adv[ft][kt][1]);
+          u.y = pack2<T>(adv[ft][kt][2], adv[ft][kt][3]);
+          *reinterpret_cast<uint2*>(dvr + d) = u;
+        }
+      }
+    }
+    return;
+  }
+  wait_vmcnt<0>();
+}
+
 BwdShape make_shape(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
                     int64_t head_dim, const int64_t* q_strides, const int64_t* kv_strides,
                     float sm_scale, const int32_t* cu_seqlens, int64_t total) {
@@ -502,29 +1046,35 @@ BwdShape make_shape(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
   return s;
 }
 
-#define TK_BWD_LAUNCH(TILES, KERNEL, ...)                                                   \
-  do {                                                                                      \
-    const dim3 grid(static_cast<unsigned>(TILES));                                         \
-    if (dtype == TK_DTYPE_F16) {                                                            \
-      using T = _Float16;                                                                   \
-      if (head_dim == 64) {                                                                 \
-        if (causal) hipLaunchKernelGGL((KERNEL<T, 64, true>), grid, dim3(kThreads), 0, stream, __VA_ARGS__); \
-        else hipLaunchKernelGGL((KERNEL<T, 64, false>), grid, dim3(kThreads), 0, stream, __VA_ARGS__);      \
-      } else {                                                                              \
-        if (causal) hipLaunchKernelGGL((KERNEL<T, 128, true>), grid, dim3(kThreads), 0, stream, __VA_ARGS__); \
-        else hipLaunchKernelGGL((KERNEL<T, 128, false>), grid, dim3(kThreads), 0, stream, __VA_ARGS__);      \
-      }                                                                                     \
-    } else {                                                                                \
-      using T = __bf16;                                                                     \
-      if (head_dim == 64) {                                                                 \
-        if (causal) hipLaunchKernelGGL((KERNEL<T, 64, true>), grid, dim3(kThreads), 0, stream, __VA_ARGS__); \
-        else hipLaunchKernelGGL((KERNEL<T, 64, false>), grid, dim3(kThreads), 0, stream, __VA_ARGS__);      \
-      } else {                                                                              \
-        if (causal) hipLaunchKernelGGL((KERNEL<T, 128, true>), grid, dim3(kThreads), 0, stream, __VA_ARGS__); \
-        else hipLaunchKernelGGL((KERNEL<T, 128, false>), grid, dim3(kThreads), 0, stream, __VA_ARGS__);      \
-      }                                                                                     \
-    }                                                                                       \
-  } while (0)
+// head_dim 128: the producer/consumer kernel; head_dim 64: the one-wave-per-SIMD kernel,
+// whose two workgroups per CU overlap one workgroup's exponentials with the other's
+// MFMAs (at head_dim 64 a producer's elementwise phase, the same work as at 128, outlasts
+// the consumer's halved MFMA phase).
+template <typename T>
+void launch_dkdv(int64_t head_dim, bool causal, unsigned tiles, hipStream_t stream,
+                 const void* q, const void* k, const void* v, const void* dout, void* dk,
+                 void* dv, const float* lse, const float* delta, const BwdShape& s) {
+  const dim3 grid(tiles);
+  if (head_dim == 64) {
+    if (causal)
+      hipLaunchKernelGGL((attn_bwd_dkdv_dma_kernel<T, 64, true>), grid, dim3(kThreads1), 0,
+                         stream, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, (T*)dk,
+                         (T*)dv, lse, delta, s);
+    else
+      hipLaunchKernelGGL((attn_bwd_dkdv_dma_kernel<T, 64, false>), grid, dim3(kThreads1), 0,
+                         stream, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, (T*)dk,
+                         (T*)dv, lse, delta, s);
+  } else {
+    if (causal)
+      hipLaunchKernelGGL((attn_bwd_dkdv_pp_kernel<T, 128, true>), grid, dim3(kThreads), 0,
+                         stream, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, (T*)dk,
+                         (T*)dv, lse, delta, s);
+    else
+      hipLaunchKernelGGL((attn_bwd_dkdv_pp_kernel<T, 128, false>), grid, dim3(kThreads), 0,
+                         stream, (const T*)q, (const T*)k, (const T*)v, (const T*)dout, (T*)dk,
+                         (T*)dv, lse, delta, s);
+  }
+}
 
 }  // namespace
 
@@ -547,8 +1097,11 @@ void attn_bwd_dkdv_dma_launch(int dtype, const void* q, const void* k, const voi
                               const int32_t* cu_seqlens, int64_t total) {
   const BwdShape s = make_shape(batch, heads, kv_heads, seq, head_dim, q_strides, kv_strides,
                                 sm_scale, cu_seqlens, total);
-  TK_BWD_LAUNCH(s.kv_tiles, attn_bwd_dkdv_dma_kernel, (const T*)q, (const T*)k, (const T*)v,
-                (const T*)dout, (T*)dk, (T*)dv, lse, delta, s);
+  const unsigned tiles = static_cast<unsigned>(s.kv_tiles);
+  if (dtype == TK_DTYPE_F16)
+    launch_dkdv<_Float16>(head_dim, causal, tiles, stream, q, k, v, dout, dk, dv, lse, delta, s);
+  else
+    launch_dkdv<__bf16>(head_dim, causal, tiles, stream, q, k, v, dout, dk, dv, lse, delta, s);
 }
 
 }  // namespace tk

@@ -64,12 +64,15 @@ struct DqGeo {
   // registers); PREFETCH transposed units are issued at the end of the elementwise phase.
   static constexpr int NT = 2 * FP;
   static constexpr int DEPTH = D == 128 ? 2 : 3, PREFETCH = 2;
-  // K (rows and transposed): rows 16 apart take distinct values, and within 8 consecutive
-  // rows (of one parity for D = 64, whose 128-byte rows pair up on the 64 banks) the values
-  // differ above bit 0.
+  // Tiles read both as rows (ds_read_b128: 16 rows of one chunk) and transposed
+  // (ds_read_b64_tr_b16: 8 rows x 32 bytes per 32-lane phase). The transposed phases need
+  // bits 1..3 of the swizzle distinct over rows 0..7 and over rows 8..15; for the row reads
+  // gfx950's bank mapping was measured rather than derived: with these swizzles a stream of
+  // either read sustains 236-256 B/clock/CU, while the swizzle ((r & 7) << 1) | r3 (a
+  // bijection on 16 rows) held the row reads to 155 B/clock/CU.
   static __device__ __forceinline__ int kswz(int r) {
-    return D == 128 ? (((r & 7) << 1) | ((r >> 3) & 1))
-                    : ((((r >> 1) & 3) << 1) | ((r >> 3) & 1));
+    return D == 128 ? (((r >> 3) & 1) | ((r & 3) << 1) | ((((r >> 2) ^ (r >> 3)) & 1) << 3))
+                    : (r & 7);
   }
   // V (rows only): 16 consecutive rows of one chunk on distinct banks.
   static __device__ __forceinline__ int vswz(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
