@@ -26,7 +26,7 @@ cache reuse; MFMA rows flush 1 GiB before each launch.
 dense-MFMA calibration kernels); every row and ``roofline`` also carry
 ``frac_measured`` against them, beside ``frac`` against the published peaks.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu] [--only TEXT]
 """
 
 from __future__ import annotations
@@ -63,6 +63,9 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-kernels", action="store_true", help="skip the per-config kernel table")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--only", default=None,
+                   help="time only the kernel-table rows whose kernel name contains this text "
+                        "(for profiling one kernel family)")
     return p.parse_args()
 
 
@@ -278,8 +281,9 @@ def measured_roofs(torch, device) -> dict:
     }
 
 
-def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
-    """Per-kernel timings of every benchmark configuration (see the module docstring)."""
+def kernel_table(torch, device, roofs: dict | None = None, only: str | None = None) -> list[dict]:
+    """Per-kernel timings of every benchmark configuration (see the module docstring); with
+    `only`, just the rows whose kernel name contains it."""
     from tklab.kernels import flash_attention as fa
     from tklab.kernels import fused_softmax as sm
     from tklab.kernels import matmul as mm
@@ -331,6 +335,8 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
 
     def mem_row(name, config, make, nbytes, reps=30):
         """`make(i)` returns the launch for tensor copy i (copy 0 may reuse the originals)."""
+        if only and only not in name:
+            return False
         ms = streamed(make, nbytes, reps)
         gbps = nbytes / ms / 1e6
         row = {"kernel": name, "config": config, "ms": round(ms, 4), "bytes": nbytes,
@@ -338,8 +344,11 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
         if roofs:
             row["frac_measured"] = round(gbps / roofs["copy_GBps"], 4)
         rows.append(row)
+        return True
 
     def mfma_row(name, config, fn, flops, dtype, reps=10):
+        if only and only not in name:
+            return False
         ms = timed(fn, reps)
         tf = flops / ms / 1e9
         row = {"kernel": name, "config": config, "ms": round(ms, 4), "flops": flops,
@@ -348,6 +357,7 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
             roof = roofs["mfma_TFLOPs"][dtype]["1ms" if ms < 2.5 else "4ms"]
             row["frac_measured"] = round(tf / roof, 4)
         rows.append(row)
+        return True
 
     g = torch.Generator(device=device).manual_seed(0)
     bf16 = torch.bfloat16
@@ -440,16 +450,18 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
     wum = (torch.randn(4096, 14336, device=device, generator=g) * sc).to(bf16)
     ym = torch.empty(16384, 14336, device=device, dtype=bf16)
     gm, um = torch.empty_like(ym), torch.empty_like(ym)
-    mfma_row("tk_gemm_swiglu", "bf16 16384x14336x4096 (gate+up GEMMs, SwiGLU epilogue)",
-             lambda: mms._launch(xm, wgm, wum, ym), 2 * 2 * 16384 * 14336 * 4096, "bfloat16",
-             reps=5)
+    timed_swiglu = mfma_row("tk_gemm_swiglu",
+                            "bf16 16384x14336x4096 (gate+up GEMMs, SwiGLU epilogue)",
+                            lambda: mms._launch(xm, wgm, wum, ym),
+                            2 * 2 * 16384 * 14336 * 4096, "bfloat16", reps=5)
 
     def unfused():
         mm._launch_fp32acc((xm, wgm), gm)
         mm._launch_fp32acc((xm, wum), um)
         sgl._launch_forward(um, gm, ym)
 
-    rows[-1]["unfused_ms"] = round(timed(unfused, 5), 4)
+    if timed_swiglu:
+        rows[-1]["unfused_ms"] = round(timed(unfused, 5), 4)
     del xm, wgm, wum, ym, gm, um
     # Config 2 feeding its consumer: residual-RMSNorm then the grouped-query QKV
     # projection, x, r [16384, 4096] @ W [4096, 6144] (32 query + 2 x 8 KV heads of 128):
@@ -462,7 +474,7 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
     wn = (1 + 0.02 * torch.randn(4096, device=device, generator=g)).to(bf16)
     wq = (torch.randn(4096, 6144, device=device, generator=g) * 4096 ** -0.5).to(bf16)
     wf = rnm.fold_norm_weight(wn, wq)
-    mfma_row("residual_rms_norm_matmul (tk_rmsnorm_fwd stats + tk_gemm_rowscale)",
+    timed_norm = mfma_row("residual_rms_norm_matmul (tk_rmsnorm_fwd stats + tk_gemm_rowscale)",
              "bf16 16384x6144x4096, residual add + RMSNorm in front",
              lambda: rnm.residual_rms_norm_matmul(xq, rq, wf, eps=1e-6),
              2 * 16384 * 6144 * 4096, "bfloat16", reps=5)
@@ -475,8 +487,9 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
                             store_stats=True)
         mm._launch_fp32acc((yq, wq), cq)
 
-    rows[-1]["unfused_ms"] = round(timed(unfused_norm_gemm, 5), 4)
-    rows[-1]["fold_ms"] = round(timed(lambda: rnm.fold_norm_weight(wn, wq), 5), 4)
+    if timed_norm:
+        rows[-1]["unfused_ms"] = round(timed(unfused_norm_gemm, 5), 4)
+        rows[-1]["fold_ms"] = round(timed(lambda: rnm.fold_norm_weight(wn, wq), 5), 4)
     del xq, rq, wq, wf, sq, yq, cq
     # Config 5: attention.
     for causal, nctx, d in ((True, 8192, 128), (False, 4096, 128), (True, 8192, 64), (False, 4096, 64)):
@@ -517,7 +530,7 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
     ang = torch.arange(8192, dtype=torch.float32)[:, None] * inv_f[None]
     rcos, rsin = ang.cos().to(bf16).to(device), ang.sin().to(bf16).to(device)
     kr, qr = torch.empty_like(kk), torch.empty_like(qq)
-    mfma_row("tk_attn_fwd_rope", tag + ", RoPE on Q (prologue) and K",
+    timed_rope = mfma_row("tk_attn_fwd_rope", tag + ", RoPE on Q (prologue) and K",
              lambda: fa._launch_rope_forward(qq, kk, vv, rcos, rsin, o, lse, kr, causal=True),
              flops, "bfloat16", reps=5)
 
@@ -526,7 +539,8 @@ def kernel_table(torch, device, roofs: dict | None = None) -> list[dict]:
         fa._rope_positions(kk, rcos, rsin, kr, inverse=False)
         fa._launch_gqa_forward(qr, kr, vv, o, lse, causal=True)
 
-    rows[-1]["unfused_ms"] = round(timed(unfused_rope, 5), 4)
+    if timed_rope:
+        rows[-1]["unfused_ms"] = round(timed(unfused_rope, 5), 4)
     del qq, kk, vv, do, o, lse, kr, qr
     # Variable-length causal attention: one packed batch of 32768 tokens in sequences of
     # 8192, 2 x 4096, 4 x 2048 and 8 x 1024 (H32 Hkv8 D128); FLOPs summed per sequence.
@@ -616,7 +630,7 @@ def main() -> int:
     roofline["measured_peak"] = roofs["copy_GBps"]
     roofline["frac_measured"] = round(achieved / roofs["copy_GBps"], 4)
     if not args.no_kernels:
-        line["kernels"] = kernel_table(torch, device, roofs)
+        line["kernels"] = kernel_table(torch, device, roofs, args.only)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     else:
