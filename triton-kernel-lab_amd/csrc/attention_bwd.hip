@@ -12,14 +12,15 @@
 //             written to LDS as the consumer's B-operand fragments (lane = key);
 //   consumer  dV^T += dO^T P, dK^T += Q^T dS with dO^T / Q^T read transposed
 //             (ds_read_b64_tr_b16) from the same tiles, accumulators in registers.
-// Barrier-separated phases: producer MFMA (block v) | producer elementwise (v) with the
-// consumer's MFMAs (v - 1) | ..., so the exponentials of one wave run beside the other
-// wave's MFMAs, and each wave holds only half of the state (K/V and S/dP, or the dK/dV
-// accumulators). The consumer reads the exchange fragments in the producer's MFMA phase,
-// so one 8 KiB buffer per pair suffices. Q/dO tiles reach LDS by buffer->LDS DMA into a
-// ring (block v is read in phases 2v - 1 .. 2v+3); tiles read both ways store the 16-byte
-// chunk c of row r at slot c ^ swz(r), which keeps the 16-row ds_read_b128 phases and the
-// transposed phases on distinct banks.
+// Barrier-separated phases: producer MFMA (block v) | producer elementwise (v) | ...; the
+// consumer reads block v - 1's exchange fragments at the start of the producer's MFMA
+// phase v and runs its MFMAs for v - 1 beside the producer's elementwise phase (non-causal:
+// its first 2 of 16 read units already beside the producer's MFMAs), so the exponentials of
+// one wave run beside the other wave's MFMAs. Each wave holds only half of the state (K/V
+// and S/dP, or the dK/dV accumulators), and one 8 KiB exchange buffer per pair suffices.
+// Q/dO tiles reach LDS by buffer->LDS DMA into a ring (block v is read in phases 2v - 1 ..
+// 2v+3); tiles read both ways store the 16-byte chunk c of row r at slot c ^ swz(r), which
+// keeps the 16-row ds_read_b128 phases and the transposed phases on distinct banks.
 //
 // head_dim 64, attn_bwd_dkdv_dma_kernel: a workgroup owns 128 keys (4 wave64s x 32, one
 // wave per SIMD) and walks the query blocks of 64. It is held to 256 registers, so two
@@ -510,7 +511,12 @@ struct KvGeo {
   // are in flight; the first PREFETCH units of an MFMA phase are issued at the end of the
   // wave's preceding phase.
   static constexpr int NA = 2 * KS, NB = 4 * FP;
-  static constexpr int DEPTH_A = 3, PREFETCH_A = 2, DEPTH_B = 3, PREFETCH_B = 3;
+  static constexpr int DEPTH_A = 3, PREFETCH_A = 2, DEPTH_B = 3;
+  // Without causal masking the consumer runs units 0 .. SPLIT_B - 1 of a block beside the
+  // producer's MFMAs and the rest beside the producer's elementwise phase (non-causal D128
+  // 1.995 -> 1.934 ms); causal runs all of them beside the elementwise phase (3.77 vs 3.85
+  // ms split), whose diagonal blocks carry the masking.
+  static constexpr int SPLIT_B = 2;
   // Tiles read both as rows (ds_read_b128: 16 rows of one chunk) and transposed
   // (ds_read_b64_tr_b16: 8 rows x 32 bytes per 32-lane phase). The transposed phases need
   // bits 1..3 of the swizzle distinct over rows 0..7 and over rows 8..15; for the row reads
@@ -675,20 +681,23 @@ __device__ __forceinline__ void consumer_unit(i32x4 (&tu)[KvGeo<D>::NB][2], uint
   }
 }
 
-// Consumer MFMA phase: dV^T += dO^T P and dK^T += Q^T dS over the block's 64 queries
-// (adv / adk [ft][kt] register r: feature 16 ft + 4 g + r, key 16 kt + c). Its first
-// PREFETCH_B units were issued by the preceding phase.
-template <typename T, int D>
+// Consumer MFMAs of one block: dV^T += dO^T P and dK^T += Q^T dS over the block's 64
+// queries (adv / adk [ft][kt] register r: feature 16 ft + 4 g + r, key 16 kt + c). The first
+// DEPTH_B units were issued by the caller; after unit SPLIT - 1 (before the first, for
+// SPLIT = 0) the accumulators are pinned and `mid` (the phase barrier) runs, the reads in
+// flight continuing across it.
+template <typename T, int D, int SPLIT, typename F>
 __device__ __forceinline__ void consumer_mfma(uint32_t sb, const uint32_t (&ta)[KvGeo<D>::FT],
                                               const i32x4 (&pf)[2][2], const i32x4 (&df)[2][2],
                                               f32x4 (&adv)[KvGeo<D>::FT][2],
                                               f32x4 (&adk)[KvGeo<D>::FT][2],
-                                              i32x4 (&tu)[KvGeo<D>::NB][2]) {
+                                              i32x4 (&tu)[KvGeo<D>::NB][2], F&& mid) {
   using G = KvGeo<D>;
-  constexpr int FP = G::FP, NU = G::NB, DEPTH = G::DEPTH_B, PRE = G::PREFETCH_B;
-#pragma unroll
-  for (int u = PRE; u < DEPTH && u < NU; ++u) consumer_unit<D>(tu, sb, ta, u);
-  sched_fence();
+  constexpr int FP = G::FP, FT = G::FT, NU = G::NB, DEPTH = G::DEPTH_B;
+  if constexpr (SPLIT == 0) {
+    mid();
+    sched_fence();
+  }
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
     const int after = (u + DEPTH < NU ? u + DEPTH : NU) - (u + 1);
@@ -715,6 +724,17 @@ __device__ __forceinline__ void consumer_mfma(uint32_t sb, const uint32_t (&ta)[
       }
     if (u + DEPTH < NU) consumer_unit<D>(tu, sb, ta, u + DEPTH);
     sched_fence();
+    if (u == SPLIT - 1) {
+#pragma unroll
+      for (int ft = 0; ft < FT; ++ft)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          pin(adv[ft][kt]);
+          pin(adk[ft][kt]);
+        }
+      mid();
+      sched_fence();
+    }
   }
 }
 
@@ -955,14 +975,21 @@ attn_bwd_dkdv_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K,
     i32x4 tu[G::NB][2];
     end_phase();
     end_phase();
-    int stage = 0, j = 0;
-    for (int v = 0; v < nv; ++v, j = j + 1 == nblk ? 0 : j + 1) {
-      const bool act = active(j);
-      const uint32_t sb = lds_base + stage * STB;
-      i32x4 pf[2][2], df[2][2];
-      if (act) {
+    // Causal: the pair's blocks of each head start at the first one holding a query >= its
+    // first key; the blocks before it only keep the phase count.
+    const int jact = CAUSAL ? min(nblk, max(0, pk0 / BB - first)) : 0;
+    int stage = 0, v = 0;
+    for (int dg = 0; dg < s.group; ++dg) {
+      for (int j = 0; j < jact; ++j, ++v) {
+        end_phase();
+        if (v + 1 < nv) end_phase();
+        stage = stage + 1 == STAGES ? 0 : stage + 1;
+      }
+      for (int j = jact; j < nblk; ++j, ++v) {
+        const uint32_t sb = lds_base + stage * STB;
         // The producer's fragments of block v, then the first transposed units; the
-        // exchange reads have completed once only the prefetched units are outstanding.
+        // exchange reads have completed once only those units are outstanding.
+        i32x4 pf[2][2], df[2][2];
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
@@ -971,8 +998,8 @@ attn_bwd_dkdv_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K,
             df[s2][kt] = lds_read_b128<4096>(xb + (2 * s2 + kt) * 1024);
           }
 #pragma unroll
-        for (int u = 0; u < G::PREFETCH_B; ++u) consumer_unit<D>(tu, sb, ta, u);
-        wait_lgkm<4 * G::PREFETCH_B>();
+        for (int u = 0; u < G::DEPTH_B; ++u) consumer_unit<D>(tu, sb, ta, u);
+        wait_lgkm<4 * G::DEPTH_B>();
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
@@ -980,18 +1007,17 @@ attn_bwd_dkdv_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K,
             pin(pf[s2][kt]);
             pin(df[s2][kt]);
           }
+        consumer_mfma<T, D, CAUSAL ? 0 : G::SPLIT_B>(sb, ta, pf, df, adv, adk, tu, end_phase);
+#pragma unroll
+        for (int ft = 0; ft < FT; ++ft)
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) {
+            pin(adv[ft][kt]);
+            pin(adk[ft][kt]);
+          }
+        if (v + 1 < nv) end_phase();
+        stage = stage + 1 == STAGES ? 0 : stage + 1;
       }
-      end_phase();
-      if (act) consumer_mfma<T, D>(sb, ta, pf, df, adv, adk, tu);
-#pragma unroll
-      for (int ft = 0; ft < FT; ++ft)
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          pin(adv[ft][kt]);
-          pin(adk[ft][kt]);
-        }
-      if (v + 1 < nv) end_phase();
-      stage = stage + 1 == STAGES ? 0 : stage + 1;
     }
     wait_vmcnt<0>();
     // dK = scale (dK^T)^T, dV = (dV^T)^T: register r of adk / adv [ft][kt] is feature
