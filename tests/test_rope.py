@@ -112,3 +112,33 @@ def test_config_shape_bf16_q_4x32x4096x128() -> None:
     # bf16 tables: |cos^2 + sin^2 - 1| <= ~2^-7; outputs round to bf16 too.
     assert torch.allclose(norms_out, norms_in, rtol=2e-2, atol=1e-2)
     assert math.isfinite(float(y.float().abs().max()))
+
+
+def _config3_tables(b: int, h: int, s: int, d: int):
+    inv_freq = 10000.0 ** (-torch.arange(0, d, 2, device="cuda", dtype=torch.float32) / d)
+    angle = torch.arange(s, device="cuda", dtype=torch.float32)[:, None] * inv_freq[None, :]
+    cos = torch.cos(angle).to(torch.bfloat16).expand(b * h, s, d // 2).reshape(-1, d // 2)
+    sin = torch.sin(angle).to(torch.bfloat16).expand(b * h, s, d // 2).reshape(-1, d // 2)
+    return cos, sin
+
+
+def test_config_shape_backward_bf16_4x32x4096x128() -> None:
+    """benchmark config 3 RoPE backward: dx only (constant tables, the autograd path) and the
+    dcos/dsin variant, at [4,32,4096,128] bf16, bitwise on every 509th row against the oracle;
+    dx is the inverse rotation of dy, so row norms are preserved up to bf16 rounding."""
+    torch.manual_seed(1)
+    b, h, s, d = 4, 32, 4096, 128
+    cos, sin = _config3_tables(b, h, s, d)
+    x = torch.randn(b * h * s, d, device="cuda", dtype=torch.bfloat16).requires_grad_(True)
+    dy = torch.randn_like(x)
+    (dx,) = torch.autograd.grad(rope(x, cos, sin), (x,), grad_outputs=dy)
+    rows = torch.arange(0, x.shape[0], 509, device="cuda")
+    want_dx, want_dcos, want_dsin = oracle.rope_bwd(
+        host(dy[rows]), host(x[rows]), host(cos[rows]), host(sin[rows]), "bfloat16"
+    )
+    assert bits_equal(dx[rows], dev(want_dx, dx).to(torch.bfloat16))
+    assert torch.allclose(dx.float().pow(2).sum(-1), dy.float().pow(2).sum(-1), rtol=2e-2, atol=1e-2)
+    dx_all, dcos, dsin = _launch_backward(dy, x.detach(), cos, sin)
+    assert bits_equal(dx_all, dx)
+    assert bits_equal(dcos[rows], dev(want_dcos, dcos).to(torch.bfloat16))
+    assert bits_equal(dsin[rows], dev(want_dsin, dsin).to(torch.bfloat16))
