@@ -134,3 +134,32 @@ def test_config_shape_bf16_16384x4096_matches_the_oracle() -> None:
     assert bits_equal(dx, dr)
     assert_relative_frobenius(dw, dev(dw_ref, dw), max_relative_error=1e-2)
     assert_close(dw, dev(dw_ref, dw))
+
+
+def test_backward_rejects_deterministic_mode_like_the_reference() -> None:
+    """Reference ``tests/test_residual_rms_norm.py:242-257``: both outputs receive gradient,
+    so the norm backward runs and raises RuntimeError "not deterministic"."""
+    x, r, w, dsum, dout = _problem(rows=8, cols=16)
+    previous = torch.are_deterministic_algorithms_enabled()
+    previous_warn = torch.is_deterministic_algorithms_warn_only_enabled()
+    try:
+        torch.use_deterministic_algorithms(True)
+        s, y = residual_rms_norm(x, r, w)
+        with pytest.raises(RuntimeError, match="not deterministic"):
+            torch.autograd.grad((s, y), (x, r, w), grad_outputs=(dsum, dout))
+    finally:
+        torch.use_deterministic_algorithms(previous, warn_only=previous_warn)
+
+
+def test_backward_warns_in_deterministic_warn_only_mode() -> None:
+    x, r, w, dsum, dout = _problem(rows=8, cols=16)
+    previous = torch.are_deterministic_algorithms_enabled()
+    previous_warn = torch.is_deterministic_algorithms_warn_only_enabled()
+    try:
+        torch.use_deterministic_algorithms(True, warn_only=True)
+        s, y = residual_rms_norm(x, r, w)
+        with pytest.warns(RuntimeWarning, match="not deterministic"):
+            grads = torch.autograd.grad((s, y), (x, r, w), grad_outputs=(dsum, dout))
+    finally:
+        torch.use_deterministic_algorithms(previous, warn_only=previous_warn)
+    assert bits_equal(grads[0], grads[1])

@@ -14,6 +14,7 @@ import torch.nn.functional as F
 from _helpers import bits_equal, dev, host, name, strided_rows
 from oracle import oracle
 from tklab.harness.tolerances import assert_close, assert_relative_frobenius
+from tklab.kernels import _norm_common
 from tklab.kernels.rms_norm import (
     _launch_backward_stage1,
     _launch_backward_stage2,
@@ -139,7 +140,38 @@ def test_stage1_ragged_and_empty_groups(rows: int, dtype: torch.dtype, cols: int
     assert_relative_frobenius(buffers.dw, dev(dw_ref, buffers.dw), max_relative_error=1e-2)
 
 
-def test_backward_is_bitwise_reproducible_and_runs_in_deterministic_mode() -> None:
+def test_backward_rejects_deterministic_mode_like_the_reference() -> None:
+    """Reference ``tests/test_rms_norm.py:127-139``: RuntimeError "not deterministic"."""
+    x, w, dy = _problem(rows=8, cols=16)
+    previous = torch.are_deterministic_algorithms_enabled()
+    previous_warn = torch.is_deterministic_algorithms_warn_only_enabled()
+    try:
+        torch.use_deterministic_algorithms(True)
+        output = rms_norm(x, w)
+        with pytest.raises(RuntimeError, match="not deterministic"):
+            torch.autograd.grad(output, (x, w), grad_outputs=dy)
+    finally:
+        torch.use_deterministic_algorithms(previous, warn_only=previous_warn)
+
+
+def test_backward_warns_in_deterministic_warn_only_mode_like_the_reference() -> None:
+    """Reference ``tests/test_rms_norm.py:142-152``: RuntimeWarning "not deterministic"."""
+    x, w, dy = _problem(rows=8, cols=16)
+    previous = torch.are_deterministic_algorithms_enabled()
+    previous_warn = torch.is_deterministic_algorithms_warn_only_enabled()
+    try:
+        torch.use_deterministic_algorithms(True, warn_only=True)
+        output = rms_norm(x, w)
+        with pytest.warns(RuntimeWarning, match="not deterministic"):
+            torch.autograd.grad(output, (x, w), grad_outputs=dy)
+    finally:
+        torch.use_deterministic_algorithms(previous, warn_only=previous_warn)
+
+
+def test_backward_is_bitwise_reproducible_and_runs_in_deterministic_mode_when_allowed(
+    monkeypatch: pytest.MonkeyPatch,
+) -> None:
+    monkeypatch.setattr(_norm_common, "REJECT_DETERMINISTIC_MODE", False)
     torch.manual_seed(5)
     x, w, dy = _problem(rows=515, cols=4096)
     previous = torch.are_deterministic_algorithms_enabled()

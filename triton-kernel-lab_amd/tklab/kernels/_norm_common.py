@@ -9,6 +9,9 @@ MI355X ones used by ``csrc/rmsnorm.hip``.
 from __future__ import annotations
 
 import math
+import warnings
+
+import torch
 
 # A normalized row is held in registers by one thread group, so it must fit
 # the single-pass budget (reference ``_norm_common.py:17``).
@@ -26,6 +29,34 @@ STAGE2_BLOCK_N = 32
 # keep two 4-wave workgroups per compute unit (256 CUs) streaming rows, while the
 # float32 partial buffer stays at 512 x columns.
 DEFAULT_GROUPS = 512
+
+# The reference's norm backwards reduce dweight under a spin lock in a scheduling-dependent
+# order, so under ``torch.use_deterministic_algorithms(True)`` they raise ``RuntimeError`` (and
+# warn with ``RuntimeWarning`` in warn-only mode), reference ``rms_norm.py:370-378`` and
+# ``layer_norm.py:367-375``. The reduction here is order-fixed and bitwise reproducible, but the
+# drop-in keeps that observable by default so code (and tests) written against the reference
+# behave the same. Setting this to False lets deterministic mode run the backward.
+REJECT_DETERMINISTIC_MODE = True
+
+
+def check_deterministic_mode(kernel: str) -> None:
+    """Raise or warn like the reference's norm backward under PyTorch's deterministic mode.
+
+    Does nothing when deterministic algorithms are off or ``REJECT_DETERMINISTIC_MODE`` is
+    False. The message keeps the reference's "not deterministic" fragment.
+    """
+    if not REJECT_DETERMINISTIC_MODE or not torch.are_deterministic_algorithms_enabled():
+        return
+    message = (
+        f"{kernel} backward is reported as not deterministic, as the reference's lock "
+        "reduction is; this build's fixed-order reduction is bitwise reproducible: set "
+        "tklab.kernels._norm_common.REJECT_DETERMINISTIC_MODE = False to run it in "
+        "deterministic mode"
+    )
+    if torch.is_deterministic_algorithms_warn_only_enabled():
+        warnings.warn(message, RuntimeWarning, stacklevel=3)
+    else:
+        raise RuntimeError(message)
 
 
 def validate_epsilon(eps: float) -> None:

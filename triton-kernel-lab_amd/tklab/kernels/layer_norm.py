@@ -4,8 +4,10 @@ Contract of ``src/tklab/kernels/layer_norm.py``: 2-D input with unit-stride
 rows, contiguous weight and bias of the feature width, float32 statistics,
 validation order and messages as in ``layer_norm.py:177-205``. The backward
 uses the same lock-free group reduction as RMSNorm (``tklab.kernels.rms_norm``),
-so it is bitwise reproducible and runs under PyTorch's deterministic mode;
-``_BackwardBuffers`` keeps the reference's fields.
+so it is bitwise reproducible; under PyTorch's deterministic mode it raises (or warns)
+as the reference does (``layer_norm.py:367-375``) unless
+``_norm_common.REJECT_DETERMINISTIC_MODE`` is False. ``_BackwardBuffers`` keeps the
+reference's fields.
 """
 
 from __future__ import annotations
@@ -24,6 +26,7 @@ from tklab.kernels._norm_common import (
     EPS,
     MAX_FEATURE_BYTES,
     block_size_and_warps,
+    check_deterministic_mode,
     group_size_m,
     validate_epsilon,
 )
@@ -176,6 +179,7 @@ def _launch_backward(
     if dy.stride(1) != 1:
         dy = dy.contiguous()
     assert_int32_addressable(dy, name="upstream gradient")
+    check_deterministic_mode("LayerNorm")
     buffers = _make_backward_buffers(x, weight)
     _launch_backward_stage1(dy, x, weight, mean, rstd, buffers)
     _launch_backward_stage2(buffers, x.shape[1])

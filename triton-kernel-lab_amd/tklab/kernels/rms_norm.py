@@ -9,8 +9,10 @@ Backward. The reference reduces dweight partials under a global spin lock in
 a scheduling-dependent order and therefore refuses PyTorch's deterministic
 mode (``rms_norm.py:370-378``). Here each of ``min(group_size, rows)``
 workgroups owns one contiguous range of ``ceil(rows / groups)`` rows, writes
-one float32 partial row with a plain store (zero for a group past the last row), and stage 2 sums the partial rows in a fixed order. The result is
-bitwise reproducible, so deterministic mode is honoured instead of refused.
+one float32 partial row with a plain store (zero for a group past the last row), and stage 2
+sums the partial rows in a fixed order. The result is bitwise reproducible. Under deterministic
+mode ``_launch_backward`` still raises (or warns) as the reference does, unless
+``_norm_common.REJECT_DETERMINISTIC_MODE`` is set to False.
 ``_BackwardBuffers.locks`` keeps its reference layout (``locks || counts``):
 the lock half stays zero and stage 1 sets count ``g`` to 1 for every active
 group, the observable state the reference's protocol leaves behind.
@@ -32,6 +34,7 @@ from tklab.kernels._norm_common import (
     EPS,
     MAX_FEATURE_BYTES,
     block_size_and_warps,
+    check_deterministic_mode,
     group_size_m,
     validate_epsilon,
 )
@@ -229,6 +232,7 @@ def _launch_backward(
         if incoming_dx.stride(1) != 1:
             incoming_dx = incoming_dx.contiguous()
         assert_int32_addressable(incoming_dx, name="incoming input gradient")
+    check_deterministic_mode("RMSNorm")
     buffers = _make_backward_buffers(x, weight)
     _launch_backward_stage1(dy, x, weight, rstd, buffers, incoming_dx=incoming_dx)
     _launch_backward_stage2(buffers, x.shape[1])
