@@ -96,6 +96,26 @@ int tk_rmsnorm_bwd_stage1(int dtype, void* dx, const void* dy, const void* incom
 int tk_rmsnorm_bwd_stage2(int dtype, const float* partial_dw, void* dw, int64_t group_count,
                           int64_t cols, void* stream);
 
+/* Size of the device array that holds tk_rmsnorm_bwd_noalloc's partial rows (16 MiB per GPU). */
+#define TK_RMSNORM_NOALLOC_SCRATCH_BYTES (16LL << 20)
+
+/* RMSNorm backward, both stages, allocating nothing: the same kernels and results as
+ * tk_rmsnorm_bwd_stage1 (no `locks` counts) followed by tk_rmsnorm_bwd_stage2 with the same
+ * group_size, so dx and dw are bitwise those of the two-call path. The float32 partial rows
+ * (group_count = min(group_size, rows) rows of `cols`) live in a library-owned device array of
+ * TK_RMSNORM_NOALLOC_SCRATCH_BYTES on each GPU, kept until the process ends; a problem needing
+ * more (group_count * cols * 4 bytes) is rejected with an error, before any launch. The call
+ * makes no hipMalloc/hipFree and no memset: every partial row read is written first.
+ * All calls on one GPU share that array, so calls that overlap on one GPU (different streams or
+ * threads) race; serialize them. The stream must belong to the current device.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid allocation). */
+int tk_rmsnorm_bwd_noalloc(int dtype, void* dx, void* dw, const void* dy, const void* incoming_dx,
+                           const void* x, const void* weight, const float* rstd, int64_t rows,
+                           int64_t cols, int64_t x_row_stride, int64_t dy_row_stride,
+                           int64_t incoming_dx_row_stride, int64_t dx_row_stride,
+                           int64_t group_size, void* stream);
+
 /* SwiGLU forward y = value * gate * sigmoid(gate).
  * Replaces `_swiglu_forward_kernel[...]`, src/tklab/kernels/swiglu.py:157-167. */
 int tk_swiglu_fwd(int dtype, const void* value, const void* gate, void* y, int64_t rows,

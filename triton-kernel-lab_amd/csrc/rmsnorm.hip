@@ -15,6 +15,8 @@
 // registers (a thread always holds the same columns), folds its row slots together
 // in LDS in a fixed order and writes partial_dw[g] once. Stage 2 sums the partial
 // rows in a fixed order. Both stages are bitwise reproducible.
+#include <atomic>
+
 #include "rows.hpp"
 
 #pragma clang fp contract(off)
@@ -267,7 +269,7 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
     }
     for (int c = threadIdx.x; c < cols; c += bwd_block<RT>()) out[c] = fold[c];
   }
-  if (threadIdx.x == 0) counts[group] = 1;
+  if (counts != nullptr && threadIdx.x == 0) counts[group] = 1;
 }
 
 constexpr int kStage2Cols = 32;    // columns per workgroup: 128-byte row segments
@@ -404,4 +406,99 @@ extern "C" int tk_rmsnorm_bwd_stage2(int dtype, const float* partial_dw, void* d
     hipLaunchKernelGGL((rmsnorm_bwd_stage2_kernel<T>), grid, dim3(kStage2Threads), 0, s,
                        partial_dw, static_cast<T*>(dw), (int)group_count, (int)cols));
   return tk::check_launch("rmsnorm_bwd_stage2");
+}
+
+// ----------------------------------------------------------------------------------------------
+// Backward without allocation: the dweight partial rows live in a library-owned device array.
+
+namespace {
+
+// Float32 dweight partial rows of tk_rmsnorm_bwd_noalloc: group_count x cols floats at most
+// (16 MiB). Each GPU holds its own copy for the life of the process. In host code the name is
+// only a stand-in: kernels receive the device address from hipGetSymbolAddress.
+constexpr int64_t kNoallocScratchFloats = TK_RMSNORM_NOALLOC_SCRATCH_BYTES / 4;
+__device__ __align__(256) float scratch[kNoallocScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch_address[kMaxDevices];
+
+// Device address of the current device's `scratch`, looked up once per device (the lookup is
+// idempotent, so two threads racing on the first call store the same address).
+int scratch_address(const char* what, hipStream_t stream, float** out) {
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return tk::fail("%s: hipGetDevice failed: %s", what, hipGetErrorString(err));
+  if (device < 0 || device >= kMaxDevices)
+    return tk::fail("%s: device ordinal %d out of range", what, device);
+  if (stream != nullptr) {
+    hipDevice_t stream_device = 0;
+    err = hipStreamGetDevice(stream, &stream_device);
+    if (err != hipSuccess)
+      return tk::fail("%s: hipStreamGetDevice failed: %s", what, hipGetErrorString(err));
+    if (stream_device != device)
+      return tk::fail("%s: the stream belongs to device %d, the current device is %d", what,
+                      static_cast<int>(stream_device), device);
+  }
+  float* address = g_scratch_address[device].load(std::memory_order_acquire);
+  if (address == nullptr) {
+    void* symbol = nullptr;
+    err = hipGetSymbolAddress(&symbol, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || symbol == nullptr)
+      return tk::fail("%s: hipGetSymbolAddress(scratch) failed: %s", what, hipGetErrorString(err));
+    address = static_cast<float*>(symbol);
+    g_scratch_address[device].store(address, std::memory_order_release);
+  }
+  *out = address;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int tk_rmsnorm_bwd_noalloc(int dtype, void* dx, void* dw, const void* dy,
+                                      const void* incoming_dx, const void* x, const void* weight,
+                                      const float* rstd, int64_t rows, int64_t cols,
+                                      int64_t x_row_stride, int64_t dy_row_stride,
+                                      int64_t incoming_dx_row_stride, int64_t dx_row_stride,
+                                      int64_t group_size, void* stream) {
+  if (dx == nullptr || dw == nullptr || dy == nullptr || x == nullptr || weight == nullptr ||
+      rstd == nullptr)
+    return tk::fail("rmsnorm_bwd_noalloc: null pointer");
+  if (group_size <= 0 || group_size > INT32_MAX)
+    return tk::fail("rmsnorm_bwd_noalloc: group_size must be positive");
+  if (rows <= 0 || cols <= 0) return tk::fail("rmsnorm_bwd_noalloc: empty problem");
+  const int64_t group_count = group_size < rows ? group_size : rows;
+  if (cols > kNoallocScratchFloats || group_count > kNoallocScratchFloats / cols)
+    return tk::fail("rmsnorm_bwd_noalloc: %lld partial rows of %lld columns need %lld bytes of "
+                    "scratch, above the %lld-byte maximum (use fewer groups)",
+                    static_cast<long long>(group_count), static_cast<long long>(cols),
+                    static_cast<long long>(group_count * cols * 4),
+                    static_cast<long long>(TK_RMSNORM_NOALLOC_SCRATCH_BYTES));
+  const bool vector_ok = tk::valid_dtype(dtype) && rows_vector_ok(
+      dtype, cols, {dx, dy, incoming_dx, x, weight},
+      {x_row_stride, dy_row_stride, incoming_dx ? incoming_dx_row_stride : 0, dx_row_stride});
+  tk::RowShape shape;
+  if (check_rows("rmsnorm_bwd_noalloc", dtype, rows, cols, vector_ok, &shape)) return 1;
+  tk::pick_row_shape(cols, &shape, 16);
+  hipStream_t s = tk::as_stream(stream);
+  float* partial = nullptr;
+  if (scratch_address("rmsnorm_bwd_noalloc", s, &partial)) return 1;
+  // Stage 1 writes every one of the group_count partial rows (zeros for a group that owns no
+  // row), so the array needs no clearing; stage 2 reads exactly those rows.
+  TK_DISPATCH_DTYPE(dtype, T,
+    TK_DISPATCH_VEC(T, vector_ok,
+      TK_DISPATCH_ROW_SHAPE(shape,
+        hipLaunchKernelGGL((rmsnorm_bwd_stage1_kernel<T, VEC, RT, VALS>),
+                           dim3(static_cast<unsigned>(group_count)), dim3(bwd_block<RT>()), 0, s,
+                           static_cast<T*>(dx), static_cast<const T*>(dy),
+                           static_cast<const T*>(incoming_dx), partial, static_cast<const T*>(x),
+                           static_cast<const T*>(weight), rstd, nullptr, (int)rows, (int)cols,
+                           x_row_stride, dy_row_stride, incoming_dx_row_stride,
+                           dx_row_stride))));
+  if (tk::check_launch("rmsnorm_bwd_noalloc (stage 1)")) return 1;
+  TK_DISPATCH_DTYPE(dtype, T,
+    hipLaunchKernelGGL((rmsnorm_bwd_stage2_kernel<T>),
+                       dim3(static_cast<unsigned>(tk::cdiv(cols, kStage2Cols))),
+                       dim3(kStage2Threads), 0, s, partial, static_cast<T*>(dw), (int)group_count,
+                       (int)cols));
+  return tk::check_launch("rmsnorm_bwd_noalloc (stage 2)");
 }

@@ -38,6 +38,9 @@ _SIGNATURES: dict[str, list[object]] = {
         _I32, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P,
     ],
     "tk_rmsnorm_bwd_stage2": [_I32, _P, _P, _I64, _I64, _P],
+    "tk_rmsnorm_bwd_noalloc": [
+        _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P,
+    ],
     "tk_swiglu_fwd": [_I32, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P],
     "tk_swiglu_bwd": [_I32, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
     "tk_rope_fwd": [_I32, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
