@@ -15,10 +15,12 @@ algorithmic bytes per launch over its average duration, measured with events
 on the launch stream around that kernel inside the timed region (an untimed
 attribution pass with events around every launch picks it; `attribution_ms`). ``traffic`` comes from the
 committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when present.
-``cpu_baseline`` times the CPU oracle (oracle/tklab_oracle.c) on a bounded
-row sample of the same workload on the host cores.
+``reference_gpu`` times the reference's PyTorch path for the same step on the GPU.
+``cpu_baseline`` times that PyTorch path on the host CPU (float32 upcasts, full size);
+``cpu_oracle_port`` the CPU oracle (oracle/tklab_oracle.c) on a row sample.
 ``kernels`` times every other benchmark configuration (softmax, SwiGLU, RoPE,
-GEMM, attention) per kernel. Memory-bound rows run back-to-back launches that
+GEMM, attention) per kernel, each beside torch's own GPU path for the same work
+(``reference_ms``, ``speedup``). Memory-bound rows run back-to-back launches that
 rotate over enough copies of their tensors to touch at least 1 GiB (four times
 the 256 MiB last-level cache), so they measure steady HBM streaming without
 cache reuse; MFMA rows flush 1 GiB before each launch.
@@ -173,8 +175,125 @@ def time_step(torch, step: Step, steps: int, warmup: int) -> tuple[float, str, f
     return ms_step, dominant, dominant_ms, attribution
 
 
-def cpu_baseline(seconds: float) -> dict:
-    """Oracle residual RMSNorm fwd+bwd on a 2048-row sample, repeated for ~`seconds`."""
+def _cpu_facts() -> dict:
+    """Host CPU model, logical CPUs, physical cores and the CPUs this process may use."""
+    model, cores = None, set()
+    try:
+        phys = core = None
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "model name" and model is None:
+                model = val
+            elif key == "physical id":
+                phys = val
+            elif key == "core id":
+                core = val
+            elif not key and phys is not None and core is not None:
+                cores.add((phys, core))
+                phys = core = None
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(),
+            "physical_cores": len(cores) or None, "usable_cpus": usable}
+
+
+def torch_gpu_step_ms(torch, step: Step, steps: int) -> float:
+    """The reference's PyTorch path for the step on the GPU in the step's dtype: x + r,
+    F.rms_norm and torch.autograd.grad of both outputs (what the reference's benchmark
+    times beside its kernels). Mean ms per step over `steps` after 3 warmups."""
+    import torch.nn.functional as F
+
+    leaves = [t.detach().requires_grad_(True) for t in (step.x, step.r, step.w)]
+
+    def once():
+        s_ = leaves[0] + leaves[1]
+        y_ = F.rms_norm(s_, (COLS,), leaves[2], EPS)
+        return torch.autograd.grad((s_, y_), leaves, (step.dsum, step.dout))
+
+    for _ in range(3):
+        once()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(steps):
+        once()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def cpu_baseline(torch, reps: int = 5) -> dict:
+    """The reference's own PyTorch path for the step on the host CPU.
+
+    The reference checks its kernels against ``x + r`` -> ``F.rms_norm`` and
+    ``torch.autograd.grad`` evaluated on float32 upcasts (its ``ref_fn``,
+    ``residual_rms_norm.py:279-286``, and ``tests/test_correctness.py:40``). This times
+    exactly that on the full 16384 x 4096 workload (same seeded draws as the GPU step,
+    rounded to bf16, then upcast), one warmup and the median of `reps`, and reports it
+    with the step's algorithmic byte count. Threads: the physical cores this process may
+    use, capped at 16 (the CPU share of one GPU on the benchmark boxes). A native-bf16
+    run of the same path is reported beside it.
+    """
+    import torch.nn.functional as F
+
+    facts = _cpu_facts()
+    usable = facts["usable_cpus"] or 1
+    threads = max(1, min(16, facts["physical_cores"] or usable, usable))
+    previous = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        g = torch.Generator().manual_seed(0)
+        bf16 = torch.bfloat16
+        x = torch.randn(ROWS, COLS, generator=g).to(bf16)
+        r = torch.randn(ROWS, COLS, generator=g).to(bf16)
+        w = (1 + 0.02 * torch.randn(COLS, generator=g)).to(bf16)
+        dsum = torch.randn(ROWS, COLS, generator=g).to(bf16)
+        dout = torch.randn(ROWS, COLS, generator=g).to(bf16)
+
+        def run(dtype) -> list[float]:
+            leaves = [t.to(dtype).requires_grad_(True) for t in (x, r, w)]
+            grads = (dsum.to(dtype), dout.to(dtype))
+            times = []
+            for _ in range(reps + 1):
+                t0 = time.perf_counter_ns()
+                s_ = leaves[0] + leaves[1]
+                y_ = F.rms_norm(s_, (COLS,), leaves[2], EPS)
+                torch.autograd.grad((s_, y_), leaves, grads)
+                times.append((time.perf_counter_ns() - t0) / 1e9)
+            return times[1:]
+
+        f32 = run(torch.float32)
+        native = run(bf16)
+    finally:
+        torch.set_num_threads(previous)
+    step_bytes = sum(STEP_BYTES.values())
+    med32, medbf = statistics.median(f32), statistics.median(native)
+    return {
+        "value": round(step_bytes / med32 / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "reference",
+        "impl": "torch",
+        "ms_per_step": round(med32 * 1e3, 2),
+        "bf16_native_value": round(step_bytes / medbf / 1e9, 3),
+        "bf16_native_ms_per_step": round(medbf * 1e3, 2),
+        "torch_threads": threads,
+        **facts,
+        "sample": f"the reference's PyTorch path (x + r, F.rms_norm, torch.autograd.grad of both "
+                  f"outputs) on float32 upcasts of the full {ROWS} x {COLS} step, median of "
+                  f"{reps} after 1 warmup, {threads} torch threads; value uses the step's "
+                  f"{step_bytes} algorithmic bytes",
+    }
+
+
+def cpu_oracle_port(seconds: float) -> dict:
+    """The CPU oracle (C restatement) on a 2048-row sample, repeated for ~`seconds`."""
     import numpy as np
 
     from oracle import oracle
@@ -245,6 +364,23 @@ def measured_roofs(torch, device) -> dict:
     if not torch.equal(src, dst):
         raise RuntimeError("tk_roof_copy produced a wrong copy")
     del src, dst
+    # Read:write mixes of the same access shape, 512 MiB per array.
+    part = 1 << 29
+    srcs = torch.randint(-2**31, 2**31 - 1, (3 * part // 4,), dtype=torch.int32, device=device)
+    dsts = torch.empty(2 * part // 4, dtype=torch.int32, device=device)
+    mixes: dict[str, float] = {}
+    for reads, writes in ((1, 0), (0, 1), (1, 1), (2, 1), (3, 1), (3, 2)):
+        ms = copy_ms(lambda: _hip.call("tk_roof_stream", srcs.data_ptr(), dsts.data_ptr(), part,
+                                       reads, writes, stream))
+        mixes[f"{reads}:{writes}"] = round((reads + writes) * part / ms / 1e6, 1)
+    chunks = part // 16
+    want = srcs.view(3, chunks, 4)
+    want = want[0] ^ want[1] ^ want[2]
+    want[:, 0] ^= torch.arange(chunks, device=device, dtype=torch.int32)
+    got = dsts.view(2, chunks, 4)
+    if not (torch.equal(got[0], want) and torch.equal(got[1], want)):
+        raise RuntimeError("tk_roof_stream (3:2) produced wrong data")
+    del srcs, dsts, want, got
     flush = torch.empty(1 << 28, dtype=torch.float32, device=device)
     waves = 8192
     out = torch.empty(waves, dtype=torch.float32, device=device)
@@ -272,12 +408,16 @@ def measured_roofs(torch, device) -> dict:
             raise RuntimeError("tk_roof_mfma produced non-finite sums")
     del flush, out
     torch.cuda.empty_cache()
+    copy = max(own, ref)
     return {
-        "copy_GBps": round(max(own, ref), 1),
+        "hbm_GBps": round(max(copy, *mixes.values()), 1),
+        "copy_GBps": round(copy, 1),
         "copy_kernels_GBps": {"tk_roof_copy": round(own, 1), "torch copy_": round(ref, 1)},
+        "stream_mixes_GBps": mixes,
         "mfma_TFLOPs": mfma,
-        "note": "measured on this GPU by bench.py; frac_measured divides by copy_GBps "
-                "(HBM rows) or by the MFMA roof of the nearer burst length (MFMA rows)",
+        "note": "measured on this GPU by bench.py; frac_measured divides by hbm_GBps, the best "
+                "of the copy and the tk_roof_stream read:write mixes (HBM rows), or by the MFMA "
+                "roof of the nearer burst length (MFMA rows)",
     }
 
 
@@ -333,8 +473,25 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         torch.cuda.synchronize()
         return a.elapsed_time(b) / reps
 
-    def mem_row(name, config, make, nbytes, reps=30):
-        """`make(i)` returns the launch for tensor copy i (copy 0 may reuse the originals)."""
+    def add_reference(row, name, measure):
+        """torch's own GPU path for the same work (the reference's ref_fn: eager PyTorch,
+        hipBLASLt, SDPA), timed the same way as the row; `speedup` = reference_ms / ms."""
+        if measure is None:
+            return
+        try:
+            ref_ms = measure()
+        except (RuntimeError, NotImplementedError) as exc:  # e.g. no SDPA backend for a shape
+            row["reference"] = name
+            row["reference_error"] = str(exc).splitlines()[0][:160]
+            torch.cuda.synchronize()
+            return
+        row["reference"] = name
+        row["reference_ms"] = round(ref_ms, 4)
+        row["speedup"] = round(ref_ms / row["ms"], 3)
+
+    def mem_row(name, config, make, nbytes, reps=30, ref=None, ref_make=None):
+        """`make(i)` returns the launch for tensor copy i (copy 0 may reuse the originals);
+        `ref_make(i)` the torch reference's call on the same copy."""
         if only and only not in name:
             return False
         ms = streamed(make, nbytes, reps)
@@ -342,11 +499,13 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         row = {"kernel": name, "config": config, "ms": round(ms, 4), "bytes": nbytes,
                "GB/s": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4)}
         if roofs:
-            row["frac_measured"] = round(gbps / roofs["copy_GBps"], 4)
+            row["frac_measured"] = round(gbps / roofs["hbm_GBps"], 4)
+        add_reference(row, ref, None if ref_make is None else
+                      (lambda: streamed(ref_make, nbytes, reps)))
         rows.append(row)
         return True
 
-    def mfma_row(name, config, fn, flops, dtype, reps=10):
+    def mfma_row(name, config, fn, flops, dtype, reps=10, ref=None, ref_fn=None):
         if only and only not in name:
             return False
         ms = timed(fn, reps)
@@ -356,8 +515,43 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         if roofs:
             roof = roofs["mfma_TFLOPs"][dtype]["1ms" if ms < 2.5 else "4ms"]
             row["frac_measured"] = round(tf / roof, 4)
+        add_reference(row, ref, None if ref_fn is None else (lambda: timed(ref_fn(), reps)))
         rows.append(row)
         return True
+
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    # SDPA references run on the fused backends only: the math backend issues bf16 batched
+    # products on transposed views.
+    fused_sdpa = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]
+
+    def sdpa_fwd(q, k, v, causal, gqa=False):
+        def go():
+            with sdpa_kernel(fused_sdpa):
+                return F.scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=gqa)
+        return go
+
+    def sdpa_bwd(q, k, v, do, causal, gqa=False):
+        leaves = [t.detach().requires_grad_(True) for t in (q, k, v)]
+        with sdpa_kernel(fused_sdpa):
+            out = F.scaled_dot_product_attention(*leaves, is_causal=causal, enable_gqa=gqa)
+
+        def go():
+            with sdpa_kernel(fused_sdpa):
+                return torch.autograd.grad(out, leaves, do, retain_graph=True)
+        return go
+
+    def autograd_bwd(fn, inputs, grad_out, wrt):
+        """Backward only: the graph of fn(*inputs) is built once and differentiated again."""
+        leaves = [t.detach().requires_grad_(i in wrt) for i, t in enumerate(inputs)]
+        out = fn(*leaves)
+        targets = [leaves[i] for i in wrt]
+        return lambda: torch.autograd.grad(out, targets, grad_out, retain_graph=True)
+
+    def rotate_half(x, c, s_):
+        x1, x2 = x.chunk(2, dim=-1)
+        return torch.cat((x1 * c - x2 * s_, x2 * c + x1 * s_), dim=-1)
 
     g = torch.Generator(device=device).manual_seed(0)
     bf16 = torch.bfloat16
@@ -369,7 +563,9 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         yi = torch.empty_like(x)
         return lambda: sm._launch((xi,), yi)
 
-    mem_row("tk_softmax_fwd", "f32 4096x4096", softmax_copy, 2 * x.numel() * 4)
+    mem_row("tk_softmax_fwd", "f32 4096x4096", softmax_copy, 2 * x.numel() * 4,
+            ref="torch.softmax",
+            ref_make=lambda i: (lambda xi: lambda: torch.softmax(xi, -1))(x if i == 0 else x.clone()))
     del x
     # Online softmax (rows past the single-pass limit): f32 [64, 1048576]. Bytes as the
     # single-pass cost model (one read, one write); the kernel reads each row twice.
@@ -380,7 +576,9 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         yi = torch.empty_like(xw)
         return lambda: sm._launch_online((xi,), yi)
 
-    mem_row("tk_softmax_online_fwd", "f32 64x1048576", online_copy, 2 * xw.numel() * 4)
+    mem_row("tk_softmax_online_fwd", "f32 64x1048576", online_copy, 2 * xw.numel() * 4,
+            ref="torch.softmax",
+            ref_make=lambda i: (lambda xi: lambda: torch.softmax(xi, -1))(xw if i == 0 else xw.clone()))
     del xw
     # Config 3: SwiGLU bf16 [16384, 14336].
     gate = torch.randn(16384, 14336, device=device, dtype=bf16, generator=g)
@@ -390,9 +588,12 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
     dv = torch.empty_like(gate)
     n = gate.numel()
     mem_row("tk_swiglu_fwd", "bf16 16384x14336",
-            lambda i: (lambda: sg._launch_forward(up, gate, out)), 3 * n * 2)
+            lambda i: (lambda: sg._launch_forward(up, gate, out)), 3 * n * 2,
+            ref="value * F.silu(gate)", ref_make=lambda i: (lambda: up * F.silu(gate)))
     mem_row("tk_swiglu_bwd", "bf16 16384x14336",
-            lambda i: (lambda: sg._launch_backward_into(dy, up, gate, dv, out)), 5 * n * 2)
+            lambda i: (lambda: sg._launch_backward_into(dy, up, gate, dv, out)), 5 * n * 2,
+            ref="autograd of value * F.silu(gate)",
+            ref_make=lambda i: autograd_bwd(lambda v_, g_: v_ * F.silu(g_), (up, gate), dy, (0, 1)))
     del gate, up, dy, out, dv
     # Config 3: RoPE on q [4, 32, 4096, 128] viewed [524288, 128], per-row tables.
     q = torch.randn(4 * 32 * 4096, 128, device=device, dtype=bf16, generator=g)
@@ -409,9 +610,14 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         return lambda: rp._launch_forward(qi, ci, si, out)
 
     mem_row("tk_rope_fwd", "bf16 [4,32,4096,128]", lambda i: rope_copy(i, False),
-            3 * q.numel() * 2)
+            3 * q.numel() * 2, ref="rotate-half (torch.cat of x1*c - x2*s, x2*c + x1*s)",
+            ref_make=lambda i: (lambda a: lambda: rotate_half(*a))(
+                (q, cos, sin) if i == 0 else (q.clone(), cos.clone(), sin.clone())))
     mem_row("tk_rope_bwd", "bf16 [4,32,4096,128] dx only", lambda i: rope_copy(i, True),
-            3 * q.numel() * 2)
+            3 * q.numel() * 2, ref="autograd of rotate-half, dx only",
+            ref_make=lambda i: autograd_bwd(
+                rotate_half, (q, cos, sin) if i == 0 else (q.clone(), cos.clone(), sin.clone()),
+                q, (0,)))
     del q, cos, sin
     # GQA decode (reference decode model geometry Hq 32, Hkv 8, D 128; B 32, L 8192):
     # bytes = unique KV + Q + O (the model's Bytes_min).
@@ -424,7 +630,8 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
     lsed = torch.empty(32, 32, device=device)
     mem_row("tk_gqa_decode", "bf16 B32 Hq32 Hkv8 L8192 D128",
             lambda i: (lambda: gd._launch(qd, kd, vd, None, od, lsed, scale=128 ** -0.5)),
-            2 * kd.numel() * 2 + 2 * qd.numel() * 2)
+            2 * kd.numel() * 2 + 2 * qd.numel() * 2, ref="SDPA (enable_gqa)",
+            ref_make=lambda i: sdpa_fwd(qd[:, :, None], kd, vd, False, gqa=True))
     del qd, kd, vd, od, lsed
     # Config 4: GEMM.
     for dt_name, dt in (("float16", torch.float16), ("bfloat16", bf16)):
@@ -436,7 +643,8 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
             b = (torch.randn(k, nn, device=device, generator=g) * sc).to(dt)
             c = torch.empty(m, nn, device=device, dtype=dt)
             mfma_row("tk_gemm", f"{dt_name} {m}x{nn}x{k}", lambda: mm._launch_fp32acc((a, b), c),
-                     2 * m * nn * k, dt_name)
+                     2 * m * nn * k, dt_name, ref="torch.mm (hipBLASLt)",
+                     ref_fn=lambda: (lambda: torch.mm(a, b)))
             del a, b, c
     # Config 3 fused into its producer: the gate/up GEMM with SwiGLU in the epilogue,
     # x [16384, 4096] @ W_gate, W_up [4096, 14336] -> y [16384, 14336] (two GEMMs' FLOPs);
@@ -453,7 +661,9 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
     timed_swiglu = mfma_row("tk_gemm_swiglu",
                             "bf16 16384x14336x4096 (gate+up GEMMs, SwiGLU epilogue)",
                             lambda: mms._launch(xm, wgm, wum, ym),
-                            2 * 2 * 16384 * 14336 * 4096, "bfloat16", reps=5)
+                            2 * 2 * 16384 * 14336 * 4096, "bfloat16", reps=5,
+                            ref="torch.mm x2 + value * F.silu(gate)",
+                            ref_fn=lambda: (lambda: torch.mm(xm, wum) * F.silu(torch.mm(xm, wgm))))
 
     def unfused():
         mm._launch_fp32acc((xm, wgm), gm)
@@ -477,7 +687,9 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
     timed_norm = mfma_row("residual_rms_norm_matmul (tk_rmsnorm_fwd stats + tk_gemm_rowscale)",
              "bf16 16384x6144x4096, residual add + RMSNorm in front",
              lambda: rnm.residual_rms_norm_matmul(xq, rq, wf, eps=1e-6),
-             2 * 16384 * 6144 * 4096, "bfloat16", reps=5)
+             2 * 16384 * 6144 * 4096, "bfloat16", reps=5,
+             ref="x + r, F.rms_norm, torch.mm",
+             ref_fn=lambda: (lambda: torch.mm(F.rms_norm(xq + rq, (4096,), wn, 1e-6), wq)))
     sq, yq = torch.empty_like(xq), torch.empty_like(xq)
     rstdq = torch.empty(16384, device=device, dtype=torch.float32)
     cq = torch.empty(16384, 6144, device=device, dtype=bf16)
@@ -503,11 +715,13 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         tag = f"bf16 B4 H32 N{nctx} D{d} {'causal' if causal else 'non-causal'}"
         mfma_row("tk_attn_fwd", tag,
                  lambda: fa._launch_forward(qq, kk, vv, o, lse, causal=causal, store_lse=True),
-                 flops, "bfloat16", reps=5)
+                 flops, "bfloat16", reps=5, ref="SDPA (flash/efficient backends)",
+                 ref_fn=lambda: sdpa_fwd(qq, kk, vv, causal))
         mfma_row("tk_attn_bwd (preprocess+dkdv+dq)", tag + ", 2.5x fwd FLOPs",
                  lambda: fa._launch_backward_into(qq, kk, vv, o, lse, do, delta, gq, gk, gv,
                                                   causal=causal),
-                 int(2.5 * flops), "bfloat16", reps=5)
+                 int(2.5 * flops), "bfloat16", reps=5, ref="SDPA backward (flash/efficient)",
+                 ref_fn=lambda: sdpa_bwd(qq, kk, vv, do, causal))
         del qq, kk, vv, do, o, lse, delta, gq, gk, gv
     # Grouped-query attention at the causal config with 8 KV heads (4 query heads each).
     shape, kv_shape = (4, 32, 8192, 128), (4, 8, 8192, 128)
@@ -519,10 +733,11 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
     tag = "bf16 B4 H32 Hkv8 N8192 D128 causal"
     mfma_row("tk_attn_fwd_gqa", tag,
              lambda: fa._launch_gqa_forward(qq, kk, vv, o, lse, causal=True), flops, "bfloat16",
-             reps=5)
+             reps=5, ref="SDPA (enable_gqa)", ref_fn=lambda: sdpa_fwd(qq, kk, vv, True, gqa=True))
     mfma_row("tk_attn_bwd_gqa (preprocess+dkdv+dq)", tag + ", 2.5x fwd FLOPs",
              lambda: fa._launch_gqa_backward(qq, kk, vv, o, lse, do, causal=True),
-             int(2.5 * flops), "bfloat16", reps=5)
+             int(2.5 * flops), "bfloat16", reps=5, ref="SDPA backward (enable_gqa)",
+             ref_fn=lambda: sdpa_bwd(qq, kk, vv, do, True, gqa=True))
     # RoPE in the attention prologue: position tables [8192, 64] (base 1e4); Q rotated
     # as the forward loads it, K rotated once into a workspace. `unfused_ms` is the RoPE
     # kernel on Q and on K, then the plain forward on the rotated tensors.
@@ -586,6 +801,7 @@ def main() -> int:
     ms_step, dominant, dominant_ms, attribution = time_step(torch, step, args.steps, args.warmup)
     step_bytes = sum(STEP_BYTES.values())
     value = step_bytes / (ms_step / 1e3) / 1e9
+    ref_step_ms = torch_gpu_step_ms(torch, step, max(10, args.steps // 4))
 
     achieved = STEP_BYTES[dominant] / (dominant_ms / 1e3) / 1e9
     traffic = _traffic_from_summary() if dominant == "tk_rmsnorm_bwd_stage1" else None
@@ -622,17 +838,24 @@ def main() -> int:
             "bytes_per_step": step_bytes,
         },
         "roofline": roofline,
+        "reference_gpu": {
+            "impl": "torch (x + r, F.rms_norm, torch.autograd.grad), bf16 on this GPU",
+            "ms_per_step": round(ref_step_ms, 5),
+            "value": round(step_bytes / (ref_step_ms / 1e3) / 1e9, 1),
+            "speedup": round(ref_step_ms / ms_step, 3),
+        },
     }
     del step
     torch.cuda.empty_cache()
     roofs = measured_roofs(torch, device)
     line["measured_roofs"] = roofs
-    roofline["measured_peak"] = roofs["copy_GBps"]
-    roofline["frac_measured"] = round(achieved / roofs["copy_GBps"], 4)
+    roofline["measured_peak"] = roofs["hbm_GBps"]
+    roofline["frac_measured"] = round(achieved / roofs["hbm_GBps"], 4)
     if not args.no_kernels:
         line["kernels"] = kernel_table(torch, device, roofs, args.only)
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(torch)
+        line["cpu_oracle_port"] = cpu_oracle_port(args.cpu_seconds)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line))

@@ -79,11 +79,14 @@ def test_matches_the_oracle() -> None:
 
 
 def test_malformed_offsets_stay_inside_the_tensors() -> None:
-    """Offsets past total or decreasing are clamped by the kernels: no fault, finite output."""
+    """Offsets past total or decreasing are rejected on the host by default; without the
+    host check the kernels clamp them: no fault, finite output."""
     q, k, v, _, _ = _packed([100, 100], 2, 2, 64, torch.bfloat16, seed=4)
     cu = torch.tensor([0, 150, 90, 10_000], device="cuda", dtype=torch.int32)
+    with pytest.raises(ValueError):
+        varlen_attention(q, k, v, cu, 150, causal=True)
     with torch.no_grad():
-        out = varlen_attention(q, k, v, cu, 150, causal=True)
+        out = varlen_attention(q, k, v, cu, 150, causal=True, check_offsets=False)
     torch.cuda.synchronize()
     assert torch.isfinite(out[:150].float()).all()
 
@@ -96,3 +99,37 @@ def test_contract() -> None:
         varlen_attention(q, k, v, cu, 0, causal=True)
     with pytest.raises(ValueError, match="total, heads, dim"):
         varlen_attention(q[None], k, v, cu, 20, causal=True)
+
+
+@pytest.mark.parametrize("check_offsets", [True, False])
+def test_padded_packing_zeroes_rows_outside_every_sequence(check_offsets) -> None:
+    """Tokens before cu[0] and after cu[-1] belong to no sequence: zero output and gradients;
+    the sequences themselves match the unpadded packing bitwise."""
+    lengths = [130, 64, 7]
+    lead, tail = 5, 40
+    q, k, v, do, cu = _packed(lengths, 4, 2, 128, torch.bfloat16, seed=71)
+    total = q.shape[0]
+    pad = lambda t: torch.cat([torch.randn(lead, *t.shape[1:], device="cuda", dtype=t.dtype), t,  # noqa: E731
+                               torch.randn(tail, *t.shape[1:], device="cuda", dtype=t.dtype)])
+    qp, kp, vp, dop = (pad(t) for t in (q, k, v, do))
+    cup = cu + lead
+    got = _run(lambda a, b, c: varlen_attention(a, b, c, cup, max(lengths), causal=True,
+                                                check_offsets=check_offsets), (qp, kp, vp), dop)
+    want = _run(lambda a, b, c: varlen_attention(a, b, c, cu, max(lengths), causal=True),
+                (q, k, v), do)
+    for g_t, w_t in zip(got, want):
+        assert bits_equal(g_t[lead:lead + total], w_t)
+        assert not g_t[:lead].any() and not g_t[lead + total:].any()
+
+
+def test_invalid_offsets_are_rejected_on_the_host() -> None:
+    q, k, v, _, cu = _packed([10, 20], 2, 2, 64, torch.float16, seed=72)
+    bad = [
+        (torch.tensor([0, 20, 10], device="cuda", dtype=torch.int32), 20, "non-decreasing"),
+        (torch.tensor([0, 10, 31], device="cuda", dtype=torch.int32), 21, r"\[0, total\]"),
+        (torch.tensor([-1, 10, 30], device="cuda", dtype=torch.int32), 20, r"\[0, total\]"),
+        (cu, 19, "longest sequence"),
+    ]
+    for offsets, max_len, match in bad:
+        with pytest.raises(ValueError, match=match):
+            varlen_attention(q, k, v, offsets, max_len, causal=False)

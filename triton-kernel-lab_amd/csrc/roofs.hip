@@ -5,6 +5,10 @@
 //                   non-temporal accesses, each thread issuing the loads of kUnroll
 //                   chunks of a contiguous 4 KiB-per-wave run before its stores (the
 //                   access shape and cache policy of the elementwise kernels).
+//   tk_roof_stream — the same access shape with R reads and W writes per chunk position
+//                   (R:W of 1:0, 0:1, 1:1, 2:1, 3:1, 3:2): the HBM roof is the best of
+//                   these mixes, since reads and writes turn the HBM bus around
+//                   differently and the kernels here run several mixes.
 //   tk_roof_mfma  — dense v_mfma_f32_16x16x32_{f16,bf16} issue with no memory
 //                   traffic: each wave keeps 2 * kChains independent 16x16 float32
 //                   accumulators so back-to-back MFMAs never wait on one
@@ -49,6 +53,48 @@ __global__ __launch_bounds__(kCopyBlock) void roof_copy_kernel(const i32x4* __re
       const int64_t i = i0 + int64_t(u) * kCopyBlock;
       if (i < chunks) __builtin_nontemporal_store(v[u], dst + i);
     }
+  }
+}
+
+// R arrays of `chunks` 16-byte chunks read, W arrays written; written chunk i is
+// {i, 0, 0, 0} xor the chunks read at position i. With W == 0
+// the xor of everything a thread read is stored only when it equals `sentinel`, which
+// never happens for the calibration data but keeps every load live.
+template <int R, int W>
+__global__ __launch_bounds__(kCopyBlock) void roof_stream_kernel(const i32x4* __restrict__ src,
+                                                                 i32x4* __restrict__ dst,
+                                                                 int64_t chunks, int sentinel) {
+  constexpr int64_t kPass = int64_t(kCopyBlock) * kCopyUnroll;
+  i32x4 sink = i32x4{0, 0, 0, 0};
+  for (int64_t base = int64_t(blockIdx.x) * kPass; base < chunks;
+       base += int64_t(gridDim.x) * kPass) {
+    const int64_t i0 = base + threadIdx.x;
+    i32x4 v[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) v[u] = i32x4{int(i0 + int64_t(u) * kCopyBlock), 0, 0, 0};
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int u = 0; u < kCopyUnroll; ++u) {
+        const int64_t i = i0 + int64_t(u) * kCopyBlock;
+        if (i < chunks) v[u] ^= __builtin_nontemporal_load(src + int64_t(r) * chunks + i);
+      }
+    if constexpr (W == 0) {
+#pragma unroll
+      for (int u = 0; u < kCopyUnroll; ++u) sink ^= v[u];
+    } else {
+#pragma unroll
+      for (int w = 0; w < W; ++w)
+#pragma unroll
+        for (int u = 0; u < kCopyUnroll; ++u) {
+          const int64_t i = i0 + int64_t(u) * kCopyBlock;
+          if (i < chunks) __builtin_nontemporal_store(v[u], dst + int64_t(w) * chunks + i);
+        }
+    }
+  }
+  if constexpr (W == 0) {
+    if (sink[0] == sentinel && sink[1] == sentinel && sink[2] == sentinel && sink[3] == sentinel)
+      dst[blockIdx.x * kCopyBlock + threadIdx.x] = sink;
   }
 }
 
@@ -132,6 +178,41 @@ extern "C" int tk_roof_copy(const void* src, void* dst, int64_t bytes, void* str
                      tk::as_stream(stream), static_cast<const i32x4*>(src),
                      static_cast<i32x4*>(dst), chunks);
   return tk::check_launch("tk_roof_copy");
+}
+
+extern "C" int tk_roof_stream(const void* src, void* dst, int64_t bytes, int reads, int writes,
+                              void* stream) {
+  if (bytes <= 0 || bytes % 16 != 0)
+    return tk::fail("tk_roof_stream: bytes must be a positive multiple of 16 (got %lld)",
+                    static_cast<long long>(bytes));
+  if (src == nullptr || dst == nullptr || !tk::aligned16(src) || !tk::aligned16(dst))
+    return tk::fail("tk_roof_stream: src and dst must be non-null and 16-byte aligned");
+  const int64_t chunks = bytes / 16;
+  int64_t blocks = tk::cdiv(chunks, int64_t(kCopyBlock) * kCopyUnroll);
+  if (blocks > kCopyMaxBlocks) blocks = kCopyMaxBlocks;
+  // With no writes the sink store may touch one chunk per thread of the grid.
+  if (writes == 0 && blocks * kCopyBlock > chunks)
+    return tk::fail("tk_roof_stream: a read-only run needs at least %lld bytes",
+                    static_cast<long long>(blocks * kCopyBlock * 16));
+  const dim3 grid(static_cast<unsigned>(blocks));
+  hipStream_t s = tk::as_stream(stream);
+  const i32x4* in = static_cast<const i32x4*>(src);
+  i32x4* out = static_cast<i32x4*>(dst);
+  const int sentinel = 0x5A5A5A5A;
+#define TK_ROOF_STREAM(R, W)                                                                    \
+  if (reads == R && writes == W) {                                                              \
+    hipLaunchKernelGGL((roof_stream_kernel<R, W>), grid, dim3(kCopyBlock), 0, s, in, out,       \
+                       chunks, sentinel);                                                       \
+    return tk::check_launch("tk_roof_stream");                                                 \
+  }
+  TK_ROOF_STREAM(1, 0)
+  TK_ROOF_STREAM(0, 1)
+  TK_ROOF_STREAM(1, 1)
+  TK_ROOF_STREAM(2, 1)
+  TK_ROOF_STREAM(3, 1)
+  TK_ROOF_STREAM(3, 2)
+#undef TK_ROOF_STREAM
+  return tk::fail("tk_roof_stream: unsupported mix %d reads : %d writes", reads, writes);
 }
 
 extern "C" int tk_roof_mfma(int dtype, float* out, int64_t waves, int64_t iters, void* stream) {

@@ -55,18 +55,19 @@ def time_ms(
     flush = _flush_buffer(device)
     stream = torch.cuda.current_stream(device)
 
-    # Estimate one launch from five, then size the warmup and the timed set.
+    # Estimate one launch from five (events around the launch only, not the flush), then
+    # size the warmup and the timed set.
     fn()
     torch.cuda.synchronize(device)
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(5):
+    probes = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(5)]
+    for a, b in probes:
         flush.zero_()
+        a.record(stream)
         fn()
-    end.record(stream)
+        b.record(stream)
     torch.cuda.synchronize(device)
-    estimate = max(start.elapsed_time(end) / 5, 1e-3)
+    estimate = max(statistics.fmean(a.elapsed_time(b) for a, b in probes), 1e-3)
     for _ in range(max(1, int(warmup_ms / estimate))):
         fn()
     reps = max(1, int(repetition_ms / estimate))

@@ -53,7 +53,14 @@ _DTYPES = (torch.float16, torch.bfloat16)
 _LOG2_E = 1.4426950408889634
 
 # Tile configuration of csrc/attention.hip (forward / backward).
-FORWARD_TILE = {"block_m": 256, "block_n": 64, "num_warps": 4, "num_stages": 2}
+# csrc/attention_fwd.hip (Geo<D>: BM, BN, WAVES, STAGES): 256 queries per workgroup as eight
+# wave64s of 32, key blocks of 64, a 4-stage buffer->LDS K/V ring, v_mfma_f32_16x16x32.
+# "num_warps" counts wave64s.
+FORWARD_TILE = {"kernel": "attn_fwd_dma_kernel", "block_m": 256, "block_n": 64, "num_warps": 8,
+                "num_stages": 4}
+FORWARD_MFMA = {torch.float16: "v_mfma_f32_16x16x32_f16", torch.bfloat16: "v_mfma_f32_16x16x32_bf16"}
+# Backward (csrc/attention_bwd.hip, attention_bwd_dq.hip): dK/dV owns 128 keys per workgroup
+# over query blocks of 64; dQ owns 256 queries over key blocks of 64.
 BACKWARD_TILE = {"block_m": 128, "block_n": 64}
 
 
@@ -506,6 +513,24 @@ def _validate_varlen(
         assert_int32_addressable(tensor, name=name)
 
 
+def _check_offsets(cu_seqlens: torch.Tensor, total: int, max_seqlen: int) -> bool:
+    """Validate the offsets table on the host (one small device-to-host copy).
+
+    Offsets must start at 0 or later, never decrease, end at ``total`` or earlier, and no
+    sequence may be longer than ``max_seqlen``. Returns True when some token rows lie
+    outside every sequence (a padded packing), whose outputs and gradients are then zero.
+    """
+    offsets = cu_seqlens.tolist()
+    if offsets[0] < 0 or offsets[-1] > total:
+        raise ValueError("cu_seqlens must lie in [0, total]")
+    lengths = [b - a for a, b in zip(offsets, offsets[1:])]
+    if min(lengths) < 0:
+        raise ValueError("cu_seqlens must be non-decreasing")
+    if max(lengths) > max_seqlen:
+        raise ValueError("max_seqlen must be at least the longest sequence")
+    return offsets[0] > 0 or offsets[-1] < total
+
+
 def _launch_varlen_forward(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
     max_seqlen: int, output: torch.Tensor, softmax_lse: torch.Tensor | None, *, causal: bool,
@@ -525,9 +550,12 @@ def _launch_varlen_forward(
 def _launch_varlen_backward(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
     max_seqlen: int, output: torch.Tensor, softmax_lse: torch.Tensor, do: torch.Tensor,
-    *, causal: bool,
+    *, causal: bool, zero_fill: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Varlen backward: delta [heads, total], dK/dV per KV head, dQ per query head."""
+    """Varlen backward: delta [heads, total], dK/dV per KV head, dQ per query head.
+
+    With ``zero_fill`` the gradients start at zero, so token rows outside every sequence
+    (which no kernel writes) read as zero."""
     if do.shape != q.shape or do.device != q.device or do.dtype != q.dtype:
         raise ValueError("attention upstream gradient metadata must match Q")
     do = do.contiguous()
@@ -537,7 +565,8 @@ def _launch_varlen_backward(
     stream = _hip.stream_of(q)
     scale = 1.0 / math.sqrt(head_dim)
     delta = torch.empty((heads, total), dtype=torch.float32, device=q.device)
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    alloc = torch.zeros_like if zero_fill else torch.empty_like
+    dq, dk, dv = alloc(q), alloc(k), alloc(v)
     # delta as one sequence of `total` rows: index head * total + token.
     token, head = q.stride(0), q.stride(1)
     _hip.call("tk_attn_bwd_preprocess", code, output.data_ptr(), do.data_ptr(), delta.data_ptr(),
@@ -561,9 +590,9 @@ class _VarlenFunction(torch.autograd.Function):
     @staticmethod
     def forward(
         ctx: Any, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
-        max_seqlen: int, causal: bool,
+        max_seqlen: int, causal: bool, zero_fill: bool,
     ) -> torch.Tensor:
-        output = torch.empty_like(q)
+        output = (torch.zeros_like if zero_fill else torch.empty_like)(q)
         softmax_lse = torch.empty((q.shape[1], q.shape[0]), dtype=torch.float32,
                                   device=q.device)
         _launch_varlen_forward(q, k, v, cu_seqlens, max_seqlen, output, softmax_lse,
@@ -571,6 +600,7 @@ class _VarlenFunction(torch.autograd.Function):
         ctx.save_for_backward(q, k, v, cu_seqlens, output, softmax_lse)
         ctx.max_seqlen = max_seqlen
         ctx.causal = causal
+        ctx.zero_fill = zero_fill
         return output
 
     @staticmethod
@@ -578,30 +608,42 @@ class _VarlenFunction(torch.autograd.Function):
     def backward(ctx: Any, do: torch.Tensor) -> tuple[Any, ...]:
         q, k, v, cu_seqlens, output, softmax_lse = ctx.saved_tensors
         dq, dk, dv = _launch_varlen_backward(q, k, v, cu_seqlens, ctx.max_seqlen, output,
-                                             softmax_lse, do, causal=ctx.causal)
-        return dq, dk, dv, None, None, None
+                                             softmax_lse, do, causal=ctx.causal,
+                                             zero_fill=ctx.zero_fill)
+        return dq, dk, dv, None, None, None, None
 
 
 def varlen_attention(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
-    max_seqlen: int, *, causal: bool,
+    max_seqlen: int, *, causal: bool, check_offsets: bool = True,
 ) -> torch.Tensor:
     """Attention over a variable-length batch packed along the token axis.
 
     ``q`` is ``(total, heads, head_dim)``, ``k`` and ``v`` ``(total, kv_heads,
     head_dim)`` (``heads % kv_heads == 0``); sequence ``b`` is tokens
     ``cu_seqlens[b]`` .. ``cu_seqlens[b + 1]`` (int32, on the device) and attends
-    only to itself; ``max_seqlen`` is the longest sequence. Each sequence gets
-    exactly the result :func:`grouped_query_attention` gives it alone, with
-    autograd (first order).
+    only to itself; ``max_seqlen`` is at least the longest sequence. Each sequence
+    gets exactly the result :func:`grouped_query_attention` gives it alone, with
+    autograd (first order). Token rows outside every sequence (``cu_seqlens[0] > 0``
+    or ``cu_seqlens[-1] < total``: a padded packing) get zero output and gradients.
+
+    With ``check_offsets`` (default) the offsets are copied to the host and checked
+    (start >= 0, non-decreasing, end <= total, no sequence longer than ``max_seqlen``;
+    ``ValueError`` otherwise), which synchronizes with the device. ``check_offsets=False``
+    skips the copy (no synchronization, e.g. under graph capture): outputs and gradients
+    are then zero-filled before the launch, and offsets that break the rules above give
+    unspecified values in the rows they cover (the kernels clamp every offset and length,
+    so no access leaves the tensors).
     """
     _validate_varlen(q, k, v, cu_seqlens, max_seqlen)
+    zero_fill = _check_offsets(cu_seqlens, q.shape[0], max_seqlen) if check_offsets else True
     needs_grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
     if not needs_grad:
-        output = torch.empty_like(q)
+        output = (torch.zeros_like if zero_fill else torch.empty_like)(q)
         _launch_varlen_forward(q, k, v, cu_seqlens, max_seqlen, output, None, causal=causal)
         return output
-    return cast(torch.Tensor, _VarlenFunction.apply(q, k, v, cu_seqlens, max_seqlen, causal))
+    return cast(torch.Tensor,
+                _VarlenFunction.apply(q, k, v, cu_seqlens, max_seqlen, causal, zero_fill))
 
 
 def _reference_factory(*, causal: bool) -> TensorFn:
@@ -647,9 +689,9 @@ def _flops_factory(*, causal: bool) -> CostFn:
 def _metadata_factory(*, causal: bool) -> BenchmarkMetadataFn:
     """Tile configuration and problem constants in the reference's keys."""
 
-    def metadata(_size: int, _dtype: torch.dtype) -> dict[str, BenchmarkScalar]:
+    def metadata(_size: int, dtype: torch.dtype) -> dict[str, BenchmarkScalar]:
         return {**FORWARD_TILE, "heads": _HEADS, "head_dim": _HEAD_DIM, "causal": causal,
-                "mma_opcode": "v_mfma_f32_32x32x16"}
+                "mma_opcode": FORWARD_MFMA.get(dtype, FORWARD_MFMA[torch.float16])}
 
     return metadata
 

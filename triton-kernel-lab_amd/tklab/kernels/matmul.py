@@ -6,9 +6,13 @@ int32 range, float16 (and here also bfloat16) inputs, a contiguous output of
 the input dtype. Validation order and messages follow ``matmul.py:167-186``.
 
 The reference autotunes 25 Triton configurations per shape
-(``matmul.py:23-75``); this build uses one MI355X tile (256 x 256 x 64, four
-wave64s, ``v_mfma_f32_32x32x16``) for every shape and reports it in the same
-metadata keys. ``matmul_fp16acc`` keeps its registry entry, but gfx950 MFMA
+(``matmul.py:23-75``); this build has a static choice between two kernels and
+reports the one a shape launches in the same metadata keys: row-major operands
+with K % 32 == 0 (every registry shape) take ``gemm_dma_kernel`` (256 x 256
+tiles, K step 32, eight wave64s, a 5-stage buffer->LDS ring,
+``v_mfma_f32_16x16x32``); strided operands or other K take the register-staged
+``gemm_kernel`` (256 x 256 x 64, four wave64s, ``v_mfma_f32_32x32x16``).
+``matmul_fp16acc`` keeps its registry entry, but gfx950 MFMA
 accumulates f16 products in float32 only, so both entry points run the same
 FP32-accumulate kernel (its result is at least as accurate as an FP16
 accumulation and meets the looser 5e-2 bound the reference sets for it).
@@ -32,12 +36,46 @@ from tklab.registry import (
 
 _DTYPES = (torch.float16, torch.bfloat16)
 
-# The single tile configuration of csrc/gemm.hip.
-TILE = {"block_m": 256, "block_n": 256, "block_k": 64, "group_m": 4, "num_warps": 4, "num_stages": 2}
+# csrc/gemm_dma.hip (BM, BN, BK, kGroupM, kThreads / 64 waves, kStages): row-major operands
+# with K % 32 == 0. "num_warps" counts wave64s.
+TILE = {"kernel": "gemm_dma_kernel", "block_m": 256, "block_n": 256, "block_k": 32, "group_m": 4,
+        "num_warps": 8, "num_stages": 5}
 _MFMA = {
+    torch.float16: "v_mfma_f32_16x16x32_f16",
+    torch.bfloat16: "v_mfma_f32_16x16x32_bf16",
+}
+# csrc/gemm.hip's register-staged kernel: every other operand layout (double-buffered in registers).
+FALLBACK_TILE = {"kernel": "gemm_kernel", "block_m": 256, "block_n": 256, "block_k": 64,
+                 "group_m": 4, "num_warps": 4, "num_stages": 2}
+_FALLBACK_MFMA = {
     torch.float16: "v_mfma_f32_32x32x16_f16",
     torch.bfloat16: "v_mfma_f32_32x32x16_bf16",
 }
+
+
+def launch_config(a: torch.Tensor, b: torch.Tensor) -> dict[str, BenchmarkScalar]:
+    """Tile configuration and MFMA of the kernel ``tk_gemm`` launches for ``a @ b``.
+
+    Mirrors ``gemm_dma_applies`` (csrc/gemm_dma.hip): unit column strides, K % 32 == 0,
+    N and both row strides multiples of 8, 16-byte aligned bases and operand extents
+    under 2 GiB take the DMA kernel.
+    """
+    (m, k), n = a.shape, b.shape[1]
+    dma = (
+        a.stride(1) == 1
+        and b.stride(1) == 1
+        and k % 32 == 0
+        and n % 8 == 0
+        and a.stride(0) % 8 == 0
+        and b.stride(0) % 8 == 0
+        and a.data_ptr() % 16 == 0
+        and b.data_ptr() % 16 == 0
+        and ((m - 1) * a.stride(0) + k) * 2 < 2**31
+        and ((k - 1) * b.stride(0) + n) * 2 < 2**31
+    )
+    if dma:
+        return {**TILE, "mma_opcode": _MFMA.get(a.dtype, _MFMA[torch.float16])}
+    return {**FALLBACK_TILE, "mma_opcode": _FALLBACK_MFMA.get(a.dtype, _FALLBACK_MFMA[torch.float16])}
 
 
 def _validate(a: torch.Tensor, b: torch.Tensor) -> None:
@@ -158,7 +196,9 @@ def _assert_fp16acc(output: torch.Tensor, reference: torch.Tensor) -> None:
 def _metadata_factory() -> BenchmarkMetadataFn:
     """Tile configuration in the reference's metadata keys (``matmul.py:292-312``)."""
 
-    def metadata(_size: int, dtype: torch.dtype) -> dict[str, BenchmarkScalar]:
+    def metadata(size: int, dtype: torch.dtype) -> dict[str, BenchmarkScalar]:
+        # Registry inputs are contiguous size x size matrices (size % 32 == 0).
+        del size
         return {**TILE, "mma_opcode": _MFMA.get(dtype, _MFMA[torch.float16])}
 
     return metadata
