@@ -58,10 +58,14 @@ __device__ __forceinline__ float round_to(float v) { return to_f32(from_f32<T>(v
 // sigmoid from exp(-|z|), branch-stable for any z
 // (src/tklab/kernels/_elementwise_math.py:12-18). Shared by the SwiGLU kernels and
 // the fused GEMM + SwiGLU epilogue so both evaluate it with the same instructions.
+// The exponential is the hardware one, exp2(-|z| * log2(e)) (v_exp_f32), and the quotient
+// a hardware reciprocal (v_rcp_f32, 1 ulp), the way Triton lowers the reference's tl.exp
+// and `/`: the libm-accurate expf plus an IEEE division took ~20 VALU instructions per
+// element, which made the SwiGLU forward (6 bytes of HBM traffic per element) VALU-bound.
 __device__ __forceinline__ float stable_sigmoid(float z) {
-  const float e = expf(-fabsf(z));
-  const float d = 1.0f + e;
-  return z >= 0.f ? 1.0f / d : e / d;
+  const float e = __builtin_amdgcn_exp2f(-fabsf(z) * 1.44269504088896341f);
+  const float r = __builtin_amdgcn_rcpf(1.0f + e);
+  return z >= 0.f ? r : e * r;
 }
 
 // ---------------------------------------------------------------- vector IO
