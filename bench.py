@@ -489,17 +489,19 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         row["reference_ms"] = round(ref_ms, 4)
         row["speedup"] = round(ref_ms / row["ms"], 3)
 
-    def mem_row(name, config, make, nbytes, reps=30, ref=None, ref_make=None):
+    def mem_row(name, config, make, nbytes, mix, reps=30, ref=None, ref_make=None):
         """`make(i)` returns the launch for tensor copy i (copy 0 may reuse the originals);
-        `ref_make(i)` the torch reference's call on the same copy."""
+        `ref_make(i)` the torch reference's call on the same copy. `mix` is the kernel's
+        read:write byte ratio, whose measured roof gives `frac_mix`."""
         if only and only not in name:
             return False
         ms = streamed(make, nbytes, reps)
         gbps = nbytes / ms / 1e6
         row = {"kernel": name, "config": config, "ms": round(ms, 4), "bytes": nbytes,
-               "GB/s": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4)}
+               "GB/s": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4), "mix": mix}
         if roofs:
             row["frac_measured"] = round(gbps / roofs["hbm_GBps"], 4)
+            row["frac_mix"] = round(gbps / roofs["stream_mixes_GBps"][mix], 4)
         add_reference(row, ref, None if ref_make is None else
                       (lambda: streamed(ref_make, nbytes, reps)))
         rows.append(row)
@@ -563,7 +565,7 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         yi = torch.empty_like(x)
         return lambda: sm._launch((xi,), yi)
 
-    mem_row("tk_softmax_fwd", "f32 4096x4096", softmax_copy, 2 * x.numel() * 4,
+    mem_row("tk_softmax_fwd", "f32 4096x4096", softmax_copy, 2 * x.numel() * 4, "1:1",
             ref="torch.softmax",
             ref_make=lambda i: (lambda xi: lambda: torch.softmax(xi, -1))(x if i == 0 else x.clone()))
     del x
@@ -576,7 +578,7 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         yi = torch.empty_like(xw)
         return lambda: sm._launch_online((xi,), yi)
 
-    mem_row("tk_softmax_online_fwd", "f32 64x1048576", online_copy, 2 * xw.numel() * 4,
+    mem_row("tk_softmax_online_fwd", "f32 64x1048576", online_copy, 2 * xw.numel() * 4, "2:1",
             ref="torch.softmax",
             ref_make=lambda i: (lambda xi: lambda: torch.softmax(xi, -1))(xw if i == 0 else xw.clone()))
     del xw
@@ -588,10 +590,10 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
     dv = torch.empty_like(gate)
     n = gate.numel()
     mem_row("tk_swiglu_fwd", "bf16 16384x14336",
-            lambda i: (lambda: sg._launch_forward(up, gate, out)), 3 * n * 2,
+            lambda i: (lambda: sg._launch_forward(up, gate, out)), 3 * n * 2, "2:1",
             ref="value * F.silu(gate)", ref_make=lambda i: (lambda: up * F.silu(gate)))
     mem_row("tk_swiglu_bwd", "bf16 16384x14336",
-            lambda i: (lambda: sg._launch_backward_into(dy, up, gate, dv, out)), 5 * n * 2,
+            lambda i: (lambda: sg._launch_backward_into(dy, up, gate, dv, out)), 5 * n * 2, "3:2",
             ref="autograd of value * F.silu(gate)",
             ref_make=lambda i: autograd_bwd(lambda v_, g_: v_ * F.silu(g_), (up, gate), dy, (0, 1)))
     del gate, up, dy, out, dv
@@ -610,11 +612,11 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         return lambda: rp._launch_forward(qi, ci, si, out)
 
     mem_row("tk_rope_fwd", "bf16 [4,32,4096,128]", lambda i: rope_copy(i, False),
-            3 * q.numel() * 2, ref="rotate-half (torch.cat of x1*c - x2*s, x2*c + x1*s)",
+            3 * q.numel() * 2, "2:1", ref="rotate-half (torch.cat of x1*c - x2*s, x2*c + x1*s)",
             ref_make=lambda i: (lambda a: lambda: rotate_half(*a))(
                 (q, cos, sin) if i == 0 else (q.clone(), cos.clone(), sin.clone())))
     mem_row("tk_rope_bwd", "bf16 [4,32,4096,128] dx only", lambda i: rope_copy(i, True),
-            3 * q.numel() * 2, ref="autograd of rotate-half, dx only",
+            3 * q.numel() * 2, "2:1", ref="autograd of rotate-half, dx only",
             ref_make=lambda i: autograd_bwd(
                 rotate_half, (q, cos, sin) if i == 0 else (q.clone(), cos.clone(), sin.clone()),
                 q, (0,)))
@@ -630,7 +632,7 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
     lsed = torch.empty(32, 32, device=device)
     mem_row("tk_gqa_decode", "bf16 B32 Hq32 Hkv8 L8192 D128",
             lambda i: (lambda: gd._launch(qd, kd, vd, None, od, lsed, scale=128 ** -0.5)),
-            2 * kd.numel() * 2 + 2 * qd.numel() * 2, ref="SDPA (enable_gqa)",
+            2 * kd.numel() * 2 + 2 * qd.numel() * 2, "1:0", ref="SDPA (enable_gqa)",
             ref_make=lambda i: sdpa_fwd(qd[:, :, None], kd, vd, False, gqa=True))
     del qd, kd, vd, od, lsed
     # Config 4: GEMM.
@@ -851,6 +853,11 @@ def main() -> int:
     line["measured_roofs"] = roofs
     roofline["measured_peak"] = roofs["hbm_GBps"]
     roofline["frac_measured"] = round(achieved / roofs["hbm_GBps"], 4)
+    # Stage 1 reads dy, s and the incoming sum gradient and writes dx: a 3:1 stream.
+    mix = {"tk_rmsnorm_bwd_stage1": "3:1", "tk_rmsnorm_fwd": "1:1"}.get(dominant)
+    if mix:
+        roofline["mix"] = mix
+        roofline["frac_mix"] = round(achieved / roofs["stream_mixes_GBps"][mix], 4)
     if not args.no_kernels:
         line["kernels"] = kernel_table(torch, device, roofs, args.only)
     if not args.no_cpu:

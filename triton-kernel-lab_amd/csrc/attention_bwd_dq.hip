@@ -8,7 +8,8 @@
 // key/value blocks of 64 (four 16-key tiles); all products are v_mfma_f32_16x16x32.
 // Per wave and key block j:
 //   S^T  = K Q^T     K rows as A operands (ds_read_b128), Q fragments in registers;
-//   dP^T = V dO^T    V rows as A operands, dO fragments in registers;
+//   dP^T = V dO^T    V rows as A operands, dO fragments in registers (head_dim 64: the
+//                    accumulators seeded with -delta, so they hold dP^T - delta);
 //   P = exp2(S^T c - lse), dS^T = P (dP^T - delta): lane l holds query 16 qt + l % 16, so
 //                    lse and delta are one value per lane and query tile;
 //   dQ^T += K^T dS^T K^T fragments read transposed (ds_read_b64_tr_b16) from the same K
@@ -48,6 +49,10 @@ template <int D>
 struct DqGeo {
   static constexpr int BM = 256, BN = 64, WAVES = 8, QW = 32;
   static constexpr int KS = D / 32;             // k-steps of S^T / dP^T
+  // dP^T accumulators seeded with -delta, one VALU subtraction per score fewer in the
+  // elementwise phase: head_dim 64 (VALU-bound, 180 registers); at head_dim 128 the kernel
+  // holds 256 registers and the seed's earlier-live accumulators spill.
+  static constexpr bool SEED = D == 64;
   static constexpr int FT = D / 16;             // 16-feature tiles of dQ^T
   static constexpr int FP = FT / 2;             // feature-tile pairs per 32-key step
   static constexpr int RB = D * 2;              // bytes per K/V row
@@ -109,7 +114,9 @@ __device__ __forceinline__ void read_t_unit(i32x4 (&tu)[DqGeo<D>::NT][2], uint32
 
 // The MFMA phase of one wave: dQ^T += K_{j-1}^T dS^T from the previous elementwise phase
 // (DO_DQ; its first PREFETCH units were issued by that phase), then S^T(j) = K_j Q^T and
-// dP^T(j) = V_j dO^T (DO_S). kb / tb: LDS addresses of block j's stage and block j-1's.
+// dP^T(j) = V_j dO^T (DO_S), with DqGeo::SEED starting from -delta of the lane's query
+// (nd), so the elementwise phase forms dS = P (dP - delta) with one multiply. kb / tb:
+// LDS addresses of block j's stage and block j-1's.
 template <typename T, int D, bool DO_S, bool DO_DQ>
 __device__ __forceinline__ void dq_mfma_phase(uint32_t kb, uint32_t tb,
                                               const uint32_t (&ka)[DqGeo<D>::KS],
@@ -118,6 +125,7 @@ __device__ __forceinline__ void dq_mfma_phase(uint32_t kb, uint32_t tb,
                                               const i32x4 (&qf)[2][DqGeo<D>::KS],
                                               const i32x4 (&of)[2][DqGeo<D>::KS],
                                               f32x4 (&st)[2][4], f32x4 (&dp)[2][4],
+                                              const float (&nd)[2],
                                               const i32x4 (&df)[2][2],
                                               f32x4 (&acc)[DqGeo<D>::FT][2],
                                               i32x4 (&tu)[DqGeo<D>::NT][2]) {
@@ -172,12 +180,15 @@ __device__ __forceinline__ void dq_mfma_phase(uint32_t kb, uint32_t tb,
                                        r == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[qt][kt]);
       } else {
         const int kk = r - KS;
+        // k-step 0 starts from -delta (SEED) or zero.
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-          for (int qt = 0; qt < 2; ++qt)
-            dp[qt][kt] = Mma16<T>::run(rf[r][kt], of[qt][kk],
-                                       kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : dp[qt][kt]);
+          for (int qt = 0; qt < 2; ++qt) {
+            const f32x4 c0 =
+                G::SEED ? f32x4{nd[qt], nd[qt], nd[qt], nd[qt]} : f32x4{0.f, 0.f, 0.f, 0.f};
+            dp[qt][kt] = Mma16<T>::run(rf[r][kt], of[qt][kk], kk == 0 ? c0 : dp[qt][kt]);
+          }
       }
     }
     if (u + DEPTH < NU) issue(u + DEPTH);
@@ -256,7 +267,8 @@ attn_bwd_dq_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T*
   // Q and dO fragments (B operands): query tile qt holds query wq0 + 16 qt + c, k-step kk
   // features 32 kk + 8 g .. +7; lse and delta of the same queries.
   i32x4 qf[2][KS], of[2][KS];
-  float lse_q[2], dl_q[2];
+  float lse_q[2];
+  float nd[2];  // -delta of the query: the dP^T accumulators' initial value
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
     const int query = wq0 + 16 * qt + c;
@@ -268,7 +280,7 @@ attn_bwd_dq_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T*
       of[qt][kk] = in ? *reinterpret_cast<const i32x4*>(dO + off) : i32x4{0, 0, 0, 0};
     }
     lse_q[qt] = in ? lse[stat + query] : 0.f;
-    dl_q[qt] = in ? delta[stat + query] : 0.f;
+    nd[qt] = in ? -delta[stat + query] : 0.f;
   }
 
   // Lane read addresses inside a stage: K / V row c of key tile kt (+16 kt rows), chunk
@@ -335,13 +347,14 @@ attn_bwd_dq_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T*
     }
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      const float nl = -lse_q[qt], dl = dl_q[qt];
+      const float nl = -lse_q[qt];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qt][kt][r], sl2, nl));
-          dp[qt][kt][r] = p * (dp[qt][kt][r] - dl);
+          // Seeded accumulators already hold dP - delta; nd is -delta.
+          dp[qt][kt][r] = G::SEED ? p * dp[qt][kt][r] : p * (dp[qt][kt][r] + nd[qt]);
         }
       df[qt][0] = acc_frag2<T>(dp[qt][0], dp[qt][1]);
       df[qt][1] = acc_frag2<T>(dp[qt][2], dp[qt][3]);
@@ -376,14 +389,14 @@ attn_bwd_dq_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T*
 
   const int n = CAUSAL ? min(kv_blocks, (wq0 + G::QW - 1) / BN + 1) : kv_blocks;
   if (grp) end_phase();
-  dq_mfma_phase<T, D, true, false>(kbase(0), 0, ka, va, ta, qf, of, st, dp, df, acc, tu);
+  dq_mfma_phase<T, D, true, false>(kbase(0), 0, ka, va, ta, qf, of, st, dp, nd, df, acc, tu);
   pin_mfma();
   end_phase();
   for (int j = 1; j < n; ++j) {
     dS_phase(j - 1);
     pin_dS(j - 1);
     end_phase();
-    dq_mfma_phase<T, D, true, true>(kbase(j), kbase(j - 1), ka, va, ta, qf, of, st, dp, df, acc,
+    dq_mfma_phase<T, D, true, true>(kbase(j), kbase(j - 1), ka, va, ta, qf, of, st, dp, nd, df, acc,
                                     tu);
     pin_mfma();
     end_phase();
@@ -391,7 +404,7 @@ attn_bwd_dq_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T*
   dS_phase(n - 1);
   pin_dS(n - 1);
   end_phase();
-  dq_mfma_phase<T, D, false, true>(0, kbase(n - 1), ka, va, ta, qf, of, st, dp, df, acc, tu);
+  dq_mfma_phase<T, D, false, true>(0, kbase(n - 1), ka, va, ta, qf, of, st, dp, nd, df, acc, tu);
   while (t < phases - 1) end_phase();
   wait_vmcnt<0>();
 
