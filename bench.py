@@ -489,10 +489,11 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         row["reference_ms"] = round(ref_ms, 4)
         row["speedup"] = round(ref_ms / row["ms"], 3)
 
-    def mem_row(name, config, make, nbytes, mix, reps=30, ref=None, ref_make=None):
+    def mem_row(name, config, make, nbytes, mix, reps=30, ref=None, ref_make=None, moved=1.0):
         """`make(i)` returns the launch for tensor copy i (copy 0 may reuse the originals);
         `ref_make(i)` the torch reference's call on the same copy. `mix` is the kernel's
-        read:write byte ratio, whose measured roof gives `frac_mix`."""
+        read:write byte ratio, whose measured roof gives `frac_mix` for the bytes the kernel
+        moves (`moved` times the algorithmic bytes)."""
         if only and only not in name:
             return False
         ms = streamed(make, nbytes, reps)
@@ -501,7 +502,9 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
                "GB/s": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4), "mix": mix}
         if roofs:
             row["frac_measured"] = round(gbps / roofs["hbm_GBps"], 4)
-            row["frac_mix"] = round(gbps / roofs["stream_mixes_GBps"][mix], 4)
+            row["frac_mix"] = round(moved * gbps / roofs["stream_mixes_GBps"][mix], 4)
+        if moved != 1.0:
+            row["moved_GB/s"] = round(moved * gbps, 1)
         add_reference(row, ref, None if ref_make is None else
                       (lambda: streamed(ref_make, nbytes, reps)))
         rows.append(row)
@@ -579,6 +582,7 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         return lambda: sm._launch_online((xi,), yi)
 
     mem_row("tk_softmax_online_fwd", "f32 64x1048576", online_copy, 2 * xw.numel() * 4, "2:1",
+            moved=1.5,
             ref="torch.softmax",
             ref_make=lambda i: (lambda xi: lambda: torch.softmax(xi, -1))(xw if i == 0 else xw.clone()))
     del xw
