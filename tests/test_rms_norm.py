@@ -122,9 +122,10 @@ def test_forward_and_backward_match_the_oracle(dtype: torch.dtype, cols: int) ->
 @pytest.mark.parametrize("rows", [1, 300, 1030, 1537])
 @pytest.mark.parametrize("dtype,cols", [(torch.bfloat16, 4096), (torch.float32, 1000)])
 def test_stage1_ragged_and_empty_groups(rows: int, dtype: torch.dtype, cols: int) -> None:
-    """512 groups over row counts that leave a short last group and trailing
-    groups owning no rows (ceil(1030/512)=3 rows per group covers 344 groups);
-    the bf16 4096-column case takes the pipelined three-row loop."""
+    """512 groups over row counts below, at and above the group count: groups own
+    the rows row % 512 == g, so 1030 rows give groups 0-5 three rows and the rest
+    two, and a single row leaves one active group; the bf16 4096-column case takes
+    the pipelined three-row loop."""
     torch.manual_seed(rows)
     x = torch.randn(rows, cols, device="cuda", dtype=dtype)
     w = (1 + 0.02 * torch.randn(cols, device="cuda")).to(dtype)

@@ -10,10 +10,11 @@
 // dweight = sum over rows of dy*x_hat.
 //
 // The reference accumulates dweight partials under a global spin lock in an
-// order that depends on scheduling. Here each workgroup is one group: it owns a
-// contiguous range of ceil(rows / group_count) rows, keeps its column partials in
-// registers (a thread always holds the same columns), folds its row slots together
-// in LDS in a fixed order and writes partial_dw[g] once. Stage 2 sums the partial
+// order that depends on scheduling. Here each workgroup is one group: it owns the
+// rows row % group_count == g (the reference's lock grouping, rms_norm.py:134) and
+// takes them in increasing order, keeps its column partials in registers (a thread
+// always holds the same columns), folds its row slots together in LDS in a fixed
+// order and writes partial_dw[g] once. Stage 2 sums the partial
 // rows in a fixed order. Both stages are bitwise reproducible.
 #include <atomic>
 
@@ -186,12 +187,12 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
   // addresses and buffer descriptors derived from it).
   const int slot = __builtin_amdgcn_readfirstlane(threadIdx.x / RT);
   const int lane = threadIdx.x % RT;
-  // Rows of this group: a contiguous range of rows_per_group rows (neighbouring groups
-  // stream neighbouring rows, which keeps HBM pages open); slot s takes the rows
-  // k = s mod SLOTS of the range.
-  const int rows_per_group = (rows + gridDim.x - 1) / gridDim.x;
-  const int group_first = group * rows_per_group;
-  const int group_rows = max(0, min(rows_per_group, rows - group_first));
+  // Rows of this group: row = group + k * G for k = 0, 1, ... (G = gridDim.x, the row % G
+  // grouping of the lock-based original), so at any time the groups stream a window of
+  // about G neighbouring rows of each tensor; slot s takes the rows k = s mod SLOTS.
+  const int G = gridDim.x;
+  const int group_rows = group < rows ? (rows - 1 - group) / G + 1 : 0;
+  auto row_of = [&](int k) { return static_cast<int64_t>(group) + static_cast<int64_t>(k) * G; };
 
   // dweight partials of this thread's columns, accumulated over its rows in order.
   float acc[ACC_LDS ? 1 : VALS];
@@ -208,10 +209,9 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
   Row wv;
   wv.load(weight, cols, lane);
   const RowPtrs<T> ptr{x, dy, incoming, dx, x_stride, dy_stride, inc_stride, dx_stride};
-  const int64_t first = group_first;
   if (group_rows == 0) {
-    // Trailing groups past the last row (rows not a multiple of the group count) own no
-    // rows; they only write a zero partial row. The pipeline below reads unconditionally.
+    // A group past the last row owns no rows (the entry points launch min(G, rows)
+    // groups, so none does); it would only write a zero partial row.
   } else if constexpr (RT < 1024 && VEC * sizeof(T) == 16) {
     // Software pipeline, unrolled by three so the three row buffers rotate roles
     // without register copies (a copy would wait for the load still in flight): the
@@ -221,21 +221,21 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
     // (the last row's address, zero extent), which returns zeros without memory traffic.
     RowSet<Row> ra, rb, rc;
     const int last = max(group_rows - 1, 0);
-    auto rowk = [&](int k) { return first + min(k, last); };
+    auto rowk = [&](int k) { return row_of(min(k, last)); };
     auto extent = [&](int k) { return k < group_rows ? cols : 0; };
     const int k0 = slot;
     load_rowset_buf<T>(ra, ptr, rowk(k0), extent(k0), lane, rstd);
     load_rowset_buf<T>(rb, ptr, rowk(k0 + SLOTS), extent(k0 + SLOTS), lane, rstd);
     for (int k = k0; k < group_rows; k += 3 * SLOTS) {
       load_rowset_buf<T>(rc, ptr, rowk(k + 2 * SLOTS), extent(k + 2 * SLOTS), lane, rstd);
-      stage1_row<T, VEC, RT, VALS, ACC_LDS>(ra, wv, ptr, first + k, cols, lane, acc, fold, scratch);
+      stage1_row<T, VEC, RT, VALS, ACC_LDS>(ra, wv, ptr, row_of(k), cols, lane, acc, fold, scratch);
       if (k + SLOTS >= group_rows) break;
       load_rowset_buf<T>(ra, ptr, rowk(k + 3 * SLOTS), extent(k + 3 * SLOTS), lane, rstd);
-      stage1_row<T, VEC, RT, VALS, ACC_LDS>(rb, wv, ptr, first + k + SLOTS, cols, lane, acc, fold,
+      stage1_row<T, VEC, RT, VALS, ACC_LDS>(rb, wv, ptr, row_of(k + SLOTS), cols, lane, acc, fold,
                                             scratch);
       if (k + 2 * SLOTS >= group_rows) break;
       load_rowset_buf<T>(rb, ptr, rowk(k + 4 * SLOTS), extent(k + 4 * SLOTS), lane, rstd);
-      stage1_row<T, VEC, RT, VALS, ACC_LDS>(rc, wv, ptr, first + k + 2 * SLOTS, cols, lane, acc,
+      stage1_row<T, VEC, RT, VALS, ACC_LDS>(rc, wv, ptr, row_of(k + 2 * SLOTS), cols, lane, acc,
                                             fold, scratch);
     }
   } else {
@@ -243,8 +243,8 @@ __global__ __launch_bounds__(bwd_block<RT>()) void rmsnorm_bwd_stage1_kernel(
     // one row at a time.
     RowSet<Row> ra;
     for (int k = slot; k < group_rows; k += SLOTS) {
-      load_rowset<T>(ra, ptr, first + k, cols, lane, rstd);
-      stage1_row<T, VEC, RT, VALS, ACC_LDS>(ra, wv, ptr, first + k, cols, lane, acc, fold, scratch);
+      load_rowset<T>(ra, ptr, row_of(k), cols, lane, rstd);
+      stage1_row<T, VEC, RT, VALS, ACC_LDS>(ra, wv, ptr, row_of(k), cols, lane, acc, fold, scratch);
     }
   }
 
@@ -375,9 +375,10 @@ extern "C" int tk_rmsnorm_bwd_stage1(int dtype, void* dx, const void* dy, const 
       {x_row_stride, dy_row_stride, incoming_dx ? incoming_dx_row_stride : 0, dx_row_stride});
   tk::RowShape shape;
   if (check_rows("rmsnorm_bwd_stage1", dtype, rows, cols, vector_ok, &shape)) return 1;
-  // Stage 1 holds three row tensors plus the dweight partials per thread: prefer at
-  // most 16 values per thread (more waves per row) so several workgroups fit per CU.
-  tk::pick_row_shape(cols, &shape, 16);
+  // Stage 1 holds three rows of three tensors plus the dweight partials per thread: at
+  // most 64 bytes of each row tensor per thread (32 packed 16-bit or 16 float32 values)
+  // keeps that in registers without spilling.
+  tk::pick_row_shape(cols, &shape, 64 / tk::elem_size(dtype));
   const dim3 grid(static_cast<unsigned>(group_count));
   hipStream_t s = tk::as_stream(stream);
   int32_t* counts = locks + group_size;
@@ -478,12 +479,12 @@ extern "C" int tk_rmsnorm_bwd_noalloc(int dtype, void* dx, void* dw, const void*
       {x_row_stride, dy_row_stride, incoming_dx ? incoming_dx_row_stride : 0, dx_row_stride});
   tk::RowShape shape;
   if (check_rows("rmsnorm_bwd_noalloc", dtype, rows, cols, vector_ok, &shape)) return 1;
-  tk::pick_row_shape(cols, &shape, 16);
+  tk::pick_row_shape(cols, &shape, 64 / tk::elem_size(dtype));
   hipStream_t s = tk::as_stream(stream);
   float* partial = nullptr;
   if (scratch_address("rmsnorm_bwd_noalloc", s, &partial)) return 1;
-  // Stage 1 writes every one of the group_count partial rows (zeros for a group that owns no
-  // row), so the array needs no clearing; stage 2 reads exactly those rows.
+  // Stage 1 writes every one of the group_count = min(group_size, rows) partial rows, so
+  // the array needs no clearing; stage 2 reads exactly those rows.
   TK_DISPATCH_DTYPE(dtype, T,
     TK_DISPATCH_VEC(T, vector_ok,
       TK_DISPATCH_ROW_SHAPE(shape,

@@ -25,10 +25,12 @@ EPS = 1e-5
 STAGE2_BLOCK_M = 32
 STAGE2_BLOCK_N = 32
 
-# Groups of the backward dweight reduction: one workgroup per group. 512 groups
-# keep two 4-wave workgroups per compute unit (256 CUs) streaming rows, while the
-# float32 partial buffer stays at 512 x columns.
-DEFAULT_GROUPS = 512
+# Groups of the backward dweight reduction: one workgroup per group, one group per
+# compute unit (256 CUs). Each streams its rows row % 256 == g with two rows of loads in
+# flight, so the 256 groups together walk each tensor through a window of about 256
+# neighbouring rows; on the 16384-row bf16 backward of 1024 to 8192 columns this ran
+# faster than 384, 512 or 1024 groups, and the float32 partial buffer is 256 x columns.
+DEFAULT_GROUPS = 256
 
 # The reference's norm backwards reduce dweight under a spin lock in a scheduling-dependent
 # order, so under ``torch.use_deterministic_algorithms(True)`` they raise ``RuntimeError`` (and
@@ -99,9 +101,9 @@ def group_size_m(columns: int) -> int:
     """Number of dweight partial groups for the backward stage 1.
 
     The reference trades lock contention against stage-two work
-    (``_norm_common.py:63-75``). Without locks the only concern is filling the
-    GPU while keeping the float32 partial buffer small, so every width uses two
-    groups per compute unit.
+    (``_norm_common.py:63-75``). Without locks the only concern is streaming the
+    rows at full bandwidth while keeping the float32 partial buffer small, so every
+    width uses one group per compute unit (``DEFAULT_GROUPS``).
     """
     del columns
     return DEFAULT_GROUPS

@@ -8,9 +8,10 @@ with the reference's validation order and messages (``rms_norm.py:176-204``).
 Backward. The reference reduces dweight partials under a global spin lock in
 a scheduling-dependent order and therefore refuses PyTorch's deterministic
 mode (``rms_norm.py:370-378``). Here each of ``min(group_size, rows)``
-workgroups owns one contiguous range of ``ceil(rows / groups)`` rows, writes
-one float32 partial row with a plain store (zero for a group past the last row), and stage 2
-sums the partial rows in a fixed order. The result is bitwise reproducible. Under deterministic
+workgroups is one group and owns the rows ``row % group_size == g`` (the reference's
+lock grouping, ``rms_norm.py:134``), accumulates them in increasing row order, writes
+one float32 partial row with a plain store, and stage 2 sums the partial rows in a
+fixed order. The result is bitwise reproducible. Under deterministic
 mode ``_launch_backward`` still raises (or warns) as the reference does, unless
 ``_norm_common.REJECT_DETERMINISTIC_MODE`` is set to False.
 ``_BackwardBuffers.locks`` keeps its reference layout (``locks || counts``):
