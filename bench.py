@@ -9,7 +9,9 @@ gradient) and tk_rmsnorm_bwd_stage2. Algorithmic bytes per step:
 forward 4*M*D*2 + backward 4*M*D*2 = 1 073 741 824 (weight, rstd and the
 float32 partial rows are not counted).
 
-``value`` is that step's throughput in GB/s with inputs resident in HBM.
+``value`` is that step's throughput in GB/s with inputs resident in HBM; the steps
+rotate over three independent tensor sets (STEP_SETS), so no step finds its tensors
+in the last-level cache from the step before.
 ``roofline`` prices the dominant kernel of the step against 8 TB/s: its
 algorithmic bytes per launch over its average duration, measured with events
 on the launch stream around that kernel inside the timed region (an untimed
@@ -25,7 +27,8 @@ rotate over enough copies of their tensors to touch at least 1 GiB (four times
 the 256 MiB last-level cache), so they measure steady HBM streaming without
 cache reuse; MFMA rows flush 1 GiB before each launch.
 ``measured_roofs`` holds the ceilings this GPU sustains (the library's copy and
-dense-MFMA calibration kernels); every row and ``roofline`` also carry
+dense-MFMA calibration kernels, the HBM read:write mixes with the better of two store
+policies); every row and ``roofline`` also carry
 ``frac_measured`` against them, beside ``frac`` against the published peaks.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu] [--only TEXT]
@@ -79,15 +82,17 @@ def _traffic_from_summary() -> float | None:
     return float(m.group(1)) if m else None
 
 
-class Step:
-    """Preallocated buffers and the three launches of one residual-RMSNorm fwd+bwd step."""
+# Independent input/output sets the steps rotate over: step i uses set i % STEP_SETS, so
+# no step finds its tensors in the 256 MiB last-level cache from the step before (one set
+# of seven 128 MiB tensors is only 3.5 times that cache; a single reused set ran the step
+# ~5 % faster).
+STEP_SETS = 3
 
-    def __init__(self, torch, device) -> None:
-        from tklab.kernels import residual_rms_norm as rrn
-        from tklab.kernels import rms_norm as rn
 
-        self.rrn, self.rn = rrn, rn
-        g = torch.Generator(device=device).manual_seed(0)
+class StepSet:
+    """One set of the step's preallocated tensors (set 0 is seeded like the CPU baseline)."""
+
+    def __init__(self, torch, device, rn, g) -> None:
         bf16 = torch.bfloat16
         self.x = torch.randn(ROWS, COLS, device=device, dtype=bf16, generator=g)
         self.r = torch.randn(ROWS, COLS, device=device, dtype=bf16, generator=g)
@@ -99,14 +104,29 @@ class Step:
         self.rstd = torch.empty(ROWS, device=device, dtype=torch.float32)
         self.buffers = rn._make_backward_buffers(self.s, self.w)
 
-    def launches(self):
-        b = self.buffers
+
+class Step:
+    """Preallocated buffers and the three launches of one residual-RMSNorm fwd+bwd step,
+    over STEP_SETS independent tensor sets."""
+
+    def __init__(self, torch, device, sets: int = STEP_SETS) -> None:
+        from tklab.kernels import residual_rms_norm as rrn
+        from tklab.kernels import rms_norm as rn
+
+        self.rrn, self.rn = rrn, rn
+        g = torch.Generator(device=device).manual_seed(0)
+        self.sets = [StepSet(torch, device, rn, g) for _ in range(sets)]
+
+    def launches(self, i: int = 0):
+        """The launches of step i (tensor set i % STEP_SETS)."""
+        t = self.sets[i % len(self.sets)]
+        b = t.buffers
         return (
             ("tk_rmsnorm_fwd", lambda: self.rrn._launch_forward(
-                self.x, self.r, self.w, self.s, self.y, self.rstd,
+                t.x, t.r, t.w, t.s, t.y, t.rstd,
                 eps=EPS, store_residual=True, store_stats=True)),
             ("tk_rmsnorm_bwd_stage1", lambda: self.rn._launch_backward_stage1(
-                self.dout, self.s, self.w, self.rstd, b, incoming_dx=self.dsum)),
+                t.dout, t.s, t.w, t.rstd, b, incoming_dx=t.dsum)),
             ("tk_rmsnorm_bwd_stage2", lambda: self.rn._launch_backward_stage2(b, COLS)),
         )
 
@@ -129,17 +149,18 @@ def time_step(torch, step: Step, steps: int, warmup: int) -> tuple[float, str, f
     Returns (ms per timed step, dominant kernel, its mean ms inside the timed region,
     attribution-pass ms per kernel).
     """
-    launches = step.launches()
+    plans = [step.launches(i) for i in range(len(step.sets))]
+    launches = plans[0]
     stream = torch.cuda.current_stream()
-    for _ in range(warmup):
-        for _, fn in launches:
+    for i in range(warmup):
+        for _, fn in plans[i % len(plans)]:
             fn()
     torch.cuda.synchronize()
     probe = 20
     pairs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in launches] for _ in range(probe)]
     for i in range(probe):
-        for j, (_, fn) in enumerate(launches):
+        for j, (_, fn) in enumerate(plans[i % len(plans)]):
             pairs[i][j][0].record(stream)
             fn()
             pairs[i][j][1].record(stream)
@@ -158,7 +179,7 @@ def time_step(torch, step: Step, steps: int, warmup: int) -> tuple[float, str, f
     t0 = time.perf_counter()
     start.record(stream)
     for i in range(steps):
-        for j, (_, fn) in enumerate(launches):
+        for j, (_, fn) in enumerate(plans[i % len(plans)]):
             if j == dom:
                 events[i][0].record(stream)
             fn()
@@ -205,24 +226,27 @@ def _cpu_facts() -> dict:
 def torch_gpu_step_ms(torch, step: Step, steps: int) -> float:
     """The reference's PyTorch path for the step on the GPU in the step's dtype: x + r,
     F.rms_norm and torch.autograd.grad of both outputs (what the reference's benchmark
-    times beside its kernels). Mean ms per step over `steps` after 3 warmups."""
+    times beside its kernels), rotating over the step's tensor sets like the timed steps.
+    Mean ms per step over `steps` after 3 warmups."""
     import torch.nn.functional as F
 
-    leaves = [t.detach().requires_grad_(True) for t in (step.x, step.r, step.w)]
+    sets = [([t.x.detach().requires_grad_(True), t.r.detach().requires_grad_(True),
+              t.w.detach().requires_grad_(True)], (t.dsum, t.dout)) for t in step.sets]
 
-    def once():
+    def once(i):
+        leaves, grads = sets[i % len(sets)]
         s_ = leaves[0] + leaves[1]
         y_ = F.rms_norm(s_, (COLS,), leaves[2], EPS)
-        return torch.autograd.grad((s_, y_), leaves, (step.dsum, step.dout))
+        return torch.autograd.grad((s_, y_), leaves, grads)
 
-    for _ in range(3):
-        once()
+    for i in range(3):
+        once(i)
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     a.record()
-    for _ in range(steps):
-        once()
+    for i in range(steps):
+        once(i)
     b.record()
     torch.cuda.synchronize()
     return a.elapsed_time(b) / steps
@@ -364,23 +388,48 @@ def measured_roofs(torch, device) -> dict:
     if not torch.equal(src, dst):
         raise RuntimeError("tk_roof_copy produced a wrong copy")
     del src, dst
-    # Read:write mixes of the same access shape, 512 MiB per array.
-    part = 1 << 29
-    srcs = torch.randint(-2**31, 2**31 - 1, (3 * part // 4,), dtype=torch.int32, device=device)
-    dsts = torch.empty(2 * part // 4, dtype=torch.int32, device=device)
+    # Read:write mixes, each the best of two layouts (128 MiB per array, the step's tensor
+    # size, rotating over three independent sets like the step; 512 MiB per array, one set)
+    # and eight access variants: 32 or 64 KiB tiles, one workgroup per tile or 8192
+    # workgroups walking them grid-stride, non-temporal or sc1 stores.
+    big = 1 << 29
+    srcs = torch.randint(-2**31, 2**31 - 1, (3 * big // 4,), dtype=torch.int32, device=device)
+    dsts = torch.empty(2 * big // 4, dtype=torch.int32, device=device)
     mixes: dict[str, float] = {}
-    for reads, writes in ((1, 0), (0, 1), (1, 1), (2, 1), (3, 1), (3, 2)):
-        ms = copy_ms(lambda: _hip.call("tk_roof_stream", srcs.data_ptr(), dsts.data_ptr(), part,
-                                       reads, writes, stream))
-        mixes[f"{reads}:{writes}"] = round((reads + writes) * part / ms / 1e6, 1)
-    chunks = part // 16
-    want = srcs.view(3, chunks, 4)
+    policies: dict[str, str] = {}
+    small = 1 << 27
+    chunks = small // 16
+    want = srcs[:3 * small // 4].view(3, chunks, 4)
     want = want[0] ^ want[1] ^ want[2]
     want[:, 0] ^= torch.arange(chunks, device=device, dtype=torch.int32)
-    got = dsts.view(2, chunks, 4)
-    if not (torch.equal(got[0], want) and torch.equal(got[1], want)):
-        raise RuntimeError("tk_roof_stream (3:2) produced wrong data")
-    del srcs, dsts, want, got
+    for reads, writes in ((1, 0), (0, 1), (1, 1), (2, 1), (3, 1), (2, 2), (3, 2)):
+        key = f"{reads}:{writes}"
+        for (part, nsets), policy, tile, grid in itertools.product(
+                ((small, 3), (big, 1)), (0, 1), (32, 64), (0, 8192)):
+            if writes == 0 and policy == 1:
+                continue  # the store policy does not apply to a read-only stream
+            turn = itertools.count()
+
+            def launch(reads=reads, writes=writes, policy=policy, tile=tile, grid=grid,
+                       part=part, nsets=nsets, turn=turn):
+                k = next(turn) % nsets
+                _hip.call("tk_roof_stream", srcs.data_ptr() + k * 3 * part,
+                          dsts.data_ptr() + k * 2 * part, part, reads, writes, policy, tile,
+                          grid, stream)
+
+            ms = copy_ms(launch, reps=30)
+            gbps = round((reads + writes) * part / ms / 1e6, 1)
+            if gbps > mixes.get(key, 0.0):
+                mixes[key] = gbps
+                policies[key] = (f"{part >> 20} MiB x {nsets}, {tile} KiB tiles, "
+                                 f"{'grid-stride' if grid else 'one per workgroup'}, "
+                                 + (f"{('nt', 'sc1')[policy]} stores" if writes else "no stores"))
+            if (reads, writes) == (3, 2) and part == small:
+                got = dsts[:2 * small // 4].view(2, chunks, 4)
+                if not (torch.equal(got[0], want) and torch.equal(got[1], want)):
+                    raise RuntimeError("tk_roof_stream (3:2) produced wrong data")
+                dsts.zero_()
+    del srcs, dsts, want
     flush = torch.empty(1 << 28, dtype=torch.float32, device=device)
     waves = 8192
     out = torch.empty(waves, dtype=torch.float32, device=device)
@@ -414,6 +463,7 @@ def measured_roofs(torch, device) -> dict:
         "copy_GBps": round(copy, 1),
         "copy_kernels_GBps": {"tk_roof_copy": round(own, 1), "torch copy_": round(ref, 1)},
         "stream_mixes_GBps": mixes,
+        "stream_mix_variant": policies,
         "mfma_TFLOPs": mfma,
         "note": "measured on this GPU by bench.py; frac_measured divides by hbm_GBps, the best "
                 "of the copy and the tk_roof_stream read:write mixes (HBM rows), or by the MFMA "
@@ -858,7 +908,7 @@ def main() -> int:
     roofline["measured_peak"] = roofs["hbm_GBps"]
     roofline["frac_measured"] = round(achieved / roofs["hbm_GBps"], 4)
     # Stage 1 reads dy, s and the incoming sum gradient and writes dx: a 3:1 stream.
-    mix = {"tk_rmsnorm_bwd_stage1": "3:1", "tk_rmsnorm_fwd": "1:1"}.get(dominant)
+    mix = {"tk_rmsnorm_bwd_stage1": "3:1", "tk_rmsnorm_fwd": "2:2"}.get(dominant)
     if mix:
         roofline["mix"] = mix
         roofline["frac_mix"] = round(achieved / roofs["stream_mixes_GBps"][mix], 4)

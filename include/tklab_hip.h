@@ -378,12 +378,15 @@ int tk_gqa_decode(int dtype, const void* q, const void* k, const void* v, void* 
  * 16-byte non-temporal accesses, four loads in flight per thread: the streaming roof. */
 int tk_roof_copy(const void* src, void* dst, int64_t bytes, void* stream);
 
-/* The copy's access shape with `reads` source arrays and `writes` destination arrays of
- * `bytes` each (src holds reads * bytes, dst writes * bytes, at least `bytes` when writes is
- * 0); each written 16-byte chunk is the xor of the chunks read at its position. Mixes
- * (reads:writes) 1:0, 0:1, 1:1, 2:1, 3:1 and 3:2. HBM traffic: (reads + writes) * bytes. */
+/* `reads` source arrays and `writes` destination arrays of `bytes` each (src holds
+ * reads * bytes, dst writes * bytes, at least `bytes` when writes is 0), cut into tiles of
+ * `tile_kib` (32 or 64) KiB per array: one workgroup per tile (max_workgroups 0) or at most
+ * max_workgroups workgroups walking the tiles grid-stride. 16-byte non-temporal loads,
+ * stores non-temporal (store_policy 0) or sc1 (1); each written 16-byte chunk i is
+ * {i, 0, 0, 0} xor the chunks read at its position. Mixes (reads:writes) 1:0, 0:1, 1:1, 2:1,
+ * 3:1, 2:2 and 3:2. HBM traffic: (reads + writes) * bytes. */
 int tk_roof_stream(const void* src, void* dst, int64_t bytes, int reads, int writes,
-                   void* stream);
+                   int store_policy, int tile_kib, int64_t max_workgroups, void* stream);
 
 /* Dense MFMA issue with no memory traffic: `waves` waves (a multiple of 4) each
  * run `iters` (a multiple of 8) iterations of 16 independent v_mfma_f32_16x16x32

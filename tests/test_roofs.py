@@ -49,3 +49,45 @@ def test_roof_arguments_are_checked() -> None:
         _hip.call("tk_roof_mfma", 1, out.data_ptr(), 8, 12, _stream())
     with pytest.raises(_hip.HipLibraryError, match="dtype"):
         _hip.call("tk_roof_mfma", 0, out.data_ptr(), 8, 8, _stream())
+
+
+@pytest.mark.parametrize("reads,writes", [(1, 0), (0, 1), (1, 1), (2, 1), (3, 1), (2, 2), (3, 2)])
+@pytest.mark.parametrize("policy,tile,grid", [(0, 64, 0), (1, 32, 0), (0, 32, 3)])
+@pytest.mark.parametrize("nbytes", [65536 * 16, 65536 * 3 + 4096 + 48])
+def test_roof_stream_writes_the_xor_of_its_reads(reads: int, writes: int, policy: int, tile: int,
+                                                 grid: int, nbytes: int) -> None:
+    """Written chunk i is {i, 0, 0, 0} xor the chunks read at position i, for whole and
+    partial tiles, one workgroup per tile or a 3-workgroup grid-stride walk; nothing past
+    `bytes` of any destination array is written."""
+    g = torch.Generator(device="cuda").manual_seed(reads * 10 + writes)
+    chunks = nbytes // 16
+    src = torch.randint(-(2**31), 2**31 - 1, (max(reads, 1) * chunks * 4,), device="cuda",
+                        dtype=torch.int32, generator=g)
+    dst = torch.full((max(writes, 1) * chunks * 4 + 64,), -1, device="cuda", dtype=torch.int32)
+    _hip.call("tk_roof_stream", src.data_ptr(), dst.data_ptr(), nbytes, reads, writes, policy,
+              tile, grid, _stream())
+    torch.cuda.synchronize()
+    want = torch.zeros(chunks, 4, device="cuda", dtype=torch.int32)
+    want[:, 0] = torch.arange(chunks, device="cuda", dtype=torch.int32)
+    for r in range(reads):
+        want ^= src[r * chunks * 4:(r + 1) * chunks * 4].view(chunks, 4)
+    for w in range(writes):
+        assert torch.equal(dst[w * chunks * 4:(w + 1) * chunks * 4].view(chunks, 4), want)
+    if writes == 0:
+        assert bool((dst == -1).all())  # the sink store never fires on this data
+    else:
+        assert bool((dst[writes * chunks * 4:] == -1).all())
+
+
+def test_roof_stream_arguments_are_checked() -> None:
+    out = torch.empty(1 << 16, device="cuda")
+    with pytest.raises(_hip.HipLibraryError, match="store_policy"):
+        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 4096, 1, 1, 2, 64, 0, _stream())
+    with pytest.raises(_hip.HipLibraryError, match="tile_kib"):
+        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 4096, 1, 1, 0, 16, 0, _stream())
+    with pytest.raises(_hip.HipLibraryError, match="max_workgroups"):
+        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 4096, 1, 1, 0, 64, -1, _stream())
+    with pytest.raises(_hip.HipLibraryError, match="unsupported mix"):
+        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 4096, 1, 2, 0, 64, 0, _stream())
+    with pytest.raises(_hip.HipLibraryError, match="read-only run"):
+        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 16, 1, 0, 0, 64, 0, _stream())

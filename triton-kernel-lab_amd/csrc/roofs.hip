@@ -5,10 +5,11 @@
 //                   non-temporal accesses, each thread issuing the loads of kUnroll
 //                   chunks of a contiguous 4 KiB-per-wave run before its stores (the
 //                   access shape and cache policy of the elementwise kernels).
-//   tk_roof_stream — the same access shape with R reads and W writes per chunk position
-//                   (R:W of 1:0, 0:1, 1:1, 2:1, 3:1, 3:2): the HBM roof is the best of
-//                   these mixes, since reads and writes turn the HBM bus around
-//                   differently and the kernels here run several mixes.
+//   tk_roof_stream — R reads and W writes per chunk position (R:W of 1:0, 0:1, 1:1, 2:1,
+//                   3:1, 2:2, 3:2), one 32 or 64 KiB tile of every array per workgroup,
+//                   stores non-temporal or sc1: the HBM roof is the best of these mixes, since
+//                   reads and writes turn the HBM bus around differently and the kernels
+//                   here run several mixes.
 //   tk_roof_mfma  — dense v_mfma_f32_16x16x32_{f16,bf16} issue with no memory
 //                   traffic: each wave keeps 2 * kChains independent 16x16 float32
 //                   accumulators so back-to-back MFMAs never wait on one
@@ -57,39 +58,50 @@ __global__ __launch_bounds__(kCopyBlock) void roof_copy_kernel(const i32x4* __re
 }
 
 // R arrays of `chunks` 16-byte chunks read, W arrays written; written chunk i is
-// {i, 0, 0, 0} xor the chunks read at position i. With W == 0
+// {i, 0, 0, 0} xor the chunks read at position i. The arrays are cut into tiles of 256 * U
+// chunks (16 U KiB per array); workgroup b takes tiles b, b + G, ... (G = gridDim.x: one
+// tile per workgroup when the grid covers the arrays, else a grid-stride walk), read with
+// non-temporal buffer loads and written with cache policy CPOL; the buffer extent ends at the array's
+// end, so a partial last tile loads zeros past it and drops those stores. With W == 0
 // the xor of everything a thread read is stored only when it equals `sentinel`, which
 // never happens for the calibration data but keeps every load live.
-template <int R, int W>
+template <int R, int W, int CPOL, int U>
 __global__ __launch_bounds__(kCopyBlock) void roof_stream_kernel(const i32x4* __restrict__ src,
                                                                  i32x4* __restrict__ dst,
                                                                  int64_t chunks, int sentinel) {
-  constexpr int64_t kPass = int64_t(kCopyBlock) * kCopyUnroll;
+  constexpr int64_t kTile = int64_t(kCopyBlock) * U;
   i32x4 sink = i32x4{0, 0, 0, 0};
-  for (int64_t base = int64_t(blockIdx.x) * kPass; base < chunks;
-       base += int64_t(gridDim.x) * kPass) {
-    const int64_t i0 = base + threadIdx.x;
-    i32x4 v[kCopyUnroll];
+  for (int64_t base = int64_t(blockIdx.x) * kTile; base < chunks;
+       base += int64_t(gridDim.x) * kTile) {
+    const int64_t left = chunks - base;
+    const uint32_t extent = uint32_t((left < kTile ? left : kTile) * 16);
+    i32x4 v[U];
 #pragma unroll
-    for (int u = 0; u < kCopyUnroll; ++u) v[u] = i32x4{int(i0 + int64_t(u) * kCopyBlock), 0, 0, 0};
+    for (int u = 0; u < U; ++u)
+      v[u] = i32x4{int(base + u * kCopyBlock + threadIdx.x), 0, 0, 0};
 #pragma unroll
-    for (int r = 0; r < R; ++r)
+    for (int r = 0; r < R; ++r) {
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<i32x4*>(src + int64_t(r) * chunks + base), (short)0, extent, 0x00020000);
 #pragma unroll
-      for (int u = 0; u < kCopyUnroll; ++u) {
-        const int64_t i = i0 + int64_t(u) * kCopyBlock;
-        if (i < chunks) v[u] ^= __builtin_nontemporal_load(src + int64_t(r) * chunks + i);
-      }
+      for (int u = 0; u < U; ++u)
+        v[u] ^= __builtin_bit_cast(
+            i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rs, uint32_t((u * kCopyBlock + threadIdx.x) * 16), 0, 2));
+    }
     if constexpr (W == 0) {
 #pragma unroll
-      for (int u = 0; u < kCopyUnroll; ++u) sink ^= v[u];
+      for (int u = 0; u < U; ++u) sink ^= v[u];
     } else {
 #pragma unroll
-      for (int w = 0; w < W; ++w)
+      for (int w = 0; w < W; ++w) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            dst + int64_t(w) * chunks + base, (short)0, extent, 0x00020000);
 #pragma unroll
-        for (int u = 0; u < kCopyUnroll; ++u) {
-          const int64_t i = i0 + int64_t(u) * kCopyBlock;
-          if (i < chunks) __builtin_nontemporal_store(v[u], dst + int64_t(w) * chunks + i);
-        }
+        for (int u = 0; u < U; ++u)
+          __builtin_amdgcn_raw_buffer_store_b128(
+              v[u], rs, uint32_t((u * kCopyBlock + threadIdx.x) * 16), 0, CPOL);
+      }
     }
   }
   if constexpr (W == 0) {
@@ -181,15 +193,24 @@ extern "C" int tk_roof_copy(const void* src, void* dst, int64_t bytes, void* str
 }
 
 extern "C" int tk_roof_stream(const void* src, void* dst, int64_t bytes, int reads, int writes,
+                              int store_policy, int tile_kib, int64_t max_workgroups,
                               void* stream) {
   if (bytes <= 0 || bytes % 16 != 0)
     return tk::fail("tk_roof_stream: bytes must be a positive multiple of 16 (got %lld)",
                     static_cast<long long>(bytes));
   if (src == nullptr || dst == nullptr || !tk::aligned16(src) || !tk::aligned16(dst))
     return tk::fail("tk_roof_stream: src and dst must be non-null and 16-byte aligned");
+  if (store_policy != 0 && store_policy != 1)
+    return tk::fail("tk_roof_stream: store_policy must be 0 (non-temporal) or 1 (sc1), got %d",
+                    store_policy);
+  if (tile_kib != 32 && tile_kib != 64)
+    return tk::fail("tk_roof_stream: tile_kib must be 32 or 64, got %d", tile_kib);
   const int64_t chunks = bytes / 16;
-  int64_t blocks = tk::cdiv(chunks, int64_t(kCopyBlock) * kCopyUnroll);
-  if (blocks > kCopyMaxBlocks) blocks = kCopyMaxBlocks;
+  if (max_workgroups < 0 || max_workgroups > INT32_MAX)
+    return tk::fail("tk_roof_stream: max_workgroups must be 0 (one per tile) or positive");
+  int64_t blocks = tk::cdiv(chunks, int64_t(kCopyBlock) * (tile_kib / 16));
+  if (max_workgroups > 0 && blocks > max_workgroups) blocks = max_workgroups;
+  if (blocks > INT32_MAX) return tk::fail("tk_roof_stream: too many bytes");
   // With no writes the sink store may touch one chunk per thread of the grid.
   if (writes == 0 && blocks * kCopyBlock > chunks)
     return tk::fail("tk_roof_stream: a read-only run needs at least %lld bytes",
@@ -199,10 +220,18 @@ extern "C" int tk_roof_stream(const void* src, void* dst, int64_t bytes, int rea
   const i32x4* in = static_cast<const i32x4*>(src);
   i32x4* out = static_cast<i32x4*>(dst);
   const int sentinel = 0x5A5A5A5A;
+#define TK_ROOF_STREAM_LAUNCH(R, W, CPOL, U)                                                    \
+  hipLaunchKernelGGL((roof_stream_kernel<R, W, CPOL, U>), grid, dim3(kCopyBlock), 0, s, in, out, \
+                     chunks, sentinel)
 #define TK_ROOF_STREAM(R, W)                                                                    \
   if (reads == R && writes == W) {                                                              \
-    hipLaunchKernelGGL((roof_stream_kernel<R, W>), grid, dim3(kCopyBlock), 0, s, in, out,       \
-                       chunks, sentinel);                                                       \
+    if (tile_kib == 64) {                                                                       \
+      if (store_policy == 0) TK_ROOF_STREAM_LAUNCH(R, W, 2, 4);                                 \
+      else TK_ROOF_STREAM_LAUNCH(R, W, 16, 4);                                                  \
+    } else {                                                                                    \
+      if (store_policy == 0) TK_ROOF_STREAM_LAUNCH(R, W, 2, 2);                                 \
+      else TK_ROOF_STREAM_LAUNCH(R, W, 16, 2);                                                  \
+    }                                                                                           \
     return tk::check_launch("tk_roof_stream");                                                 \
   }
   TK_ROOF_STREAM(1, 0)
@@ -210,8 +239,10 @@ extern "C" int tk_roof_stream(const void* src, void* dst, int64_t bytes, int rea
   TK_ROOF_STREAM(1, 1)
   TK_ROOF_STREAM(2, 1)
   TK_ROOF_STREAM(3, 1)
+  TK_ROOF_STREAM(2, 2)
   TK_ROOF_STREAM(3, 2)
 #undef TK_ROOF_STREAM
+#undef TK_ROOF_STREAM_LAUNCH
   return tk::fail("tk_roof_stream: unsupported mix %d reads : %d writes", reads, writes);
 }
 

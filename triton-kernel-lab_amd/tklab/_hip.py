@@ -105,7 +105,7 @@ _SIGNATURES: dict[str, list[object]] = {
         _I64P, _F32, _P,
     ],
     "tk_roof_copy": [_P, _P, _I64, _P],
-    "tk_roof_stream": [_P, _P, _I64, _I32, _I32, _P],
+    "tk_roof_stream": [_P, _P, _I64, _I32, _I32, _I32, _I32, _I64, _P],
     "tk_roof_mfma": [_I32, _P, _I64, _I64, _P],
 }
 
