@@ -35,6 +35,10 @@ __global__ __launch_bounds__(RT >= 256 ? RT : 256) void softmax_fwd_kernel(
   for (int e = 1; e < VALS; ++e) m = fmaxf(m, v[e]);
   m = tk::group_allreduce<RT>(m, tk::MaxOp{}, scratch);
 
+  // libm's expf, not the bare hardware exponential (tk::hw_exp, four times fewer VALU
+  // instructions): this kernel is HBM-bound and, measured on f32 4096 x 4096, ran 22.5-23.9 us
+  // with expf and 25.6-25.9 us with hw_exp (also with every load issued up front, or in two or
+  // four phases).
   float s = 0.f;
 #pragma unroll
   for (int e = 0; e < VALS; ++e) {
@@ -60,7 +64,8 @@ __global__ __launch_bounds__(RT >= 256 ? RT : 256) void softmax_fwd_kernel(
 //            order by every workgroup of the row; then y = exp(x - M) * (1 / S)
 //            (a second read of the chunk, one write).
 // HBM traffic is two reads and one write per element; the workspace holds two
-// floats per chunk.
+// floats per chunk. The exponentials are tk::hw_exp (the hardware exp2 of x log2(e)):
+// with libm's expf the two passes over f32 64 x 1048576 took 0.135 ms, with hw_exp 0.126 ms.
 
 constexpr int kOnlineThreads = 256;
 constexpr int kOnlineVals = 64;
@@ -94,7 +99,7 @@ __global__ __launch_bounds__(kOnlineThreads) void softmax_online_partial_kernel(
   float s = 0.f;
   if (m != -INFINITY) {
 #pragma unroll
-    for (int e = 0; e < kOnlineVals; ++e) s += expf(v[e] - m);
+    for (int e = 0; e < kOnlineVals; ++e) s += tk::hw_exp(v[e] - m);
   }
   s = tk::group_allreduce<kOnlineThreads>(s, tk::SumOp{}, scratch);
   if (threadIdx.x == 0) {
@@ -124,12 +129,12 @@ __global__ __launch_bounds__(kOnlineThreads) void softmax_online_apply_kernel(
   float s = 0.f;
   for (int j = threadIdx.x; j < chunks; j += kOnlineThreads) {
     const float mj = pr[2 * j];
-    if (mj != -INFINITY) s += pr[2 * j + 1] * expf(mj - m);
+    if (mj != -INFINITY) s += pr[2 * j + 1] * tk::hw_exp(mj - m);
   }
   s = tk::group_allreduce<kOnlineThreads>(s, tk::SumOp{}, scratch);
   const float inv = 1.0f / s;
 #pragma unroll
-  for (int e = 0; e < kOnlineVals; ++e) v[e] = expf(v[e] - m) * inv;
+  for (int e = 0; e < kOnlineVals; ++e) v[e] = tk::hw_exp(v[e] - m) * inv;
   T* yr = y + row * y_stride + c0;
   if constexpr (VEC * sizeof(T) == 16)
     tk::store_row_buf<T, VEC, kOnlineThreads, kOnlineVals, tk::kCpolStream>(yr, n, threadIdx.x,
