@@ -390,7 +390,7 @@ def measured_roofs(torch, device) -> dict:
     del src, dst
     # Read:write mixes, each the best of two layouts (128 MiB per array, the step's tensor
     # size, rotating over three independent sets like the step; 512 MiB per array, one set)
-    # and eight access variants: 32 or 64 KiB tiles, one workgroup per tile or 8192
+    # and eight access variants: 8 or 16 KiB tiles, one workgroup per tile or 8192
     # workgroups walking them grid-stride, non-temporal or sc1 stores.
     big = 1 << 29
     srcs = torch.randint(-2**31, 2**31 - 1, (3 * big // 4,), dtype=torch.int32, device=device)
@@ -405,7 +405,7 @@ def measured_roofs(torch, device) -> dict:
     for reads, writes in ((1, 0), (0, 1), (1, 1), (2, 1), (3, 1), (2, 2), (3, 2)):
         key = f"{reads}:{writes}"
         for (part, nsets), policy, tile, grid in itertools.product(
-                ((small, 3), (big, 1)), (0, 1), (32, 64), (0, 8192)):
+                ((small, 3), (big, 1)), (0, 1), (8, 16), (0, 8192)):
             if writes == 0 and policy == 1:
                 continue  # the store policy does not apply to a read-only stream
             turn = itertools.count()

@@ -380,7 +380,7 @@ int tk_roof_copy(const void* src, void* dst, int64_t bytes, void* stream);
 
 /* `reads` source arrays and `writes` destination arrays of `bytes` each (src holds
  * reads * bytes, dst writes * bytes, at least `bytes` when writes is 0), cut into tiles of
- * `tile_kib` (32 or 64) KiB per array: one workgroup per tile (max_workgroups 0) or at most
+ * `tile_kib` (8 or 16) KiB per array: one workgroup per tile (max_workgroups 0) or at most
  * max_workgroups workgroups walking the tiles grid-stride. 16-byte non-temporal loads,
  * stores non-temporal (store_policy 0) or sc1 (1); each written 16-byte chunk i is
  * {i, 0, 0, 0} xor the chunks read at its position. Mixes (reads:writes) 1:0, 0:1, 1:1, 2:1,

@@ -52,7 +52,7 @@ def test_roof_arguments_are_checked() -> None:
 
 
 @pytest.mark.parametrize("reads,writes", [(1, 0), (0, 1), (1, 1), (2, 1), (3, 1), (2, 2), (3, 2)])
-@pytest.mark.parametrize("policy,tile,grid", [(0, 64, 0), (1, 32, 0), (0, 32, 3)])
+@pytest.mark.parametrize("policy,tile,grid", [(0, 16, 0), (1, 8, 0), (0, 8, 3)])
 @pytest.mark.parametrize("nbytes", [65536 * 16, 65536 * 3 + 4096 + 48])
 def test_roof_stream_writes_the_xor_of_its_reads(reads: int, writes: int, policy: int, tile: int,
                                                  grid: int, nbytes: int) -> None:
@@ -82,12 +82,12 @@ def test_roof_stream_writes_the_xor_of_its_reads(reads: int, writes: int, policy
 def test_roof_stream_arguments_are_checked() -> None:
     out = torch.empty(1 << 16, device="cuda")
     with pytest.raises(_hip.HipLibraryError, match="store_policy"):
-        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 4096, 1, 1, 2, 64, 0, _stream())
+        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 4096, 1, 1, 2, 16, 0, _stream())
     with pytest.raises(_hip.HipLibraryError, match="tile_kib"):
-        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 4096, 1, 1, 0, 16, 0, _stream())
+        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 4096, 1, 1, 0, 32, 0, _stream())
     with pytest.raises(_hip.HipLibraryError, match="max_workgroups"):
-        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 4096, 1, 1, 0, 64, -1, _stream())
+        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 4096, 1, 1, 0, 16, -1, _stream())
     with pytest.raises(_hip.HipLibraryError, match="unsupported mix"):
-        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 4096, 1, 2, 0, 64, 0, _stream())
+        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 4096, 1, 2, 0, 16, 0, _stream())
     with pytest.raises(_hip.HipLibraryError, match="read-only run"):
-        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 16, 1, 0, 0, 64, 0, _stream())
+        _hip.call("tk_roof_stream", out.data_ptr(), out.data_ptr(), 16, 1, 0, 0, 16, 0, _stream())

@@ -6,7 +6,7 @@
 //                   chunks of a contiguous 4 KiB-per-wave run before its stores (the
 //                   access shape and cache policy of the elementwise kernels).
 //   tk_roof_stream — R reads and W writes per chunk position (R:W of 1:0, 0:1, 1:1, 2:1,
-//                   3:1, 2:2, 3:2), one 32 or 64 KiB tile of every array per workgroup,
+//                   3:1, 2:2, 3:2), one 8 or 16 KiB tile of every array per workgroup,
 //                   stores non-temporal or sc1: the HBM roof is the best of these mixes, since
 //                   reads and writes turn the HBM bus around differently and the kernels
 //                   here run several mixes.
@@ -59,7 +59,7 @@ __global__ __launch_bounds__(kCopyBlock) void roof_copy_kernel(const i32x4* __re
 
 // R arrays of `chunks` 16-byte chunks read, W arrays written; written chunk i is
 // {i, 0, 0, 0} xor the chunks read at position i. The arrays are cut into tiles of 256 * U
-// chunks (16 U KiB per array); workgroup b takes tiles b, b + G, ... (G = gridDim.x: one
+// chunks (4 U KiB per array); workgroup b takes tiles b, b + G, ... (G = gridDim.x: one
 // tile per workgroup when the grid covers the arrays, else a grid-stride walk), read with
 // non-temporal buffer loads and written with cache policy CPOL; the buffer extent ends at the array's
 // end, so a partial last tile loads zeros past it and drops those stores. With W == 0
@@ -203,12 +203,12 @@ extern "C" int tk_roof_stream(const void* src, void* dst, int64_t bytes, int rea
   if (store_policy != 0 && store_policy != 1)
     return tk::fail("tk_roof_stream: store_policy must be 0 (non-temporal) or 1 (sc1), got %d",
                     store_policy);
-  if (tile_kib != 32 && tile_kib != 64)
-    return tk::fail("tk_roof_stream: tile_kib must be 32 or 64, got %d", tile_kib);
+  if (tile_kib != 8 && tile_kib != 16)
+    return tk::fail("tk_roof_stream: tile_kib must be 8 or 16, got %d", tile_kib);
   const int64_t chunks = bytes / 16;
   if (max_workgroups < 0 || max_workgroups > INT32_MAX)
     return tk::fail("tk_roof_stream: max_workgroups must be 0 (one per tile) or positive");
-  int64_t blocks = tk::cdiv(chunks, int64_t(kCopyBlock) * (tile_kib / 16));
+  int64_t blocks = tk::cdiv(chunks, int64_t(kCopyBlock) * (tile_kib / 4));
   if (max_workgroups > 0 && blocks > max_workgroups) blocks = max_workgroups;
   if (blocks > INT32_MAX) return tk::fail("tk_roof_stream: too many bytes");
   // With no writes the sink store may touch one chunk per thread of the grid.
@@ -225,7 +225,7 @@ extern "C" int tk_roof_stream(const void* src, void* dst, int64_t bytes, int rea
                      chunks, sentinel)
 #define TK_ROOF_STREAM(R, W)                                                                    \
   if (reads == R && writes == W) {                                                              \
-    if (tile_kib == 64) {                                                                       \
+    if (tile_kib == 16) {                                                                       \
       if (store_policy == 0) TK_ROOF_STREAM_LAUNCH(R, W, 2, 4);                                 \
       else TK_ROOF_STREAM_LAUNCH(R, W, 16, 4);                                                  \
     } else {                                                                                    \
