@@ -87,6 +87,9 @@ def _traffic_from_summary() -> float | None:
 # of seven 128 MiB tensors is only 3.5 times that cache; a single reused set ran the step
 # ~5 % faster).
 STEP_SETS = 3
+# Every SAMPLE_EVERY-th timed step times its dominant kernel with an event pair (coprime
+# with STEP_SETS, so the sampled launches cover every tensor set).
+SAMPLE_EVERY = 4
 
 
 class StepSet:
@@ -143,9 +146,11 @@ def time_step(torch, step: Step, steps: int, warmup: int) -> tuple[float, str, f
     """W untimed steps, an untimed attribution pass, then K timed steps.
 
     The attribution pass (20 steps, events around every launch) gives each kernel's
-    mean duration and picks the dominant one. The timed steps carry events only around
-    that kernel: an event record between two launches delays the next launch by a few
-    microseconds, so events around every launch would add ~8% to the step itself.
+    mean duration and picks the dominant one. In the timed steps, every SAMPLE_EVERY-th
+    step carries events around that kernel (its mean over those launches is the dominant
+    kernel's duration): an event record between two launches delays the next launch by a
+    few microseconds, so events around every launch would add ~8 % to the step, and
+    around the dominant kernel in every step ~3 %.
     Returns (ms per timed step, dominant kernel, its mean ms inside the timed region,
     attribution-pass ms per kernel).
     """
@@ -171,25 +176,27 @@ def time_step(torch, step: Step, steps: int, warmup: int) -> tuple[float, str, f
     dominant = max(attribution, key=attribution.get)
     dom = [name for name, _ in launches].index(dominant)
 
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(steps)]
+    sampled = [i for i in range(steps) if i % SAMPLE_EVERY == 0]
+    events = {i: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for i in sampled}
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record(stream)
     for i in range(steps):
+        timed_dom = i in events
         for j, (_, fn) in enumerate(plans[i % len(plans)]):
-            if j == dom:
+            if timed_dom and j == dom:
                 events[i][0].record(stream)
             fn()
-            if j == dom:
+            if timed_dom and j == dom:
                 events[i][1].record(stream)
     end.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
     ms_step = start.elapsed_time(end) / steps
-    dominant_ms = statistics.fmean(a.elapsed_time(b) for a, b in events)
+    dominant_ms = statistics.fmean(a.elapsed_time(b) for a, b in events.values())
     # The event clock and the host clock must agree on the timed region.
     if abs(wall_ms / steps - ms_step) > 0.5 * ms_step:
         raise RuntimeError(f"event and host clocks disagree: {ms_step} vs {wall_ms / steps} ms")
