@@ -374,27 +374,48 @@ attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __res
 
 // ---------------------------------------------------------------- backward: delta
 
-// delta[row] = sum_d O[row][d] * dO[row][d]; D/8 lanes per row, 16 bytes each.
+// delta[row] = sum_d O[row][d] * dO[row][d]; D/8 lanes per row, 16 bytes each. A workgroup
+// takes kPreUnroll passes of kThreads / (D/8) consecutive rows; each thread loads its pieces
+// of kPreUnroll rows before any arithmetic, and the row -> (batch, head, position) split is
+// a multiply-shift division (one row per thread with 64-bit divisions: B4 H32 N8192 D128
+// in 93.6 instead of 89.4 us).
+constexpr int kPreUnroll = 4;
+
 template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void attn_bwd_preprocess_kernel(
-    const T* __restrict__ O, const T* __restrict__ dO, float* __restrict__ delta, int heads,
-    int seq, int64_t sb, int64_t sh, int64_t sn, int64_t rows) {
-  constexpr int LPR = D / 8;
-  const int64_t row = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) / LPR;
+    const T* __restrict__ O, const T* __restrict__ dO, float* __restrict__ delta,
+    tk::FastDiv seq_div, tk::FastDiv head_div, int64_t sb, int64_t sh, int64_t sn, int rows) {
+  constexpr int LPR = D / 8;            // lanes per row
+  constexpr int RPP = kThreads / LPR;   // rows per pass
   const int part = threadIdx.x % LPR;
-  float acc = 0.f;
-  if (row < rows) {
-    const int64_t bh = row / seq, i = row % seq;
-    const int64_t off = (bh / heads) * sb + (bh % heads) * sh + i * sn + part * 8;
-    float o[8], g[8];
-    tk::load_vec<T, 8>(O + off, o);
-    tk::load_vec<T, 8>(dO + off, g);
+  const int r0 = blockIdx.x * (RPP * kPreUnroll) + threadIdx.x / LPR;
+  float o[kPreUnroll][8], g[kPreUnroll][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += o[e] * g[e];
+  for (int u = 0; u < kPreUnroll; ++u) {
+    const int row = r0 + u * RPP;
+    if (row < rows) {
+      const int bh = static_cast<int>(seq_div.div(static_cast<uint32_t>(row)));
+      const int i = row - bh * static_cast<int>(seq_div.d);
+      const int b = static_cast<int>(head_div.div(static_cast<uint32_t>(bh)));
+      const int h = bh - b * static_cast<int>(head_div.d);
+      const int64_t off = b * sb + h * sh + i * sn + part * 8;
+      tk::load_vec<T, 8>(O + off, o[u]);
+      tk::load_vec<T, 8>(dO + off, g[u]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[u][e] = g[u][e] = 0.f;
+    }
   }
 #pragma unroll
-  for (int w = LPR / 2; w >= 1; w >>= 1) acc += __shfl_xor(acc, w);
-  if (row < rows && part == 0) delta[row] = acc;
+  for (int u = 0; u < kPreUnroll; ++u) {
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += o[u][e] * g[u][e];
+#pragma unroll
+    for (int w = LPR / 2; w >= 1; w >>= 1) acc += __shfl_xor(acc, w);
+    const int row = r0 + u * RPP;
+    if (row < rows && part == 0) delta[row] = acc;
+  }
 }
 
 // ---------------------------------------------------------------- backward: dQ
@@ -776,28 +797,31 @@ extern "C" int tk_attn_bwd_preprocess(int dtype, const void* o, const void* dout
       !tk::aligned16(dout))
     return tk::fail("attn_bwd_preprocess: unsupported layout");
   const int64_t rows = batch * heads * seq;
-  const int64_t blocks = tk::cdiv(rows * (head_dim / 8), kThreads);
+  if (rows > INT32_MAX / 2) return tk::fail("attn_bwd_preprocess: too many rows");
+  const int64_t rows_per_block = kThreads / (head_dim / 8) * kPreUnroll;
+  const int64_t blocks = tk::cdiv(rows, rows_per_block);
+  const tk::FastDiv seq_div(static_cast<uint32_t>(seq)), head_div(static_cast<uint32_t>(heads));
   hipStream_t st = tk::as_stream(stream);
   if (dtype == TK_DTYPE_F16) {
     using T = _Float16;
     if (head_dim == 64)
       hipLaunchKernelGGL((attn_bwd_preprocess_kernel<T, 64>), dim3(blocks), dim3(kThreads), 0, st,
-                         (const T*)o, (const T*)dout, delta, (int)heads, (int)seq, strides[0],
-                         strides[1], strides[2], rows);
+                         (const T*)o, (const T*)dout, delta, seq_div, head_div, strides[0],
+                         strides[1], strides[2], (int)rows);
     else
       hipLaunchKernelGGL((attn_bwd_preprocess_kernel<T, 128>), dim3(blocks), dim3(kThreads), 0, st,
-                         (const T*)o, (const T*)dout, delta, (int)heads, (int)seq, strides[0],
-                         strides[1], strides[2], rows);
+                         (const T*)o, (const T*)dout, delta, seq_div, head_div, strides[0],
+                         strides[1], strides[2], (int)rows);
   } else {
     using T = __bf16;
     if (head_dim == 64)
       hipLaunchKernelGGL((attn_bwd_preprocess_kernel<T, 64>), dim3(blocks), dim3(kThreads), 0, st,
-                         (const T*)o, (const T*)dout, delta, (int)heads, (int)seq, strides[0],
-                         strides[1], strides[2], rows);
+                         (const T*)o, (const T*)dout, delta, seq_div, head_div, strides[0],
+                         strides[1], strides[2], (int)rows);
     else
       hipLaunchKernelGGL((attn_bwd_preprocess_kernel<T, 128>), dim3(blocks), dim3(kThreads), 0, st,
-                         (const T*)o, (const T*)dout, delta, (int)heads, (int)seq, strides[0],
-                         strides[1], strides[2], rows);
+                         (const T*)o, (const T*)dout, delta, seq_div, head_div, strides[0],
+                         strides[1], strides[2], (int)rows);
   }
   return tk::check_launch("attn_bwd_preprocess");
 }
