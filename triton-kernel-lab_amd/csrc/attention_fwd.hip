@@ -29,8 +29,11 @@
 // cannot sink them into the next phase.
 //
 // K and V blocks reach LDS by buffer->LDS DMA (no VGPR staging) into a 4-stage ring; block
-// j is read in phases 2j .. 2j+3 and its stage is refilled at phase 2j+4. LDS layouts keep
-// every read phase on 64 distinct banks:
+// j is read in phases 2j .. 2j+3 and its stage is refilled from phase 2j+4 on: each wave
+// issues its share of block m + 2 spread over the read units of its MFMA phase of block m
+// (issued as one burst after a barrier, the DMA instructions held the issuing waves ~300
+// cycles per block; causal D128 1.91 -> 1.83 ms). LDS layouts keep every read phase on 64
+// distinct banks:
 //   K [64 keys][D]: 16-byte chunk c of row r at slot c ^ kswz(r) (ds_read_b128, 16 lanes
 //                   per phase read one chunk of 16 rows);
 //   V [64 keys][D]: 32-byte granule g of row r at granule g ^ vswz(r) (ds_read_b64_tr_b16,
@@ -133,6 +136,26 @@ __device__ __forceinline__ void dma_block(__amdgpu_buffer_rsrc_t rk, __amdgpu_bu
   }
 }
 
+// DMA instruction i (0 .. DMA_PER_BLOCK - 1) of this wave's share of block `blk`: K chunks
+// first, then V.
+template <int D>
+__device__ __forceinline__ void dma_one(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                        char* lds, const uint32_t* k_src, const uint32_t* v_src,
+                                        int blk, int last, uint32_t k_blk, uint32_t v_blk,
+                                        int wave, int i) {
+  using G = Geo<D>;
+  char* stage = lds + (blk % G::STAGES) * G::STB;
+  blk = min(blk, last);
+  const int x = i % G::DMA_PER_OP;
+  const int id = wave * G::DMA_PER_OP + x;
+  if (i < G::DMA_PER_OP)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(stage + id * 1024), 16, k_src[x],
+                                             blk * k_blk, 0, 0);
+  else
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(stage + G::OPB + id * 1024), 16,
+                                             v_src[x], blk * v_blk, 0, 0);
+}
+
 // The MFMA phase as a pipeline of read units of four LDS instructions each: V units
 // (u < NV) hold 32-key step s = u / (FT/2) of feature tiles 2p and 2p+1 (p = u % (FT/2)),
 // K units (u >= NV) k-step kk = u - NV of the four key tiles. Unit u's MFMAs run while
@@ -163,8 +186,8 @@ __device__ __forceinline__ void read_v_unit(i32x4 (&vu)[Units<D>::NV][2], uint32
 // (DO_PV; P^T is dead before S^T is produced), then S^T(j) = K_j Q^T into st (DO_S).
 // kb / vb: LDS addresses of the K tile of block j and the V tile of block j-1. With DO_PV
 // the first PREFETCH V units were issued by the preceding softmax phase.
-template <typename T, int D, bool DO_S, bool DO_PV>
-__device__ __forceinline__ void mfma_phase(uint32_t kb, uint32_t vb, const uint32_t (&ka)[Geo<D>::KS],
+template <typename T, int D, bool DO_S, bool DO_PV, typename Hook>
+__device__ __forceinline__ void mfma_phase(Hook&& hook, uint32_t kb, uint32_t vb, const uint32_t (&ka)[Geo<D>::KS],
                                            const uint32_t (&va)[Geo<D>::FT],
                                            const i32x4 (&qf)[2][Geo<D>::KS], f32x4 (&st)[2][4],
                                            const i32x4 (&pf)[2][2], f32x4 (&acc)[Geo<D>::FT][2],
@@ -224,6 +247,7 @@ __device__ __forceinline__ void mfma_phase(uint32_t kb, uint32_t vb, const uint3
                                      kk == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[qt][kt]);
     }
     if (u + DEPTH < NU) issue(u + DEPTH);
+    hook(u, NU);
     sched_fence();
   }
 }
@@ -377,13 +401,33 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
   grp = __builtin_amdgcn_readfirstlane(grp) & 1;
   const int phases = 2 * kv_blocks + 2;
   int t = 0;
+  // Block m + STAGES - 2 (m >= 1) is fetched during this wave's MFMA phase of block m
+  // (phase 2m + grp), its DMA_PER_BLOCK instructions spread over the phase's read units;
+  // after the wave's last MFMA phase, at the start of phase 2m + grp (tail mode). Block m+1
+  // was issued by every wave before the end of phase 2m + 1 (grp 0 in phase 2m - 2, grp 1
+  // in 2m - 1), so the wait at the end of each odd phase, which leaves one block's
+  // instructions in flight, still covers it.
+  bool tail = false;
+  int tail_m = 0;
   auto end_phase = [&]() {
     if (t & 1) wait_vmcnt<(STAGES - 3) * DPB>();
     barrier_no_fence();
     ++t;
-    if (!(t & 1))
-      dma_block<D>(rk, rv, lds, k_src, v_src, (t >> 1) + STAGES - 2, last, k_blk, v_blk, wave);
+    if (tail && tail_m <= kv_blocks && t == 2 * tail_m + grp) {
+      dma_block<D>(rk, rv, lds, k_src, v_src, tail_m + STAGES - 2, last, k_blk, v_blk, wave);
+      ++tail_m;
+    }
   };
+  // Hook of the MFMA phase of block m: after unit u of nu, the DMA instructions whose
+  // share of the phase ends there (DMA_PER_BLOCK of them over the nu units).
+  auto dma_hook = [&](int m) {
+    return [&, m](int u, int nu) {
+      const int a = (u * DPB) / nu, b2 = ((u + 1) * DPB) / nu;
+      if (b2 != a)
+        dma_one<D>(rk, rv, lds, k_src, v_src, m + STAGES - 2, last, k_blk, v_blk, wave, b2 - 1);
+    };
+  };
+  auto no_hook = [](int, int) {};
   auto kbase = [&](int j) { return lds_base + (j % STAGES) * STB; };
 
   // Softmax phase of block j: P = exp2(S * scale * log2(e) - m) into pf, the running
@@ -543,21 +587,23 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
     for (int u = 0; u < Units<D>::PREFETCH; ++u) read_v_unit<D>(vu, kbase(j), va, u);
   };
   if (grp) end_phase();
-  mfma_phase<T, D, true, false>(kbase(0), 0, ka, va, qf, st, pf, acc, vu);
+  mfma_phase<T, D, true, false>(no_hook, kbase(0), 0, ka, va, qf, st, pf, acc, vu);
   pin_mfma();
   end_phase();
   for (int j = 1; j < n; ++j) {
     softmax_phase(j - 1);
     pin_softmax(j - 1);
     end_phase();
-    mfma_phase<T, D, true, true>(kbase(j), kbase(j - 1), ka, va, qf, st, pf, acc, vu);
+    mfma_phase<T, D, true, true>(dma_hook(j), kbase(j), kbase(j - 1), ka, va, qf, st, pf, acc, vu);
     pin_mfma();
     end_phase();
   }
   softmax_phase(n - 1);
   pin_softmax(n - 1);
   end_phase();
-  mfma_phase<T, D, false, true>(0, kbase(n - 1), ka, va, qf, st, pf, acc, vu);
+  mfma_phase<T, D, false, true>(dma_hook(n), 0, kbase(n - 1), ka, va, qf, st, pf, acc, vu);
+  tail = true;
+  tail_m = n + 1;
   while (t < phases - 1) end_phase();
   // No DMA may still be writing when the workgroup's LDS is released.
   wait_vmcnt<0>();
