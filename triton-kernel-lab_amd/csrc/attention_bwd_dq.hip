@@ -21,7 +21,9 @@
 // Ping-pong, as in the forward: barrier-separated phases alternate an MFMA phase M(j)
 // (dQ^T += K_{j-1}^T dS_{j-1}^T, then S^T_j and dP^T_j) and an elementwise phase V(j)
 // (P, dS); the two waves of each SIMD run opposite phases. K/V blocks reach LDS by
-// buffer->LDS DMA into a 4-stage ring (block j is read in phases 2j .. 2j+3).
+// buffer->LDS DMA into a 4-stage ring (block j is read in phases 2j .. 2j+3); each wave
+// issues its share of block m + 2 spread over the read units of its MFMA phase of block m,
+// not as a burst after a barrier (causal D128 2.65 -> 2.60 ms).
 #include "attention.hpp"
 #include "attention_dma.hpp"
 
@@ -101,6 +103,26 @@ __device__ __forceinline__ void dq_dma_block(__amdgpu_buffer_rsrc_t rk, __amdgpu
   }
 }
 
+// DMA instruction i (0 .. DMA_PER_BLOCK - 1) of this wave's share of block `blk`: K chunks
+// first, then V.
+template <int D>
+__device__ __forceinline__ void dq_dma_one(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                           char* lds, const uint32_t* k_src,
+                                           const uint32_t* v_src, int blk, int last,
+                                           uint32_t blk_bytes, int wave, int i) {
+  using G = DqGeo<D>;
+  char* stage = lds + (blk % G::STAGES) * G::STB;
+  blk = min(blk, last);
+  const int x = i % G::DMA_PER_OP;
+  const int id = wave * G::DMA_PER_OP + x;
+  if (i < G::DMA_PER_OP)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(stage + id * 1024), 16, k_src[x],
+                                             blk * blk_bytes, 0, 0);
+  else
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(stage + G::OPB + id * 1024), 16,
+                                             v_src[x], blk * blk_bytes, 0, 0);
+}
+
 // Transposed-K unit u of the K tile at kb into tu[u].
 template <int D>
 __device__ __forceinline__ void read_t_unit(i32x4 (&tu)[DqGeo<D>::NT][2], uint32_t kb,
@@ -117,8 +139,8 @@ __device__ __forceinline__ void read_t_unit(i32x4 (&tu)[DqGeo<D>::NT][2], uint32
 // dP^T(j) = V_j dO^T (DO_S), with DqGeo::SEED starting from -delta of the lane's query
 // (nd), so the elementwise phase forms dS = P (dP - delta) with one multiply. kb / tb:
 // LDS addresses of block j's stage and block j-1's.
-template <typename T, int D, bool DO_S, bool DO_DQ>
-__device__ __forceinline__ void dq_mfma_phase(uint32_t kb, uint32_t tb,
+template <typename T, int D, bool DO_S, bool DO_DQ, typename Hook>
+__device__ __forceinline__ void dq_mfma_phase(Hook&& hook, uint32_t kb, uint32_t tb,
                                               const uint32_t (&ka)[DqGeo<D>::KS],
                                               const uint32_t (&va)[DqGeo<D>::KS],
                                               const uint32_t (&ta)[DqGeo<D>::FT],
@@ -192,6 +214,7 @@ __device__ __forceinline__ void dq_mfma_phase(uint32_t kb, uint32_t tb,
       }
     }
     if (u + DEPTH < NU) issue(u + DEPTH);
+    hook(u, NU);
     sched_fence();
   }
 }
@@ -318,13 +341,32 @@ attn_bwd_dq_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T*
   grp = __builtin_amdgcn_readfirstlane(grp) & 1;
   const int phases = 2 * kv_blocks + 2;
   int t = 0;
+  // Block m + STAGES - 2 (m >= 1) is fetched during this wave's MFMA phase of block m
+  // (phase 2m + grp), its DMA_PER_BLOCK instructions spread over the phase's read units;
+  // after the wave's last MFMA phase, at the start of phase 2m + grp (tail mode). Block m+1
+  // was issued by every wave before the end of phase 2m + 1, so the wait at the end of
+  // each odd phase, which leaves one block's instructions in flight, still covers it.
+  bool tail = false;
+  int tail_m = 0;
   auto end_phase = [&]() {
     if (t & 1) wait_vmcnt<(STAGES - 3) * DPB>();
     barrier_no_fence();
     ++t;
-    if (!(t & 1))
-      dq_dma_block<D>(rk, rv, lds, k_src, v_src, (t >> 1) + STAGES - 2, last, blk_bytes, wave);
+    if (tail && tail_m <= kv_blocks && t == 2 * tail_m + grp) {
+      dq_dma_block<D>(rk, rv, lds, k_src, v_src, tail_m + STAGES - 2, last, blk_bytes, wave);
+      ++tail_m;
+    }
   };
+  // Hook of the MFMA phase of block m: after unit u of nu, the DMA instructions whose share
+  // of the phase ends there (DMA_PER_BLOCK of them over the nu units).
+  auto dma_hook = [&](int m) {
+    return [&, m](int u, int nu) {
+      const int a = (u * DPB) / nu, b2 = ((u + 1) * DPB) / nu;
+      if (b2 != a)
+        dq_dma_one<D>(rk, rv, lds, k_src, v_src, m + STAGES - 2, last, blk_bytes, wave, b2 - 1);
+    };
+  };
+  auto no_hook = [](int, int) {};
   auto kbase = [&](int j) { return lds_base + (j % STAGES) * STB; };
 
   // Elementwise phase of block j: P = exp2(S^T c - lse), dS^T = P (dP^T - delta) into df;
@@ -389,22 +431,26 @@ attn_bwd_dq_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T*
 
   const int n = CAUSAL ? min(kv_blocks, (wq0 + G::QW - 1) / BN + 1) : kv_blocks;
   if (grp) end_phase();
-  dq_mfma_phase<T, D, true, false>(kbase(0), 0, ka, va, ta, qf, of, st, dp, nd, df, acc, tu);
+  dq_mfma_phase<T, D, true, false>(no_hook, kbase(0), 0, ka, va, ta, qf, of, st, dp, nd, df, acc,
+                                   tu);
   pin_mfma();
   end_phase();
   for (int j = 1; j < n; ++j) {
     dS_phase(j - 1);
     pin_dS(j - 1);
     end_phase();
-    dq_mfma_phase<T, D, true, true>(kbase(j), kbase(j - 1), ka, va, ta, qf, of, st, dp, nd, df, acc,
-                                    tu);
+    dq_mfma_phase<T, D, true, true>(dma_hook(j), kbase(j), kbase(j - 1), ka, va, ta, qf, of, st, dp,
+                                    nd, df, acc, tu);
     pin_mfma();
     end_phase();
   }
   dS_phase(n - 1);
   pin_dS(n - 1);
   end_phase();
-  dq_mfma_phase<T, D, false, true>(0, kbase(n - 1), ka, va, ta, qf, of, st, dp, nd, df, acc, tu);
+  dq_mfma_phase<T, D, false, true>(dma_hook(n), 0, kbase(n - 1), ka, va, ta, qf, of, st, dp, nd,
+                                   df, acc, tu);
+  tail = true;
+  tail_m = n + 1;
   while (t < phases - 1) end_phase();
   wait_vmcnt<0>();
 
