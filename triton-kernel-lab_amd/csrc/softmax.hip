@@ -1,17 +1,45 @@
 // Row-wise softmax, one row per thread group, the whole row in registers.
 //
 // Math follows the reference kernel (src/tklab/kernels/fused_softmax.py:32-39):
-// float32 values, masked tail = -inf, shifted = x - rowmax, numerator = exp,
-// y = numerator / rowsum (here numerator * (1/rowsum)), stored in the input dtype.
+// float32 values, masked tail = -inf, shifted = x - rowmax, numerator = exp (here the
+// hardware exp2 of shifted * log2(e)), y = numerator / rowsum (here numerator * (1/rowsum)),
+// stored in the input dtype.
 // One HBM read and one HBM write per element.
 #include "rows.hpp"
 
 namespace {
 
-template <typename T, int VEC, int RT, int VALS>
+// max, exponentials (tk::hw_exp, the hardware exp2 of x log2(e)), sum and scaling of one row
+// held in registers, in place.
+template <int RT, int VALS>
+__device__ __forceinline__ void softmax_row(float* v, float* scratch) {
+  float m = v[0];
+#pragma unroll
+  for (int e = 1; e < VALS; ++e) m = fmaxf(m, v[e]);
+  m = tk::group_allreduce<RT>(m, tk::MaxOp{}, scratch);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < VALS; ++e) {
+    v[e] = tk::hw_exp(v[e] - m);
+    s += v[e];
+  }
+  s = tk::group_allreduce<RT>(s, tk::SumOp{}, scratch);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int e = 0; e < VALS; ++e) v[e] *= inv;
+}
+
+// P rows per thread group (P = 2 only for single-wave rows): every row's loads are issued
+// first, so the exponentials and stores of a row overlap the loads of the next. On f32
+// 4096 x 4096 (one wave per row, all waves resident in one round) one row per wave ran
+// 26.8-27.2 us with libm's expf and 25.6 us with hw_exp; two rows per wave with hw_exp
+// 23.2-23.6 us; three or four rows per wave through two register buffers 27-29 us (too
+// few waves per SIMD).
+template <typename T, int VEC, int RT, int VALS, int P>
 __global__ __launch_bounds__(RT >= 256 ? RT : 256) void softmax_fwd_kernel(
     const T* __restrict__ x, T* __restrict__ y, int rows, int cols, int64_t x_stride,
     int64_t y_stride) {
+  static_assert(P == 1 || RT == 64, "several rows per group only for single-wave rows");
   constexpr int SLOTS = RT >= 256 ? 1 : 256 / RT;
   __shared__ float scratch[RT / 64];
   const int lane = threadIdx.x % RT;
@@ -19,40 +47,31 @@ __global__ __launch_bounds__(RT >= 256 ? RT : 256) void softmax_fwd_kernel(
   // (f32 4096 x 4096 went from 4.9 to 5.9 TB/s). The row index is wave-uniform and
   // readfirstlane lets the compiler keep each row's buffer resource scalar.
   constexpr bool kBuf = VEC * sizeof(T) == 16;
-  const int row = __builtin_amdgcn_readfirstlane(blockIdx.x * SLOTS + threadIdx.x / RT);
+  const int row0 = __builtin_amdgcn_readfirstlane((blockIdx.x * SLOTS + threadIdx.x / RT) * P);
   // SLOTS > 1 only for single-wave rows, which never reach a block barrier.
-  if (row >= rows) return;
+  if (row0 >= rows) return;
 
-  float v[VALS];
-  if constexpr (kBuf)
-    tk::load_row_buf<T, VEC, RT, VALS, tk::kCpolStream>(x + row * x_stride, cols, lane, v,
-                                                         -INFINITY);
-  else
-    tk::load_row<T, VEC, RT, VALS>(x + row * x_stride, cols, lane, v, -INFINITY);
-
-  float m = v[0];
+  float v[P][VALS];
 #pragma unroll
-  for (int e = 1; e < VALS; ++e) m = fmaxf(m, v[e]);
-  m = tk::group_allreduce<RT>(m, tk::MaxOp{}, scratch);
-
-  // libm's expf, not the bare hardware exponential (tk::hw_exp, four times fewer VALU
-  // instructions): this kernel is HBM-bound and, measured on f32 4096 x 4096, ran 22.5-23.9 us
-  // with expf and 25.6-25.9 us with hw_exp (also with every load issued up front, or in two or
-  // four phases).
-  float s = 0.f;
-#pragma unroll
-  for (int e = 0; e < VALS; ++e) {
-    v[e] = expf(v[e] - m);
-    s += v[e];
+  for (int p = 0; p < P; ++p) {
+    // A group past the last row reloads that row and does not store it.
+    const int64_t r = min(row0 + p, rows - 1);
+    if constexpr (kBuf)
+      tk::load_row_buf<T, VEC, RT, VALS, tk::kCpolStream>(x + r * x_stride, cols, lane, v[p],
+                                                           -INFINITY);
+    else
+      tk::load_row<T, VEC, RT, VALS>(x + r * x_stride, cols, lane, v[p], -INFINITY);
   }
-  s = tk::group_allreduce<RT>(s, tk::SumOp{}, scratch);
-  const float inv = 1.0f / s;
 #pragma unroll
-  for (int e = 0; e < VALS; ++e) v[e] *= inv;
-  if constexpr (kBuf)
-    tk::store_row_buf<T, VEC, RT, VALS, tk::kCpolStream>(y + row * y_stride, cols, lane, v);
-  else
-    tk::store_row<T, VEC, RT, VALS>(y + row * y_stride, cols, lane, v);
+  for (int p = 0; p < P; ++p) {
+    softmax_row<RT, VALS>(v[p], scratch);
+    const int64_t r = row0 + p;
+    if (r >= rows) break;
+    if constexpr (kBuf)
+      tk::store_row_buf<T, VEC, RT, VALS, tk::kCpolStream>(y + r * y_stride, cols, lane, v[p]);
+    else
+      tk::store_row<T, VEC, RT, VALS>(y + r * y_stride, cols, lane, v[p]);
+  }
 }
 
 // ------------------------------------------------------------------ online softmax
@@ -188,14 +207,22 @@ extern "C" int tk_softmax_fwd(int dtype, const void* x, void* y, int64_t rows, i
   const bool vector_ok = tk::aligned16(x) && tk::aligned16(y) && cols % vec == 0 &&
                          (x_row_stride * es) % 16 == 0 && (y_row_stride * es) % 16 == 0;
   const int slots = shape.rt >= 256 ? 1 : 256 / shape.rt;
-  const dim3 grid(static_cast<unsigned>(tk::cdiv(rows, slots)));
+  // Two single-wave rows per wave once that still leaves two waves per SIMD (4096 rows).
+  const bool pair = shape.rt == 64 && rows >= 4096;
+  const dim3 grid(static_cast<unsigned>(tk::cdiv(rows, slots * (pair ? 2 : 1))));
   const dim3 block(shape.rt >= 256 ? shape.rt : 256);
   hipStream_t s = tk::as_stream(stream);
   TK_DISPATCH_DTYPE(dtype, T,
     TK_DISPATCH_VEC(T, vector_ok,
       TK_DISPATCH_ROW_SHAPE(shape,
-        hipLaunchKernelGGL((softmax_fwd_kernel<T, VEC, RT, VALS>), grid, block, 0, s,
-                           static_cast<const T*>(x), static_cast<T*>(y), (int)rows, (int)cols,
-                           x_row_stride, y_row_stride))));
+        constexpr int P2 = RT == 64 ? 2 : 1;
+        if (pair)
+          hipLaunchKernelGGL((softmax_fwd_kernel<T, VEC, RT, VALS, P2>), grid, block, 0, s,
+                             static_cast<const T*>(x), static_cast<T*>(y), (int)rows, (int)cols,
+                             x_row_stride, y_row_stride);
+        else
+          hipLaunchKernelGGL((softmax_fwd_kernel<T, VEC, RT, VALS, 1>), grid, block, 0, s,
+                             static_cast<const T*>(x), static_cast<T*>(y), (int)rows, (int)cols,
+                             x_row_stride, y_row_stride))));
   return tk::check_launch("softmax");
 }
