@@ -254,6 +254,57 @@ __device__ __forceinline__ void mfma_phase(Hook&& hook, uint32_t kb, uint32_t vb
 
 // head_dim 64 uses 64 KiB of LDS per workgroup: held to 128 registers, two workgroups
 // share a CU (four waves per SIMD).
+// Tile `it` (0, 1, ...) of this workgroup in the persistent schedule of an equal-length
+// launch, as (batch * head, query block); false when the workgroup has no tile left. With
+// batch * heads and the grid both multiples of 8, workgroup w runs on XCD w % 8 and takes
+// tiles of that XCD's eighth of the heads only (a head's K/V blocks then stay in one L2),
+// head-major, so the workgroups of an XCD work through one or two heads at a time.
+// Causal: query blocks i and QB-1-i of a head form a pair of QB+1 key blocks, so every
+// pair is the same work; pair p of the XCD goes to its workgroup p % gx, heavy block first.
+// A workgroup that finishes early does not wait for the hardware dispatcher: with one
+// workgroup per tile, a CU whose causal tile ended sat idle ~9 us on average before its
+// next tile started (non-causal: 2.8 us), because the dispatcher hands tiles to the XCDs
+// in a fixed round-robin order and waits on the XCD whose next CU is still busy.
+// Persistent workgroups for head_dim 128 only: at head_dim 64 (128 registers) the values
+// the tile loop keeps live spill.
+template <int D>
+constexpr bool kPersistent = D == 128;
+
+template <bool CAUSAL>
+__device__ __forceinline__ bool fwd_tile_of(const Shape& s, int& it, int& bh, int& qb) {
+  const int QB = s.q_blocks, BH = s.tiles / QB;
+  int j = blockIdx.x, gx = gridDim.x, h0 = 0, hn = BH;
+  if (BH % 8 == 0 && gridDim.x % 8 == 0) {
+    j = blockIdx.x / 8;
+    gx = gridDim.x / 8;
+    hn = BH / 8;
+    h0 = (blockIdx.x % 8) * hn;
+  }
+  if (!CAUSAL) {
+    const int t = j + it * gx;
+    if (t >= hn * QB) return false;
+    bh = h0 + t / QB;
+    qb = t % QB;
+    return true;
+  }
+  const int ph = (QB + 1) / 2;  // pairs per head
+  for (;;) {
+    const int p = j + (it >> 1) * gx;
+    if (p >= hn * ph) return false;
+    const int i = p % ph;
+    bh = h0 + p / ph;
+    if ((it & 1) == 0) {
+      qb = QB - 1 - i;
+      return true;
+    }
+    if (i != QB - 1 - i) {
+      qb = i;
+      return true;
+    }
+    ++it;  // odd QB: the middle block has no partner
+  }
+}
+
 template <typename T, int D, bool CAUSAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(D == 64 ? 4 : 2))) void
@@ -265,376 +316,406 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
   __shared__ __attribute__((aligned(1024))) char lds[STAGES * STB];
   __shared__ int simd_of[G::WAVES];
 
-  // Workgroup -> (batch*head, query block). Equal lengths: XCD-contiguous ranges so a
-  // head's blocks share one L2; causal: the heaviest (last) query block of a head first.
-  // Varlen: the heavy-first schedule over every sequence's query blocks (level = query
-  // block), heads interleaved over the XCDs.
-  int b, h, qb, start = 0, N = s.seq;
-  uint32_t k_bytes = s.k_bytes, v_bytes = s.v_bytes;
-  if (s.cu != nullptr) {
-    h = varlen_head(blockIdx.x, s.heads);
-    VarlenTile vt;
-    if (!varlen_tile(s.cu, s.batch, s.total, s.seq, BM, blockIdx.x / s.heads, vt)) return;
-    b = vt.b;
-    qb = vt.level;
-    const VarlenRows rows = varlen_rows(s.cu, b, s.total, s.seq);
-    start = rows.start;
-    N = rows.n;
-    if (qb * BM >= N) return;  // uniform: the whole workgroup leaves
-    k_bytes = uint32_t(((N - 1) * s.k[2] + D) * 2);
-    v_bytes = uint32_t(((N - 1) * s.v[2] + D) * 2);
-  } else {
-    int w = blockIdx.x;
-    if (s.tiles % 8 == 0) w = (w % 8) * (s.tiles / 8) + w / 8;
-    const int bh = w / s.q_blocks;
-    qb = CAUSAL ? s.q_blocks - 1 - w % s.q_blocks : w % s.q_blocks;
-    b = bh / s.heads;
-    h = bh % s.heads;
-  }
-  const int kvh = h / s.group;
-  const T* Qh = Q + b * s.q[0] + h * s.q[1] + int64_t(start) * s.q[2];
-  const T* Kh = K + b * s.k[0] + kvh * s.k[1] + int64_t(start) * s.k[2];
-  const T* Vh = V + b * s.v[0] + kvh * s.v[1] + int64_t(start) * s.v[2];
-  T* Oh = O + b * s.o[0] + h * s.o[1] + int64_t(start) * s.o[2];
-
-  const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int c = lane & 15, g = lane >> 4;
-  const int q0 = qb * BM;
-  const int wq0 = q0 + wave * G::QW;
-  if (lane == 0) simd_of[wave] = simd_id();
-
-  const __amdgpu_buffer_rsrc_t rk =
-      __builtin_amdgcn_make_buffer_rsrc((void*)Kh, (short)0, k_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv =
-      __builtin_amdgcn_make_buffer_rsrc((void*)Vh, (short)0, v_bytes, 0x00020000);
+  if ((threadIdx.x & 63) == 0) simd_of[wave] = simd_id();
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
 
-  // DMA sources (bytes from the head's base, block-relative row). Rows past the sequence
-  // end are past the buffer extent and read as zero.
-  uint32_t k_src[G::DMA_PER_OP], v_src[G::DMA_PER_OP];
-#pragma unroll
-  for (int x = 0; x < G::DMA_PER_OP; ++x) {
-    const int id = wave * G::DMA_PER_OP + x;
-    const int row = id * G::ROWS_PER_DMA + lane / G::SLOTS;
-    const int slot = lane % G::SLOTS;
-    k_src[x] = uint32_t(row * s.k[2] + (slot ^ G::kswz(row)) * 8) * 2u;
-    const int granule = (slot >> 1) ^ G::vswz(row);
-    v_src[x] = uint32_t(row * s.v[2] + granule * 16 + (slot & 1) * 8) * 2u;
-  }
-  const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
-  const int kv_blocks = (kv_end + BN - 1) / BN;
-  const int last = kv_blocks - 1;
-  const uint32_t k_blk = uint32_t(BN * s.k[2]) * 2u, v_blk = uint32_t(BN * s.v[2]) * 2u;
-  // The first STAGES - 1 blocks are fetched before anything else.
-#pragma unroll
-  for (int blk = 0; blk < STAGES - 1; ++blk)
-    dma_block<D>(rk, rv, lds, k_src, v_src, blk, last, k_blk, v_blk, wave);
+  // Equal lengths: the workgroups are persistent (as many as the CUs hold), each running
+  // the tiles fwd_tile_of deals it. Varlen: one tile per workgroup, the heavy-first
+  // schedule over every sequence's query blocks (level = query block), heads interleaved
+  // over the XCDs.
+  for (int it = 0; kPersistent<D> || it == 0; ++it) {
+    int b, h, qb, start = 0, N = s.seq;
+    uint32_t k_bytes = s.k_bytes, v_bytes = s.v_bytes;
+    if (s.cu != nullptr) {
+      if (it > 0) break;
+      h = varlen_head(blockIdx.x, s.heads);
+      VarlenTile vt;
+      if (!varlen_tile(s.cu, s.batch, s.total, s.seq, BM, blockIdx.x / s.heads, vt)) break;
+      b = vt.b;
+      qb = vt.level;
+      const VarlenRows rows = varlen_rows(s.cu, b, s.total, s.seq);
+      start = rows.start;
+      N = rows.n;
+      if (qb * BM >= N) break;  // uniform: the whole workgroup leaves
+      k_bytes = uint32_t(((N - 1) * s.k[2] + D) * 2);
+      v_bytes = uint32_t(((N - 1) * s.v[2] + D) * 2);
+    } else if constexpr (kPersistent<D>) {
+      int bh;
+      if (!fwd_tile_of<CAUSAL>(s, it, bh, qb)) break;
+      b = bh / s.heads;
+      h = bh % s.heads;
+    } else {
+      // One tile per workgroup: XCD-contiguous ranges so a head's blocks share one L2;
+      // causal: the heaviest (last) query block of a head first.
+      if (it > 0) break;
+      int w = blockIdx.x;
+      if (s.tiles % 8 == 0) w = (w % 8) * (s.tiles / 8) + w / 8;
+      const int bh = w / s.q_blocks;
+      qb = CAUSAL ? s.q_blocks - 1 - w % s.q_blocks : w % s.q_blocks;
+      b = bh / s.heads;
+      h = bh % s.heads;
+    }
+    // After the first tile: every wave has left the previous tile (its last LDS reads
+    // are not followed by a barrier) before this tile's DMA refills the ring.
+    if (it > 0) barrier_no_fence();
+    // The lane index passes through an empty asm once per tile, so the per-lane addresses
+    // derived from it are formed inside the tile rather than hoisted and held across the
+    // loop (head_dim 64 runs at 128 registers, where that would spill).
+    int lane = threadIdx.x & 63;
+    if constexpr (kPersistent<D>) asm volatile("" : "+v"(lane));
+    const int c = lane & 15, g = lane >> 4;
+    const int kvh = h / s.group;
+    const T* Qh = Q + b * s.q[0] + h * s.q[1] + int64_t(start) * s.q[2];
+    const T* Kh = K + b * s.k[0] + kvh * s.k[1] + int64_t(start) * s.k[2];
+    const T* Vh = V + b * s.v[0] + kvh * s.v[1] + int64_t(start) * s.v[2];
+    T* Oh = O + b * s.o[0] + h * s.o[1] + int64_t(start) * s.o[2];
 
-  // Q fragments (B operand of S^T): query tile qt holds query wq0 + 16 qt + c, k-step kk
-  // features 32 kk + 8 g .. +7.
-  i32x4 qf[2][KS];
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int query = wq0 + 16 * qt + c;
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk)
-      qf[qt][kk] = query < N
-                       ? *reinterpret_cast<const i32x4*>(Qh + query * s.q[2] + kk * 32 + g * 8)
-                       : i32x4{0, 0, 0, 0};
-  }
-  // RoPE: fragments kk and kk + KS/2 hold features 32 kk + 8 g .. +7 and the same + D/2,
-  // so the rotate-half pairs sit in one lane. Queries past the end keep zero tables (their
-  // Q is 0).
-  if (s.rope_cos != nullptr) {
-#pragma unroll
+    const int q0 = qb * BM;
+    const int wq0 = q0 + wave * G::QW;
+
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)Kh, (short)0, k_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)Vh, (short)0, v_bytes, 0x00020000);
+
+    // DMA sources (bytes from the head's base, block-relative row). Rows past the sequence
+    // end are past the buffer extent and read as zero.
+    uint32_t k_src[G::DMA_PER_OP], v_src[G::DMA_PER_OP];
+  #pragma unroll
+    for (int x = 0; x < G::DMA_PER_OP; ++x) {
+      const int id = wave * G::DMA_PER_OP + x;
+      const int row = id * G::ROWS_PER_DMA + lane / G::SLOTS;
+      const int slot = lane % G::SLOTS;
+      k_src[x] = uint32_t(row * s.k[2] + (slot ^ G::kswz(row)) * 8) * 2u;
+      const int granule = (slot >> 1) ^ G::vswz(row);
+      v_src[x] = uint32_t(row * s.v[2] + granule * 16 + (slot & 1) * 8) * 2u;
+    }
+    const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
+    const int kv_blocks = (kv_end + BN - 1) / BN;
+    const int last = kv_blocks - 1;
+    const uint32_t k_blk = uint32_t(BN * s.k[2]) * 2u, v_blk = uint32_t(BN * s.v[2]) * 2u;
+    // The first STAGES - 1 blocks are fetched before anything else.
+  #pragma unroll
+    for (int blk = 0; blk < STAGES - 1; ++blk)
+      dma_block<D>(rk, rv, lds, k_src, v_src, blk, last, k_blk, v_blk, wave);
+
+    // Q fragments (B operand of S^T): query tile qt holds query wq0 + 16 qt + c, k-step kk
+    // features 32 kk + 8 g .. +7.
+    i32x4 qf[2][KS];
+  #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       const int query = wq0 + 16 * qt + c;
-      const int64_t at = int64_t(query) * s.rope_stride + g * 8;
-      const T* cr = static_cast<const T*>(s.rope_cos) + at;
-      const T* sr = static_cast<const T*>(s.rope_sin) + at;
-#pragma unroll
-      for (int kk = 0; kk < KS / 2; ++kk) {
-        const i32x4 cv = query < N ? *reinterpret_cast<const i32x4*>(cr + kk * 32) : i32x4{0, 0, 0, 0};
-        const i32x4 sv = query < N ? *reinterpret_cast<const i32x4*>(sr + kk * 32) : i32x4{0, 0, 0, 0};
-        rope_fragment<T>(qf[qt][kk], qf[qt][kk + KS / 2], cv, sv);
+  #pragma unroll
+      for (int kk = 0; kk < KS; ++kk)
+        qf[qt][kk] = query < N
+                         ? *reinterpret_cast<const i32x4*>(Qh + query * s.q[2] + kk * 32 + g * 8)
+                         : i32x4{0, 0, 0, 0};
+    }
+    // RoPE: fragments kk and kk + KS/2 hold features 32 kk + 8 g .. +7 and the same + D/2,
+    // so the rotate-half pairs sit in one lane. Queries past the end keep zero tables (their
+    // Q is 0).
+    if (s.rope_cos != nullptr) {
+  #pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const int query = wq0 + 16 * qt + c;
+        const int64_t at = int64_t(query) * s.rope_stride + g * 8;
+        const T* cr = static_cast<const T*>(s.rope_cos) + at;
+        const T* sr = static_cast<const T*>(s.rope_sin) + at;
+  #pragma unroll
+        for (int kk = 0; kk < KS / 2; ++kk) {
+          const i32x4 cv = query < N ? *reinterpret_cast<const i32x4*>(cr + kk * 32) : i32x4{0, 0, 0, 0};
+          const i32x4 sv = query < N ? *reinterpret_cast<const i32x4*>(sr + kk * 32) : i32x4{0, 0, 0, 0};
+          rope_fragment<T>(qf[qt][kk], qf[qt][kk + KS / 2], cv, sv);
+        }
       }
     }
-  }
-  // Lane read addresses inside a stage: K row c of key tile kt (+16 kt rows), chunk
-  // 4 kk + g; V rows 4 g + j (+32 per key step, +16 for k-index 4..7), features
-  // 16 ft + 4 q .. +3, with j = c / 4, q = c % 4.
-  uint32_t ka[KS], va[FT];
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) ka[kk] = c * RB + (((4 * kk + g) ^ G::kswz(c)) * 16);
-  {
-    const int row = 4 * g + (c >> 2), q = c & 3;
-#pragma unroll
-    for (int ft = 0; ft < FT; ++ft) va[ft] = OPB + row * RB + ((ft ^ G::vswz(row)) * 32) + q * 8;
-  }
+    // Lane read addresses inside a stage: K row c of key tile kt (+16 kt rows), chunk
+    // 4 kk + g; V rows 4 g + j (+32 per key step, +16 for k-index 4..7), features
+    // 16 ft + 4 q .. +3, with j = c / 4, q = c % 4.
+    uint32_t ka[KS], va[FT];
+  #pragma unroll
+    for (int kk = 0; kk < KS; ++kk) ka[kk] = c * RB + (((4 * kk + g) ^ G::kswz(c)) * 16);
+    {
+      const int row = 4 * g + (c >> 2), q = c & 3;
+  #pragma unroll
+      for (int ft = 0; ft < FT; ++ft) va[ft] = OPB + row * RB + ((ft ^ G::vswz(row)) * 32) + q * 8;
+    }
 
-  // O^T accumulators: acc[ft][qt] register r is feature 16 ft + 4 g + r of query
-  // wq0 + 16 qt + c. st[qt][kt] register r: score of key n0 + 16 kt + 4 g + r.
-  f32x4 acc[FT][2], st[2][4];
-  i32x4 pf[2][2], vu[Units<D>::NV][2];
-#pragma unroll
-  for (int ft = 0; ft < FT; ++ft)
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) acc[ft][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {kNegInf, kNegInf}, l_part[2] = {0.f, 0.f};
-  const float sl2 = s.scale_log2;
+    // O^T accumulators: acc[ft][qt] register r is feature 16 ft + 4 g + r of query
+    // wq0 + 16 qt + c. st[qt][kt] register r: score of key n0 + 16 kt + 4 g + r.
+    f32x4 acc[FT][2], st[2][4];
+    i32x4 pf[2][2], vu[Units<D>::NV][2];
+  #pragma unroll
+    for (int ft = 0; ft < FT; ++ft)
+  #pragma unroll
+      for (int qt = 0; qt < 2; ++qt) acc[ft][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run[2] = {kNegInf, kNegInf}, l_part[2] = {0.f, 0.f};
+    const float sl2 = s.scale_log2;
 
-  // Block 0 landed; simd_of visible.
-  wait_lgkm<0>();
-  wait_vmcnt<(STAGES - 2) * DPB>();
-  barrier_no_fence();
-  // Ping-pong: the two waves that share a SIMD take opposite phases. The workgroup runs
-  // phases t = 0, 1, ... separated by barriers; a wave alternates an MFMA phase M(j)
-  // (S^T of block j, O^T += V^T P^T of block j-1) and a softmax phase V(j), the second
-  // wave of each SIMD one phase behind the first, so one wave's exponentials run while
-  // the other's MFMAs occupy the matrix pipe. Block j is read in phases 2j .. 2j+3; at
-  // the start of phase 2m (m >= 1) its stage's next block m + STAGES - 2 is fetched,
-  // and block m must have landed before phase 2m begins.
-  int grp = 0;
-#pragma unroll
-  for (int w = 0; w < G::WAVES; ++w) grp += (w < wave && simd_of[w] == simd_of[wave]) ? 1 : 0;
-  grp = __builtin_amdgcn_readfirstlane(grp) & 1;
-  const int phases = 2 * kv_blocks + 2;
-  int t = 0;
-  // Block m + STAGES - 2 (m >= 1) is fetched during this wave's MFMA phase of block m
-  // (phase 2m + grp), its DMA_PER_BLOCK instructions spread over the phase's read units;
-  // after the wave's last MFMA phase, at the start of phase 2m + grp (tail mode). Block m+1
-  // was issued by every wave before the end of phase 2m + 1 (grp 0 in phase 2m - 2, grp 1
-  // in 2m - 1), so the wait at the end of each odd phase, which leaves one block's
-  // instructions in flight, still covers it.
-  bool tail = false;
-  int tail_m = 0;
-  auto end_phase = [&]() {
-    if (t & 1) wait_vmcnt<(STAGES - 3) * DPB>();
+    // Block 0 landed; simd_of visible.
+    wait_lgkm<0>();
+    wait_vmcnt<(STAGES - 2) * DPB>();
     barrier_no_fence();
-    ++t;
-    if (tail && tail_m <= kv_blocks && t == 2 * tail_m + grp) {
-      dma_block<D>(rk, rv, lds, k_src, v_src, tail_m + STAGES - 2, last, k_blk, v_blk, wave);
-      ++tail_m;
-    }
-  };
-  // Hook of the MFMA phase of block m: after unit u of nu, the DMA instructions whose
-  // share of the phase ends there (DMA_PER_BLOCK of them over the nu units).
-  auto dma_hook = [&](int m) {
-    return [&, m](int u, int nu) {
-      const int a = (u * DPB) / nu, b2 = ((u + 1) * DPB) / nu;
-      if (b2 != a)
-        dma_one<D>(rk, rv, lds, k_src, v_src, m + STAGES - 2, last, k_blk, v_blk, wave, b2 - 1);
+    // Ping-pong: the two waves that share a SIMD take opposite phases. The workgroup runs
+    // phases t = 0, 1, ... separated by barriers; a wave alternates an MFMA phase M(j)
+    // (S^T of block j, O^T += V^T P^T of block j-1) and a softmax phase V(j), the second
+    // wave of each SIMD one phase behind the first, so one wave's exponentials run while
+    // the other's MFMAs occupy the matrix pipe. Block j is read in phases 2j .. 2j+3; at
+    // the start of phase 2m (m >= 1) its stage's next block m + STAGES - 2 is fetched,
+    // and block m must have landed before phase 2m begins.
+    int grp = 0;
+  #pragma unroll
+    for (int w = 0; w < G::WAVES; ++w) grp += (w < wave && simd_of[w] == simd_of[wave]) ? 1 : 0;
+    grp = __builtin_amdgcn_readfirstlane(grp) & 1;
+    const int phases = 2 * kv_blocks + 2;
+    int t = 0;
+    // Block m + STAGES - 2 (m >= 1) is fetched during this wave's MFMA phase of block m
+    // (phase 2m + grp), its DMA_PER_BLOCK instructions spread over the phase's read units;
+    // after the wave's last MFMA phase, at the start of phase 2m + grp (tail mode). Block m+1
+    // was issued by every wave before the end of phase 2m + 1 (grp 0 in phase 2m - 2, grp 1
+    // in 2m - 1), so the wait at the end of each odd phase, which leaves one block's
+    // instructions in flight, still covers it.
+    bool tail = false;
+    int tail_m = 0;
+    auto end_phase = [&]() {
+      if (t & 1) wait_vmcnt<(STAGES - 3) * DPB>();
+      barrier_no_fence();
+      ++t;
+      if (tail && tail_m <= kv_blocks && t == 2 * tail_m + grp) {
+        dma_block<D>(rk, rv, lds, k_src, v_src, tail_m + STAGES - 2, last, k_blk, v_blk, wave);
+        ++tail_m;
+      }
     };
-  };
-  auto no_hook = [](int, int) {};
-  auto kbase = [&](int j) { return lds_base + (j % STAGES) * STB; };
-
-  // Softmax phase of block j: P = exp2(S * scale * log2(e) - m) into pf, the running
-  // statistics updated. The reference maximum m_run only moves when the block's maximum
-  // exceeds it by more than kLazyRescale (log2 units): exponentials stay
-  // <= 2^kLazyRescale, and O and l are rescaled in few blocks instead of whenever one of
-  // the wave's 32 maxima grows. O = acc / l and the log-sum-exp m_run + log2(l) do not
-  // depend on which reference is used.
-  auto softmax_phase = [&](int j) {
-    const int n0 = j * BN;
-    const bool need_mask = n0 + BN > N || (CAUSAL && n0 + BN - 1 > wq0);
-    if (__builtin_expect(need_mask, 0)) {
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          const int k0 = n0 + 16 * kt + 4 * g;  // the lane's first key of this tile
-          int lim = N - 1 - k0;                 // last valid offset from k0
-          if (CAUSAL) lim = min(lim, wq0 + 16 * qt + c - k0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (r > lim) st[qt][kt][r] = kNegInf;
-        }
-    }
-    if constexpr (D == 128) {
-      // Exponentials against the current reference first. A lane whose 16 exponentials of a
-      // query sum to at most 2^kLazyRescale has none above it, so when no lane of the wave
-      // exceeds that sum no reference moves and no maximum is needed. Otherwise the column
-      // maxima are formed from the scores, which are still intact, and the queries whose
-      // reference moves are recomputed.
-      f32x4 p[2][4];
-      float sum[2];
-      auto exps = [&](int qt) {
-        const float neg = -m_run[qt];
-  #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-  #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            p[qt][kt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qt][kt][r], sl2, neg));
-        float s0 = p[qt][0][0];
-  #pragma unroll
-        for (int i = 1; i < 16; ++i) s0 += p[qt][i / 4][i % 4];
-        sum[qt] = s0;
+    // Hook of the MFMA phase of block m: after unit u of nu, the DMA instructions whose
+    // share of the phase ends there (DMA_PER_BLOCK of them over the nu units).
+    auto dma_hook = [&](int m) {
+      return [&, m](int u, int nu) {
+        const int a = (u * DPB) / nu, b2 = ((u + 1) * DPB) / nu;
+        if (b2 != a)
+          dma_one<D>(rk, rv, lds, k_src, v_src, m + STAGES - 2, last, k_blk, v_blk, wave, b2 - 1);
       };
-      exps(0);
-      exps(1);
-      constexpr float kLazyLimit = 256.f;  // 2^kLazyRescale
-      if (__builtin_expect(
-              __builtin_amdgcn_ballot_w64(!(sum[0] <= kLazyLimit) || !(sum[1] <= kLazyLimit)) != 0,
-              0)) {
+    };
+    auto no_hook = [](int, int) {};
+    auto kbase = [&](int j) { return lds_base + (j % STAGES) * STB; };
+
+    // Softmax phase of block j: P = exp2(S * scale * log2(e) - m) into pf, the running
+    // statistics updated. The reference maximum m_run only moves when the block's maximum
+    // exceeds it by more than kLazyRescale (log2 units): exponentials stay
+    // <= 2^kLazyRescale, and O and l are rescaled in few blocks instead of whenever one of
+    // the wave's 32 maxima grows. O = acc / l and the log-sum-exp m_run + log2(l) do not
+    // depend on which reference is used.
+    auto softmax_phase = [&](int j) {
+      const int n0 = j * BN;
+      const bool need_mask = n0 + BN > N || (CAUSAL && n0 + BN - 1 > wq0);
+      if (__builtin_expect(need_mask, 0)) {
+  #pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+  #pragma unroll
+          for (int kt = 0; kt < 4; ++kt) {
+            const int k0 = n0 + 16 * kt + 4 * g;  // the lane's first key of this tile
+            int lim = N - 1 - k0;                 // last valid offset from k0
+            if (CAUSAL) lim = min(lim, wq0 + 16 * qt + c - k0);
+  #pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (r > lim) st[qt][kt][r] = kNegInf;
+          }
+      }
+      if constexpr (D == 128) {
+        // Exponentials against the current reference first. A lane whose 16 exponentials of a
+        // query sum to at most 2^kLazyRescale has none above it, so when no lane of the wave
+        // exceeds that sum no reference moves and no maximum is needed. Otherwise the column
+        // maxima are formed from the scores, which are still intact, and the queries whose
+        // reference moves are recomputed.
+        f32x4 p[2][4];
+        float sum[2];
+        auto exps = [&](int qt) {
+          const float neg = -m_run[qt];
+    #pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+    #pragma unroll
+            for (int r = 0; r < 4; ++r)
+              p[qt][kt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qt][kt][r], sl2, neg));
+          float s0 = p[qt][0][0];
+    #pragma unroll
+          for (int i = 1; i < 16; ++i) s0 += p[qt][i / 4][i % 4];
+          sum[qt] = s0;
+        };
+        exps(0);
+        exps(1);
+        constexpr float kLazyLimit = 256.f;  // 2^kLazyRescale
+        if (__builtin_expect(
+                __builtin_amdgcn_ballot_w64(!(sum[0] <= kLazyLimit) || !(sum[1] <= kLazyLimit)) != 0,
+                0)) {
+    #pragma unroll
+          for (int qt = 0; qt < 2; ++qt) {
+            float mx = kNegInf;
+    #pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+    #pragma unroll
+              for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[qt][kt][r]);
+            const float bm = max_over_column(mx) * sl2;
+            const bool move = bm > m_run[qt] + kLazyRescale;
+            if (__builtin_amdgcn_ballot_w64(move)) {
+              const float m_new = move ? bm : m_run[qt];
+              const float alpha = move ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.f;
+              l_part[qt] *= alpha;
+    #pragma unroll
+              for (int ft = 0; ft < FT; ++ft) acc[ft][qt] *= alpha;
+              m_run[qt] = m_new;
+              exps(qt);
+            }
+          }
+        }
+    #pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+          l_part[qt] += sum[qt];
+          pf[qt][0] = acc_frag2<T>(p[qt][0], p[qt][1]);
+          pf[qt][1] = acc_frag2<T>(p[qt][2], p[qt][3]);
+        }
+      } else {
+        // head_dim 64 (128 registers): the exponentials overwrite the scores, so the maximum
+        // comes first. A column's maximum exceeds the threshold only if one of its four
+        // lanes' does: the cross-lane reduction runs only when some lane of the wave sees
+        // such a maximum.
+        float mx[2], m_new[2];
+        bool move[2];
   #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
-          float mx = kNegInf;
+          mx[qt] = kNegInf;
   #pragma unroll
           for (int kt = 0; kt < 4; ++kt)
   #pragma unroll
-            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[qt][kt][r]);
-          const float bm = max_over_column(mx) * sl2;
-          const bool move = bm > m_run[qt] + kLazyRescale;
-          if (__builtin_amdgcn_ballot_w64(move)) {
-            const float m_new = move ? bm : m_run[qt];
-            const float alpha = move ? __builtin_amdgcn_exp2f(m_run[qt] - m_new) : 1.f;
+            for (int r = 0; r < 4; ++r) mx[qt] = fmaxf(mx[qt], st[qt][kt][r]);
+          move[qt] = mx[qt] * sl2 > m_run[qt] + kLazyRescale;
+          m_new[qt] = m_run[qt];
+        }
+        if (__builtin_expect(__builtin_amdgcn_ballot_w64(move[0] || move[1]) != 0, 0)) {
+  #pragma unroll
+          for (int qt = 0; qt < 2; ++qt) {
+            const float bm = max_over_column(mx[qt]) * sl2;
+            move[qt] = bm > m_run[qt] + kLazyRescale;
+            m_new[qt] = move[qt] ? bm : m_run[qt];
+          }
+        }
+  #pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+          const float neg = -m_new[qt];
+          float sum = 0.f;
+  #pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qt][kt][r], sl2, neg));
+              st[qt][kt][r] = pv;
+              sum += pv;
+            }
+          if (__builtin_amdgcn_ballot_w64(move[qt])) {
+            const float alpha = move[qt] ? __builtin_amdgcn_exp2f(m_run[qt] - m_new[qt]) : 1.f;
             l_part[qt] *= alpha;
   #pragma unroll
             for (int ft = 0; ft < FT; ++ft) acc[ft][qt] *= alpha;
-            m_run[qt] = m_new;
-            exps(qt);
           }
+          l_part[qt] += sum;
+          m_run[qt] = m_new[qt];
+          pf[qt][0] = acc_frag2<T>(st[qt][0], st[qt][1]);
+          pf[qt][1] = acc_frag2<T>(st[qt][2], st[qt][3]);
         }
       }
+    };
+
+    // This wave multiplies a prefix of the workgroup's blocks (causal: those starting at or
+    // before its last query); every wave takes part in every phase's barrier and loads.
+    const int n = CAUSAL ? min(kv_blocks, (wq0 + G::QW - 1) / BN + 1) : kv_blocks;
+    // The loop is entered after M(0) and leaves before V(n-1) (with the softmax phase first
+    // in the body the compiler keeps one copy of the O accumulators across the back edge).
+    // A phase's results are pinned before its closing barrier: the barrier orders memory
+    // only, and the compiler would otherwise sink register work (the exponentials, the
+    // MFMA chains) into the next phase, where it runs beside the partner wave's same kind
+    // of work.
+    auto pin_mfma = [&]() {
+  #pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+  #pragma unroll
+        for (int kt = 0; kt < 4; ++kt) pin(st[qt][kt]);
+  #pragma unroll
+      for (int ft = 0; ft < FT; ++ft)
+  #pragma unroll
+        for (int qt = 0; qt < 2; ++qt) pin(acc[ft][qt]);
+    };
+    // The softmax phase ends by issuing the first PREFETCH V units of the next MFMA phase
+    // (block j's V tile has landed since phase 2j).
+    auto pin_softmax = [&](int j) {
   #pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
-        l_part[qt] += sum[qt];
-        pf[qt][0] = acc_frag2<T>(p[qt][0], p[qt][1]);
-        pf[qt][1] = acc_frag2<T>(p[qt][2], p[qt][3]);
+        pin(pf[qt][0]);
+        pin(pf[qt][1]);
+        asm volatile("" : "+v"(l_part[qt]), "+v"(m_run[qt]));
       }
-    } else {
-      // head_dim 64 (128 registers): the exponentials overwrite the scores, so the maximum
-      // comes first. A column's maximum exceeds the threshold only if one of its four
-      // lanes' does: the cross-lane reduction runs only when some lane of the wave sees
-      // such a maximum.
-      float mx[2], m_new[2];
-      bool move[2];
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        mx[qt] = kNegInf;
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) mx[qt] = fmaxf(mx[qt], st[qt][kt][r]);
-        move[qt] = mx[qt] * sl2 > m_run[qt] + kLazyRescale;
-        m_new[qt] = m_run[qt];
-      }
-      if (__builtin_expect(__builtin_amdgcn_ballot_w64(move[0] || move[1]) != 0, 0)) {
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-          const float bm = max_over_column(mx[qt]) * sl2;
-          move[qt] = bm > m_run[qt] + kLazyRescale;
-          m_new[qt] = move[qt] ? bm : m_run[qt];
-        }
-      }
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        const float neg = -m_new[qt];
-        float sum = 0.f;
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qt][kt][r], sl2, neg));
-            st[qt][kt][r] = pv;
-            sum += pv;
-          }
-        if (__builtin_amdgcn_ballot_w64(move[qt])) {
-          const float alpha = move[qt] ? __builtin_amdgcn_exp2f(m_run[qt] - m_new[qt]) : 1.f;
-          l_part[qt] *= alpha;
-#pragma unroll
-          for (int ft = 0; ft < FT; ++ft) acc[ft][qt] *= alpha;
-        }
-        l_part[qt] += sum;
-        m_run[qt] = m_new[qt];
-        pf[qt][0] = acc_frag2<T>(st[qt][0], st[qt][1]);
-        pf[qt][1] = acc_frag2<T>(st[qt][2], st[qt][3]);
-      }
-    }
-  };
-
-  // This wave multiplies a prefix of the workgroup's blocks (causal: those starting at or
-  // before its last query); every wave takes part in every phase's barrier and loads.
-  const int n = CAUSAL ? min(kv_blocks, (wq0 + G::QW - 1) / BN + 1) : kv_blocks;
-  // The loop is entered after M(0) and leaves before V(n-1) (with the softmax phase first
-  // in the body the compiler keeps one copy of the O accumulators across the back edge).
-  // A phase's results are pinned before its closing barrier: the barrier orders memory
-  // only, and the compiler would otherwise sink register work (the exponentials, the
-  // MFMA chains) into the next phase, where it runs beside the partner wave's same kind
-  // of work.
-  auto pin_mfma = [&]() {
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) pin(st[qt][kt]);
-#pragma unroll
-    for (int ft = 0; ft < FT; ++ft)
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) pin(acc[ft][qt]);
-  };
-  // The softmax phase ends by issuing the first PREFETCH V units of the next MFMA phase
-  // (block j's V tile has landed since phase 2j).
-  auto pin_softmax = [&](int j) {
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      pin(pf[qt][0]);
-      pin(pf[qt][1]);
-      asm volatile("" : "+v"(l_part[qt]), "+v"(m_run[qt]));
-    }
-#pragma unroll
-    for (int u = 0; u < Units<D>::PREFETCH; ++u) read_v_unit<D>(vu, kbase(j), va, u);
-  };
-  if (grp) end_phase();
-  mfma_phase<T, D, true, false>(no_hook, kbase(0), 0, ka, va, qf, st, pf, acc, vu);
-  pin_mfma();
-  end_phase();
-  for (int j = 1; j < n; ++j) {
-    softmax_phase(j - 1);
-    pin_softmax(j - 1);
-    end_phase();
-    mfma_phase<T, D, true, true>(dma_hook(j), kbase(j), kbase(j - 1), ka, va, qf, st, pf, acc, vu);
+  #pragma unroll
+      for (int u = 0; u < Units<D>::PREFETCH; ++u) read_v_unit<D>(vu, kbase(j), va, u);
+    };
+    if (grp) end_phase();
+    mfma_phase<T, D, true, false>(no_hook, kbase(0), 0, ka, va, qf, st, pf, acc, vu);
     pin_mfma();
     end_phase();
-  }
-  softmax_phase(n - 1);
-  pin_softmax(n - 1);
-  end_phase();
-  mfma_phase<T, D, false, true>(dma_hook(n), 0, kbase(n - 1), ka, va, qf, st, pf, acc, vu);
-  tail = true;
-  tail_m = n + 1;
-  while (t < phases - 1) end_phase();
-  // No DMA may still be writing when the workgroup's LDS is released.
-  wait_vmcnt<0>();
+    for (int j = 1; j < n; ++j) {
+      softmax_phase(j - 1);
+      pin_softmax(j - 1);
+      end_phase();
+      mfma_phase<T, D, true, true>(dma_hook(j), kbase(j), kbase(j - 1), ka, va, qf, st, pf, acc, vu);
+      pin_mfma();
+      end_phase();
+    }
+    softmax_phase(n - 1);
+    pin_softmax(n - 1);
+    end_phase();
+    mfma_phase<T, D, false, true>(dma_hook(n), 0, kbase(n - 1), ka, va, qf, st, pf, acc, vu);
+    tail = true;
+    tail_m = n + 1;
+    while (t < phases - 1) end_phase();
+    // No DMA may still be writing when the workgroup's LDS is released.
+    wait_vmcnt<0>();
 
-  // O = O^T / l: acc[ft][qt] register r is feature 16 ft + 4 g + r.
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const float l = sum_over_column(l_part[qt]);
-    const float inv = 1.0f / l;
-    const int query = wq0 + 16 * qt + c;
-    if (query < N) {
-      T* orow = Oh + query * s.o[2];
-#pragma unroll
-      for (int ft = 0; ft < FT; ++ft) {
-        uint2 u;
-        u.x = pack2<T>(acc[ft][qt][0] * inv, acc[ft][qt][1] * inv);
-        u.y = pack2<T>(acc[ft][qt][2] * inv, acc[ft][qt][3] * inv);
-        *reinterpret_cast<uint2*>(orow + ft * 16 + g * 4) = u;
-      }
-      if (lse != nullptr && g == 0) {
-        const int64_t at = s.cu != nullptr ? int64_t(h) * s.total + start + query
-                                           : (int64_t(b) * s.heads + h) * N + query;
-        lse[at] = m_run[qt] + __log2f(l);
+    // O = O^T / l: acc[ft][qt] register r is feature 16 ft + 4 g + r.
+  #pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      const float l = sum_over_column(l_part[qt]);
+      const float inv = 1.0f / l;
+      const int query = wq0 + 16 * qt + c;
+      if (query < N) {
+        T* orow = Oh + query * s.o[2];
+  #pragma unroll
+        for (int ft = 0; ft < FT; ++ft) {
+          uint2 u;
+          u.x = pack2<T>(acc[ft][qt][0] * inv, acc[ft][qt][1] * inv);
+          u.y = pack2<T>(acc[ft][qt][2] * inv, acc[ft][qt][3] * inv);
+          *reinterpret_cast<uint2*>(orow + ft * 16 + g * 4) = u;
+        }
+        if (lse != nullptr && g == 0) {
+          const int64_t at = s.cu != nullptr ? int64_t(h) * s.total + start + query
+                                             : (int64_t(b) * s.heads + h) * N + query;
+          lse[at] = m_run[qt] + __log2f(l);
+        }
       }
     }
-  }
+  }  // tiles
 }
 
+// Varlen and head_dim 64: one workgroup per tile. Otherwise `items` schedule units (tiles,
+// or causal pairs of tiles), dealt to at most as many persistent workgroups as the device
+// holds.
 template <typename T, int D>
-void launch(bool causal, dim3 grid, hipStream_t st, const void* q, const void* k, const void* v,
-            void* o, float* lse, const Shape& s) {
+void launch(bool causal, int64_t items, hipStream_t st, const void* q, const void* k,
+            const void* v, void* o, float* lse, const Shape& s) {
+  const void* fn = causal ? reinterpret_cast<const void*>(attn_fwd_dma_kernel<T, D, true>)
+                          : reinterpret_cast<const void*>(attn_fwd_dma_kernel<T, D, false>);
+  int64_t n = kPersistent<D> ? items : int64_t(s.tiles);
+  if (s.cu == nullptr && kPersistent<D>) {
+    const int resident = tk::resident_workgroups(fn, kThreads);
+    if (resident > 0 && resident < n) n = resident;
+  }
+  const dim3 grid(static_cast<unsigned>(n));
   if (causal)
     hipLaunchKernelGGL((attn_fwd_dma_kernel<T, D, true>), grid, dim3(kThreads), 0, st,
                        (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, s);
@@ -688,13 +769,15 @@ void attn_fwd_dma_launch(int dtype, const void* q, const void* k, const void* v,
                                   : (int)(s.q_blocks * batch * heads);
   s.k_bytes = (uint32_t)head_extent_bytes(seq, head_dim, k_strides[2]);
   s.v_bytes = (uint32_t)head_extent_bytes(seq, head_dim, v_strides[2]);
-  const dim3 grid(static_cast<unsigned>(s.tiles));
+  const int64_t items = cu_seqlens == nullptr && causal
+                            ? batch * heads * ((s.q_blocks + 1) / 2)
+                            : int64_t(s.tiles);
   if (dtype == TK_DTYPE_F16) {
-    if (head_dim == 64) launch<_Float16, 64>(causal, grid, stream, q, k, v, o, lse, s);
-    else launch<_Float16, 128>(causal, grid, stream, q, k, v, o, lse, s);
+    if (head_dim == 64) launch<_Float16, 64>(causal, items, stream, q, k, v, o, lse, s);
+    else launch<_Float16, 128>(causal, items, stream, q, k, v, o, lse, s);
   } else {
-    if (head_dim == 64) launch<__bf16, 64>(causal, grid, stream, q, k, v, o, lse, s);
-    else launch<__bf16, 128>(causal, grid, stream, q, k, v, o, lse, s);
+    if (head_dim == 64) launch<__bf16, 64>(causal, items, stream, q, k, v, o, lse, s);
+    else launch<__bf16, 128>(causal, items, stream, q, k, v, o, lse, s);
   }
 }
 
