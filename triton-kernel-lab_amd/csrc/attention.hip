@@ -22,9 +22,6 @@
 //  * Row-major LDS tiles ([64][D]) and transposed tiles ([D][64]) store 16-byte
 //    chunk c of row r at chunk c ^ (r % 8): 8 consecutive rows read by one
 //    operand load hit 8 distinct bank groups.
-#include <mutex>
-#include <vector>
-
 #include "attention.hpp"
 #include "tk_common.hpp"
 
@@ -1120,28 +1117,3 @@ extern "C" int tk_attn_bwd_dq_varlen(int dtype, const void* q, const void* k, co
   return tk::check_launch("attn_bwd_dq_varlen");
 }
 
-namespace tk {
-
-int resident_workgroups(const void* kernel, int threads) {
-  struct Entry {
-    int device;
-    const void* kernel;
-    int count;
-  };
-  static std::mutex mu;
-  static std::vector<Entry> cache;
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess) return 0;
-  std::lock_guard<std::mutex> lock(mu);
-  for (const Entry& e : cache)
-    if (e.device == device && e.kernel == kernel) return e.count;
-  int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
-    return 0;
-  const int count = per_cu > 0 && cus > 0 ? per_cu * cus : 0;
-  cache.push_back({device, kernel, count});
-  return count;
-}
-
-}  // namespace tk

@@ -12,11 +12,6 @@
 
 namespace tk {
 
-// Workgroups of `threads` threads of `kernel` the current device holds at once (its CUs
-// times the workgroups one CU holds), cached per device and kernel; 0 when the runtime
-// cannot say.
-int resident_workgroups(const void* kernel, int threads);
-
 // True when each head's K and V rows span less than 2 GiB (32-bit buffer offsets).
 // The caller has already checked dtype, head_dim and 16-byte row alignment.
 bool attn_fwd_dma_applies(int64_t seq, int64_t head_dim, const int64_t* k_strides,

@@ -236,6 +236,13 @@ __device__ __forceinline__ void pin_sub_rows(SubRows& r) {
 
 // ---------------------------------------------------------------- dK / dV
 
+// Equal lengths: one workgroup per causal pair of key blocks (paired_tile) in the head_dim
+// 64 kernel (causal B4 H32 N8192 2.13-2.23 -> 2.11-2.16 ms). The head_dim 128 kernel keeps
+// one key block per workgroup: there a two-block loop spilled 97 registers around the key
+// block's stream (3.86 -> 4.10 ms).
+template <int D>
+constexpr bool kPairedKv = D == 64;
+
 template <typename T, int D, bool CAUSAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads1, kThreads1),
                           amdgpu_waves_per_eu(D == 64 ? 2 : 1, D == 64 ? 2 : 1))) void
@@ -250,240 +257,256 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
   constexpr int NDMA = 2 * G::DMA_PER_TILE + 1; // per wave per block
   __shared__ __attribute__((aligned(1024))) char lds[G::STAGES * STB];
 
-  // Workgroup -> (batch, KV head, key block). The KV head's `group` query heads are
+  // Workgroup -> (batch, KV head, key blocks). The KV head's `group` query heads are
   // streamed one after another as one sequence of query blocks (virtual block J: head
   // J / nblk), so dK and dV sum over the group in a fixed order with a single writer.
-  // Varlen: the heavy-first schedule over every sequence's key blocks (level = blocks
-  // after this one, so causal's longest query ranges start first), KV heads interleaved
-  // over the XCDs.
-  const int kv_heads = s.heads / s.group;
-  int b, kvh, kblk;
-  if (s.cu != nullptr) {
-    kvh = varlen_head(blockIdx.x, kv_heads);
-    VarlenTile vt;
-    if (!varlen_tile(s.cu, s.batch, s.total, s.seq, G::BW, blockIdx.x / kv_heads, vt)) return;
-    b = vt.b;
-    const int nb = (varlen_rows(s.cu, b, s.total, s.seq).n + G::BW - 1) / G::BW;
-    kblk = nb - 1 - vt.level;
-  } else {
-    int w = blockIdx.x;
-    if (s.kv_tiles % 8 == 0) w = (w % 8) * (s.kv_tiles / 8) + w / 8;
-    const int bkv = w / s.blocks_per_head;
-    kblk = w % s.blocks_per_head;
-    b = bkv / kv_heads;
-    kvh = bkv % kv_heads;
-  }
-  const SeqSpan sp = seq_span<D>(s, b);
-  const int N = sp.n;
-  const int64_t sn = s.st[2], kn = s.kst[2];
-  const int64_t kvbase = b * s.kst[0] + kvh * s.kst[1] + int64_t(sp.start) * kn;
-  const int64_t qbase = b * s.st[0] + int64_t(kvh) * s.group * s.st[1] + int64_t(sp.start) * sn;
-  // Statistics of the group's first query head; head g of the group is g heads later.
-  const int64_t stat_head = s.cu != nullptr ? s.total : N;
-  const int64_t stat0 = s.cu != nullptr
-                            ? int64_t(kvh) * s.group * s.total + sp.start
-                            : (int64_t(b) * s.heads + int64_t(kvh) * s.group) * N;
-
-  const int lane = threadIdx.x & 63;
+  // Equal lengths: the key blocks paired_tile deals this workgroup (causal: blocks i and
+  // NB-1-i of one KV head). Varlen: one key block per workgroup, the heavy-first schedule
+  // over every sequence's key blocks (level = blocks after this one, so causal's longest
+  // query ranges start first), KV heads interleaved over the XCDs.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int l32 = lane & 31, hi = lane >> 5;
-  const int kb0 = kblk * G::BW;
-  if (kb0 >= N) return;  // varlen: past this sequence's end (uniform)
-  const int wk0 = kb0 + wave * G::LW;
-  const int key = wk0 + l32;  // this lane's key (column of S and dP)
-
-  // K and V fragments of this wave's keys (B operands of S = Q K^T and dP = dO V^T).
-  i32x4 kf[KS], vf[KS];
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) {
-    const int64_t off = kvbase + int64_t(key) * kn + kk * 16 + hi * 8;
-    kf[kk] = key < N ? *reinterpret_cast<const i32x4*>(K + off) : i32x4{0, 0, 0, 0};
-    vf[kk] = key < N ? *reinterpret_cast<const i32x4*>(V + off) : i32x4{0, 0, 0, 0};
-  }
-
-  // Query-side sources of the group's first head; head g adds g head strides. Each
-  // head gets its own buffer extent, so rows past the sequence end read as zero.
-  const T* q_head0 = Q + qbase;
-  const T* do_head0 = dO + qbase;
-  const float* stat_head0 = (wave < 2 ? lse : delta) + stat0;
-  const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
-
-  uint32_t q_src[G::DMA_PER_TILE];
-#pragma unroll
-  for (int x = 0; x < G::DMA_PER_TILE; ++x) q_src[x] = tile_src<D, true>(wave, x, lane, sn);
-  const uint32_t st_src = uint32_t((wave & 1) * 32 + l32) * 4u;
-  const uint32_t blk_bytes = uint32_t(BB * sn) * 2u;
-
-  const int first = CAUSAL ? kb0 / BB : 0;  // first query block with a query >= kb0
-  const int nblk = (N + BB - 1) / BB - first;
-
-  // DMA of the next block in stream order (head dg of the group, relative block dj) into
-  // stage ST; past the end the last block is reloaded. Blocks are fetched strictly in
-  // order, so a cursor replaces a division, and the head's buffer resources are rebuilt
-  // only when the cursor moves to the next head.
-  int dg = 0, dj = 0;
-  __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)q_head0, (short)0,
-                                                                sp.q_bytes, 0x00020000);
-  __amdgpu_buffer_rsrc_t rdo = __builtin_amdgcn_make_buffer_rsrc((void*)do_head0, (short)0,
-                                                                 sp.q_bytes, 0x00020000);
-  __amdgpu_buffer_rsrc_t rst = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)stat_head0, (short)0, uint32_t(N) * 4u, 0x00020000);
-#define TK_BWD_DKDV_DMA(ST)                                                                 \
-  {                                                                                         \
-    const int qb_ = first + (dg >= s.group ? nblk - 1 : dj);                                \
-    dma_tiles<D>(rq, rdo, lds + (ST) * STB, q_src, q_src, qb_ * blk_bytes, wave);           \
-    dma_stats(rst, lds + (ST) * STB + 2 * TILE + wave * 128, st_src, qb_ * BB * 4, lane);   \
-    if (dg < s.group && ++dj == nblk) {                                                     \
-      dj = 0;                                                                               \
-      if (++dg < s.group) {                                                                 \
-        const int64_t h_ = int64_t(dg) * s.st[1];                                           \
-        rq = __builtin_amdgcn_make_buffer_rsrc((void*)(q_head0 + h_), (short)0,             \
-                                               sp.q_bytes, 0x00020000);                     \
-        rdo = __builtin_amdgcn_make_buffer_rsrc((void*)(do_head0 + h_), (short)0,           \
-                                                sp.q_bytes, 0x00020000);                    \
-        rst = __builtin_amdgcn_make_buffer_rsrc((void*)(stat_head0 + dg * stat_head),       \
-                                                (short)0, uint32_t(N) * 4u, 0x00020000);    \
-      }                                                                                     \
-    }                                                                                       \
-  }
-
-  f32x16 acc_dv[DT], acc_dk[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc_dv[dt][r] = acc_dk[dt][r] = 0.f;
-
-  uint32_t qa[KS], ta0[DT], ta8[DT];
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) qa[kk] = frag_addr<D, true>(lane, kk);
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    ta0[dt] = tr_addr<D>(lane, dt, 0);
-    ta8[dt] = tr_addr<D>(lane, dt, 8);
-  }
-  const uint32_t sa = (hi * 4) * 4;  // statistics: query offset 4 hi within each group of 8
-  const float sl2 = s.scale_log2;
-
-  TK_BWD_DKDV_DMA(0)
-  TK_BWD_DKDV_DMA(1)
-  int stage = 0, fill = 2;
-  // Causal: this wave's blocks start at the first one holding a query >= its first key.
-  const int wave_first = CAUSAL ? min(nblk, (wk0 / BB) - first) : 0;
-  for (int g = 0; g < s.group; ++g) {
-  int j = 0;
-  for (; j < wave_first; ++j) {
-    wait_vmcnt<NDMA>();
-    barrier_no_fence();
-    TK_BWD_DKDV_DMA(fill)
-    stage = stage + 1 == G::STAGES ? 0 : stage + 1;
-    fill = fill + 1 == G::STAGES ? 0 : fill + 1;
-  }
-  for (; j < nblk; ++j) {
-    wait_vmcnt<NDMA>();
-    barrier_no_fence();
-    TK_BWD_DKDV_DMA(fill)
-    const int q0 = (first + j) * BB;
-    // Lane addresses for this stage; the dO tile and the 16-row steps are immediates.
-    const uint32_t sbase = lds_base + stage * STB;
-    uint32_t qs_a[KS], t0[DT], t8[DT];
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) qs_a[kk] = sbase + qa[kk];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      t0[dt] = sbase + ta0[dt];
-      t8[dt] = sbase + ta8[dt];
+  const int kv_heads = s.heads / s.group;
+  for (int it = 0; (kPairedKv<D> && CAUSAL) || it == 0; ++it) {
+    int b, kvh, kblk;
+    if (s.cu != nullptr) {
+      if (it > 0) break;
+      kvh = varlen_head(blockIdx.x, kv_heads);
+      VarlenTile vt;
+      if (!varlen_tile(s.cu, s.batch, s.total, s.seq, G::BW, blockIdx.x / kv_heads, vt)) break;
+      b = vt.b;
+      const int nb = (varlen_rows(s.cu, b, s.total, s.seq).n + G::BW - 1) / G::BW;
+      kblk = nb - 1 - vt.level;
+    } else if constexpr (kPairedKv<D> && CAUSAL) {
+      int bkv;
+      if (!paired_tile(it, s.kv_tiles / s.blocks_per_head, s.blocks_per_head, bkv, kblk))
+        break;
+      b = bkv / kv_heads;
+      kvh = bkv % kv_heads;
+    } else {
+      int w = blockIdx.x;
+      if (s.kv_tiles % 8 == 0) w = (w % 8) * (s.kv_tiles / 8) + w / 8;
+      const int bkv = w / s.blocks_per_head;
+      kblk = w % s.blocks_per_head;
+      b = bkv / kv_heads;
+      kvh = bkv % kv_heads;
     }
-    const uint32_t st_a = sbase + 2 * TILE + sa;
-    const bool need_mask = CAUSAL && q0 < wk0 + G::LW - 1;
+    // After the first key block: every wave has left the previous block (its last LDS
+    // reads are not followed by a barrier) before this block's DMA refills the ring.
+    if (it > 0) barrier_no_fence();
+    const SeqSpan sp = seq_span<D>(s, b);
+    const int N = sp.n;
+    const int64_t sn = s.st[2], kn = s.kst[2];
+    const int64_t kvbase = b * s.kst[0] + kvh * s.kst[1] + int64_t(sp.start) * kn;
+    const int64_t qbase = b * s.st[0] + int64_t(kvh) * s.group * s.st[1] + int64_t(sp.start) * sn;
+    // Statistics of the group's first query head; head g of the group is g heads later.
+    const int64_t stat_head = s.cu != nullptr ? s.total : N;
+    const int64_t stat0 = s.cu != nullptr
+                              ? int64_t(kvh) * s.group * s.total + sp.start
+                              : (int64_t(b) * s.heads + int64_t(kvh) * s.group) * N;
 
-    // Two sub-blocks of 32 queries (query tile mt); each sub-block's transposed reads are
-    // issued before its softmax arithmetic.
+    // The lane index passes through an empty asm once per key block, so the per-lane
+    // addresses derived from it are formed inside the block rather than held across the loop.
+    int lane = threadIdx.x & 63;
+    if constexpr (kPairedKv<D> && CAUSAL) asm volatile("" : "+v"(lane));
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int kb0 = kblk * G::BW;
+    if (kb0 >= N) break;  // varlen: past this sequence's end (uniform)
+    const int wk0 = kb0 + wave * G::LW;
+    const int key = wk0 + l32;  // this lane's key (column of S and dP)
+
+    // K and V fragments of this wave's keys (B operands of S = Q K^T and dP = dO V^T).
+    i32x4 kf[KS], vf[KS];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      SubRows rows;
-      read_sub_rows<D>(rows, mt, qs_a, st_a);
-      wait_lgkm<0>();
-      pin_sub_rows<D>(rows);
-      // S = Q K^T and dP = dO V^T for 32 queries x this wave's 32 keys.
-      f32x16 sc, dp;
-      {
-        const f32x16 z = {};
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk) {
-          sc = Mma<T>::run(rows.q[kk], kf[kk], kk == 0 ? z : sc);
-          dp = Mma<T>::run(rows.o[kk], vf[kk], kk == 0 ? z : dp);
-        }
-      }
-      i32x4 to[2][DT], tq[2][DT];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          to[i][dt] = read_tr_step<RB, TILE>(2 * mt + i, t0[dt], t8[dt]);
-          tq[i][dt] = read_tr_step<RB>(2 * mt + i, t0[dt], t8[dt]);
-        }
-      // Causal: keys after a query get S = -inf (exp2 -> 0); only diagonal blocks.
-      if (__builtin_expect(need_mask, 0)) {
-        const int lim = q0 + mt * 32 + 4 * hi - key;  // key <= query  <=>  offset >= -lim
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (acc_row(r, 0) + lim < 0) sc[r] = kNegInf;
-      }
-      // P = exp2(S c - lse), dS = P (dP - delta); register r holds query
-      // q0 + 32 mt + 8 (r / 4) + 4 hi + r % 4.
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float l = __int_as_float(rows.lse[r >> 2][r & 3]);
-        const float dl = __int_as_float(rows.dlt[r >> 2][r & 3]);
-        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], sl2, -l));
-        sc[r] = pv;
-        dp[r] = pv * (dp[r] - dl);
-      }
-      const i32x4 pf[2] = {acc_frag<T>(sc, 0), acc_frag<T>(sc, 1)};
-      const i32x4 df[2] = {acc_frag<T>(dp, 0), acc_frag<T>(dp, 1)};
-      wait_lgkm<0>();
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          pin(to[i][dt]);
-          pin(tq[i][dt]);
-        }
-      // dV^T += dO^T P and dK^T += Q^T dS.
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          acc_dv[dt] = Mma<T>::run(to[i][dt], pf[i], acc_dv[dt]);
-          acc_dk[dt] = Mma<T>::run(tq[i][dt], df[i], acc_dk[dt]);
-        }
+    for (int kk = 0; kk < KS; ++kk) {
+      const int64_t off = kvbase + int64_t(key) * kn + kk * 16 + hi * 8;
+      kf[kk] = key < N ? *reinterpret_cast<const i32x4*>(K + off) : i32x4{0, 0, 0, 0};
+      vf[kk] = key < N ? *reinterpret_cast<const i32x4*>(V + off) : i32x4{0, 0, 0, 0};
     }
-    stage = stage + 1 == G::STAGES ? 0 : stage + 1;
-    fill = fill + 1 == G::STAGES ? 0 : fill + 1;
-  }
-  }
-#undef TK_BWD_DKDV_DMA
-  wait_vmcnt<0>();
 
-  // dK = scale (dK^T)^T, dV = (dV^T)^T: register r of tile dt is feature
-  // 32 dt + 8 (r / 4) + 4 hi + r % 4 of this lane's key.
-  if (key < N) {
-    T* dkr = dK + kvbase + int64_t(key) * kn;
-    T* dvr = dV + kvbase + int64_t(key) * kn;
+    // Query-side sources of the group's first head; head g adds g head strides. Each
+    // head gets its own buffer extent, so rows past the sequence end read as zero.
+    const T* q_head0 = Q + qbase;
+    const T* do_head0 = dO + qbase;
+    const float* stat_head0 = (wave < 2 ? lse : delta) + stat0;
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
+
+    uint32_t q_src[G::DMA_PER_TILE];
+#pragma unroll
+    for (int x = 0; x < G::DMA_PER_TILE; ++x) q_src[x] = tile_src<D, true>(wave, x, lane, sn);
+    const uint32_t st_src = uint32_t((wave & 1) * 32 + l32) * 4u;
+    const uint32_t blk_bytes = uint32_t(BB * sn) * 2u;
+
+    const int first = CAUSAL ? kb0 / BB : 0;  // first query block with a query >= kb0
+    const int nblk = (N + BB - 1) / BB - first;
+
+    // DMA of the next block in stream order (head dg of the group, relative block dj) into
+    // stage ST; past the end the last block is reloaded. Blocks are fetched strictly in
+    // order, so a cursor replaces a division, and the head's buffer resources are rebuilt
+    // only when the cursor moves to the next head.
+    int dg = 0, dj = 0;
+    __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)q_head0, (short)0,
+                                                                  sp.q_bytes, 0x00020000);
+    __amdgpu_buffer_rsrc_t rdo = __builtin_amdgcn_make_buffer_rsrc((void*)do_head0, (short)0,
+                                                                   sp.q_bytes, 0x00020000);
+    __amdgpu_buffer_rsrc_t rst = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)stat_head0, (short)0, uint32_t(N) * 4u, 0x00020000);
+  #define TK_BWD_DKDV_DMA(ST)                                                                 \
+    {                                                                                         \
+      const int qb_ = first + (dg >= s.group ? nblk - 1 : dj);                                \
+      dma_tiles<D>(rq, rdo, lds + (ST) * STB, q_src, q_src, qb_ * blk_bytes, wave);           \
+      dma_stats(rst, lds + (ST) * STB + 2 * TILE + wave * 128, st_src, qb_ * BB * 4, lane);   \
+      if (dg < s.group && ++dj == nblk) {                                                     \
+        dj = 0;                                                                               \
+        if (++dg < s.group) {                                                                 \
+          const int64_t h_ = int64_t(dg) * s.st[1];                                           \
+          rq = __builtin_amdgcn_make_buffer_rsrc((void*)(q_head0 + h_), (short)0,             \
+                                                 sp.q_bytes, 0x00020000);                     \
+          rdo = __builtin_amdgcn_make_buffer_rsrc((void*)(do_head0 + h_), (short)0,           \
+                                                  sp.q_bytes, 0x00020000);                    \
+          rst = __builtin_amdgcn_make_buffer_rsrc((void*)(stat_head0 + dg * stat_head),       \
+                                                  (short)0, uint32_t(N) * 4u, 0x00020000);    \
+        }                                                                                     \
+      }                                                                                       \
+    }
+
+    f32x16 acc_dv[DT], acc_dk[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int d = dt * 32 + g4 * 8 + hi * 4;
-        uint2 u;
-        u.x = pack2<T>(acc_dk[dt][g4 * 4 + 0] * s.scale, acc_dk[dt][g4 * 4 + 1] * s.scale);
-        u.y = pack2<T>(acc_dk[dt][g4 * 4 + 2] * s.scale, acc_dk[dt][g4 * 4 + 3] * s.scale);
-        *reinterpret_cast<uint2*>(dkr + d) = u;
-        u.x = pack2<T>(acc_dv[dt][g4 * 4 + 0], acc_dv[dt][g4 * 4 + 1]);
-        u.y = pack2<T>(acc_dv[dt][g4 * 4 + 2], acc_dv[dt][g4 * 4 + 3]);
-        *reinterpret_cast<uint2*>(dvr + d) = u;
+      for (int r = 0; r < 16; ++r) acc_dv[dt][r] = acc_dk[dt][r] = 0.f;
+
+    uint32_t qa[KS], ta0[DT], ta8[DT];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) qa[kk] = frag_addr<D, true>(lane, kk);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      ta0[dt] = tr_addr<D>(lane, dt, 0);
+      ta8[dt] = tr_addr<D>(lane, dt, 8);
+    }
+    const uint32_t sa = (hi * 4) * 4;  // statistics: query offset 4 hi within each group of 8
+    const float sl2 = s.scale_log2;
+
+    TK_BWD_DKDV_DMA(0)
+    TK_BWD_DKDV_DMA(1)
+    int stage = 0, fill = 2;
+    // Causal: this wave's blocks start at the first one holding a query >= its first key.
+    const int wave_first = CAUSAL ? min(nblk, (wk0 / BB) - first) : 0;
+    for (int g = 0; g < s.group; ++g) {
+    int j = 0;
+    for (; j < wave_first; ++j) {
+      wait_vmcnt<NDMA>();
+      barrier_no_fence();
+      TK_BWD_DKDV_DMA(fill)
+      stage = stage + 1 == G::STAGES ? 0 : stage + 1;
+      fill = fill + 1 == G::STAGES ? 0 : fill + 1;
+    }
+    for (; j < nblk; ++j) {
+      wait_vmcnt<NDMA>();
+      barrier_no_fence();
+      TK_BWD_DKDV_DMA(fill)
+      const int q0 = (first + j) * BB;
+      // Lane addresses for this stage; the dO tile and the 16-row steps are immediates.
+      const uint32_t sbase = lds_base + stage * STB;
+      uint32_t qs_a[KS], t0[DT], t8[DT];
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) qs_a[kk] = sbase + qa[kk];
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        t0[dt] = sbase + ta0[dt];
+        t8[dt] = sbase + ta8[dt];
       }
-  }
+      const uint32_t st_a = sbase + 2 * TILE + sa;
+      const bool need_mask = CAUSAL && q0 < wk0 + G::LW - 1;
+
+      // Two sub-blocks of 32 queries (query tile mt); each sub-block's transposed reads are
+      // issued before its softmax arithmetic.
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        SubRows rows;
+        read_sub_rows<D>(rows, mt, qs_a, st_a);
+        wait_lgkm<0>();
+        pin_sub_rows<D>(rows);
+        // S = Q K^T and dP = dO V^T for 32 queries x this wave's 32 keys.
+        f32x16 sc, dp;
+        {
+          const f32x16 z = {};
+#pragma unroll
+          for (int kk = 0; kk < KS; ++kk) {
+            sc = Mma<T>::run(rows.q[kk], kf[kk], kk == 0 ? z : sc);
+            dp = Mma<T>::run(rows.o[kk], vf[kk], kk == 0 ? z : dp);
+          }
+        }
+        i32x4 to[2][DT], tq[2][DT];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            to[i][dt] = read_tr_step<RB, TILE>(2 * mt + i, t0[dt], t8[dt]);
+            tq[i][dt] = read_tr_step<RB>(2 * mt + i, t0[dt], t8[dt]);
+          }
+        // Causal: keys after a query get S = -inf (exp2 -> 0); only diagonal blocks.
+        if (__builtin_expect(need_mask, 0)) {
+          const int lim = q0 + mt * 32 + 4 * hi - key;  // key <= query  <=>  offset >= -lim
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (acc_row(r, 0) + lim < 0) sc[r] = kNegInf;
+        }
+        // P = exp2(S c - lse), dS = P (dP - delta); register r holds query
+        // q0 + 32 mt + 8 (r / 4) + 4 hi + r % 4.
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float l = __int_as_float(rows.lse[r >> 2][r & 3]);
+          const float dl = __int_as_float(rows.dlt[r >> 2][r & 3]);
+          const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], sl2, -l));
+          sc[r] = pv;
+          dp[r] = pv * (dp[r] - dl);
+        }
+        const i32x4 pf[2] = {acc_frag<T>(sc, 0), acc_frag<T>(sc, 1)};
+        const i32x4 df[2] = {acc_frag<T>(dp, 0), acc_frag<T>(dp, 1)};
+        wait_lgkm<0>();
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            pin(to[i][dt]);
+            pin(tq[i][dt]);
+          }
+        // dV^T += dO^T P and dK^T += Q^T dS.
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) {
+            acc_dv[dt] = Mma<T>::run(to[i][dt], pf[i], acc_dv[dt]);
+            acc_dk[dt] = Mma<T>::run(tq[i][dt], df[i], acc_dk[dt]);
+          }
+      }
+      stage = stage + 1 == G::STAGES ? 0 : stage + 1;
+      fill = fill + 1 == G::STAGES ? 0 : fill + 1;
+    }
+    }
+  #undef TK_BWD_DKDV_DMA
+    wait_vmcnt<0>();
+
+    // dK = scale (dK^T)^T, dV = (dV^T)^T: register r of tile dt is feature
+    // 32 dt + 8 (r / 4) + 4 hi + r % 4 of this lane's key.
+    if (key < N) {
+      T* dkr = dK + kvbase + int64_t(key) * kn;
+      T* dvr = dV + kvbase + int64_t(key) * kn;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int d = dt * 32 + g4 * 8 + hi * 4;
+          uint2 u;
+          u.x = pack2<T>(acc_dk[dt][g4 * 4 + 0] * s.scale, acc_dk[dt][g4 * 4 + 1] * s.scale);
+          u.y = pack2<T>(acc_dk[dt][g4 * 4 + 2] * s.scale, acc_dk[dt][g4 * 4 + 3] * s.scale);
+          *reinterpret_cast<uint2*>(dkr + d) = u;
+          u.x = pack2<T>(acc_dv[dt][g4 * 4 + 0], acc_dv[dt][g4 * 4 + 1]);
+          u.y = pack2<T>(acc_dv[dt][g4 * 4 + 2], acc_dv[dt][g4 * 4 + 3]);
+          *reinterpret_cast<uint2*>(dvr + d) = u;
+        }
+    }
+  }  // key blocks
 }
 
 template <int D>
@@ -1076,11 +1099,16 @@ BwdShape make_shape(int64_t batch, int64_t heads, int64_t kv_heads, int64_t seq,
 // whose two workgroups per CU overlap one workgroup's exponentials with the other's
 // MFMAs (at head_dim 64 a producer's elementwise phase, the same work as at 128, outlasts
 // the consumer's halved MFMA phase).
+// Causal head_dim 64 (kPairedKv), equal lengths: paired_items workgroups; otherwise one
+// workgroup per key block.
 template <typename T>
-void launch_dkdv(int64_t head_dim, bool causal, unsigned tiles, hipStream_t stream,
-                 const void* q, const void* k, const void* v, const void* dout, void* dk,
-                 void* dv, const float* lse, const float* delta, const BwdShape& s) {
-  const dim3 grid(tiles);
+void launch_dkdv(int64_t head_dim, bool causal, hipStream_t stream, const void* q,
+                 const void* k, const void* v, const void* dout, void* dk, void* dv,
+                 const float* lse, const float* delta, const BwdShape& s) {
+  const bool paired = s.cu == nullptr && causal && head_dim == 64 && kPairedKv<64>;
+  const int64_t n = paired ? paired_items(s.kv_tiles / s.blocks_per_head, s.blocks_per_head)
+                           : int64_t(s.kv_tiles);
+  const dim3 grid(static_cast<unsigned>(n));
   if (head_dim == 64) {
     if (causal)
       hipLaunchKernelGGL((attn_bwd_dkdv_dma_kernel<T, 64, true>), grid, dim3(kThreads1), 0,
@@ -1123,11 +1151,10 @@ void attn_bwd_dkdv_dma_launch(int dtype, const void* q, const void* k, const voi
                               const int32_t* cu_seqlens, int64_t total) {
   const BwdShape s = make_shape(batch, heads, kv_heads, seq, head_dim, q_strides, kv_strides,
                                 sm_scale, cu_seqlens, total);
-  const unsigned tiles = static_cast<unsigned>(s.kv_tiles);
   if (dtype == TK_DTYPE_F16)
-    launch_dkdv<_Float16>(head_dim, causal, tiles, stream, q, k, v, dout, dk, dv, lse, delta, s);
+    launch_dkdv<_Float16>(head_dim, causal, stream, q, k, v, dout, dk, dv, lse, delta, s);
   else
-    launch_dkdv<__bf16>(head_dim, causal, tiles, stream, q, k, v, dout, dk, dv, lse, delta, s);
+    launch_dkdv<__bf16>(head_dim, causal, stream, q, k, v, dout, dk, dv, lse, delta, s);
 }
 
 }  // namespace tk

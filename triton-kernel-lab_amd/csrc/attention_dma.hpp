@@ -270,4 +270,58 @@ inline int64_t varlen_tiles(int64_t batch, int64_t total, int64_t seq, int64_t b
   return by_total < by_seq ? by_total : by_seq;
 }
 
+// A kernel's argument block, read afresh: `Args` is the kernel's only parameter, so it
+// starts the kernarg segment. The segment pointer passes through an empty asm at each
+// call, so a loop that calls this once per iteration loads the arguments where each
+// iteration uses them instead of hoisting the loads out of the loop and holding every
+// field in scalar registers across it (which made persistent loops spill).
+template <typename Args>
+__device__ __forceinline__ const Args& kernel_args() {
+  typedef const __attribute__((address_space(4))) char kernarg_char;
+  kernarg_char* p = (kernarg_char*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return *(const Args*)p;
+}
+
+// Block `it` (0, 1) of this workgroup in a causal launch that deals blocks in pairs: the
+// grid has one workgroup per pair (paired_items), ranks i and units-1-i of one head (rank 0
+// is a head's heaviest block under causal masking), so every pair carries the same work.
+// Returns (head, rank), or false when the workgroup is done. With heads and the grid both
+// multiples of 8, workgroup w runs on XCD w % 8 and takes a pair of that XCD's eighth of
+// the heads (a head's K/V or Q/dO blocks then stay in one L2), head-major. Equal durations
+// keep the hardware dispatcher from stalling: it hands workgroups to the XCDs in a fixed
+// round-robin order and waits on an XCD whose next CU is still busy, so with one causal
+// block per workgroup a CU sat idle ~11.5 us on average between blocks (non-causal:
+// 2.8 us). Pairs ran the causal D128 forward 1.80 -> 1.75 ms on one box and 1.86 -> 1.81 ms
+// on another; persistent workgroups (one per CU slot, walking their pairs) 1.82 ms there.
+__device__ __forceinline__ bool paired_tile(int& it, int heads, int units, int& head,
+                                            int& rank) {
+  int j = blockIdx.x, gx = gridDim.x, h0 = 0, hn = heads;
+  if (heads % 8 == 0 && gridDim.x % 8 == 0) {
+    j = blockIdx.x / 8;
+    gx = gridDim.x / 8;
+    hn = heads / 8;
+    h0 = (blockIdx.x % 8) * hn;
+  }
+  const int ph = (units + 1) / 2;  // pairs per head
+  for (;;) {
+    const int p = j + (it >> 1) * gx;
+    if (p >= hn * ph) return false;
+    const int i = p % ph;
+    head = h0 + p / ph;
+    if ((it & 1) == 0) {
+      rank = i;
+      return true;
+    }
+    if (i != units - 1 - i) {
+      rank = units - 1 - i;
+      return true;
+    }
+    ++it;  // odd unit count: the middle rank has no partner
+  }
+}
+
+// Workgroups of a paired launch over `heads` heads of `units` blocks (paired_tile).
+inline int64_t paired_items(int64_t heads, int64_t units) { return heads * ((units + 1) / 2); }
+
 }  // namespace tk_attn

@@ -71,6 +71,18 @@ struct Shape {
   int64_t rope_stride;
 };
 
+// Arguments of the forward kernel, passed as its only parameter (read through kernel_args
+// in its tile loop).
+template <typename T>
+struct FwdArgs {
+  const T* Q;
+  const T* K;
+  const T* V;
+  T* O;
+  float* lse;
+  Shape s;
+};
+
 // Rotate-half RoPE of one 16-byte Q fragment pair: x1 holds features f .. f+7 and x2
 // features f + D/2 .. f + D/2 + 7 (f < D/2); c and s hold cos/sin of f .. f+7. The
 // arithmetic is the RoPE kernel's: products rounded separately (no contraction), then
@@ -254,77 +266,38 @@ __device__ __forceinline__ void mfma_phase(Hook&& hook, uint32_t kb, uint32_t vb
 
 // head_dim 64 uses 64 KiB of LDS per workgroup: held to 128 registers, two workgroups
 // share a CU (four waves per SIMD).
-// Tile `it` (0, 1, ...) of this workgroup in the persistent schedule of an equal-length
-// launch, as (batch * head, query block); false when the workgroup has no tile left. With
-// batch * heads and the grid both multiples of 8, workgroup w runs on XCD w % 8 and takes
-// tiles of that XCD's eighth of the heads only (a head's K/V blocks then stay in one L2),
-// head-major, so the workgroups of an XCD work through one or two heads at a time.
-// Causal: query blocks i and QB-1-i of a head form a pair of QB+1 key blocks, so every
-// pair is the same work; pair p of the XCD goes to its workgroup p % gx, heavy block first.
-// A workgroup that finishes early does not wait for the hardware dispatcher: with one
-// workgroup per tile, a CU whose causal tile ended sat idle ~9 us on average before its
-// next tile started (non-causal: 2.8 us), because the dispatcher hands tiles to the XCDs
-// in a fixed round-robin order and waits on the XCD whose next CU is still busy.
-// Persistent workgroups for head_dim 128 only: at head_dim 64 (128 registers) the values
-// the tile loop keeps live spill.
+// Equal lengths at head_dim 128: one workgroup per causal pair of query blocks
+// (paired_tile). Not at head_dim 64: at 128 registers the two-block loop spills inside the
+// key loop (causal B4 H32 N8192 1.22 -> 1.42 ms).
 template <int D>
-constexpr bool kPersistent = D == 128;
-
-template <bool CAUSAL>
-__device__ __forceinline__ bool fwd_tile_of(const Shape& s, int& it, int& bh, int& qb) {
-  const int QB = s.q_blocks, BH = s.tiles / QB;
-  int j = blockIdx.x, gx = gridDim.x, h0 = 0, hn = BH;
-  if (BH % 8 == 0 && gridDim.x % 8 == 0) {
-    j = blockIdx.x / 8;
-    gx = gridDim.x / 8;
-    hn = BH / 8;
-    h0 = (blockIdx.x % 8) * hn;
-  }
-  if (!CAUSAL) {
-    const int t = j + it * gx;
-    if (t >= hn * QB) return false;
-    bh = h0 + t / QB;
-    qb = t % QB;
-    return true;
-  }
-  const int ph = (QB + 1) / 2;  // pairs per head
-  for (;;) {
-    const int p = j + (it >> 1) * gx;
-    if (p >= hn * ph) return false;
-    const int i = p % ph;
-    bh = h0 + p / ph;
-    if ((it & 1) == 0) {
-      qb = QB - 1 - i;
-      return true;
-    }
-    if (i != QB - 1 - i) {
-      qb = i;
-      return true;
-    }
-    ++it;  // odd QB: the middle block has no partner
-  }
-}
+constexpr bool kPaired = D == 128;
 
 template <typename T, int D, bool CAUSAL>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(D == 64 ? 4 : 2))) void
-attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
-                    T* __restrict__ O, float* __restrict__ lse, Shape s) {
+attn_fwd_dma_kernel(FwdArgs<T> kernel_arg) {
   using G = Geo<D>;
   constexpr int BM = G::BM, BN = G::BN, KS = G::KS, FT = G::FT, RB = G::RB, OPB = G::OPB,
                 STB = G::STB, STAGES = G::STAGES, DPB = G::DMA_PER_BLOCK;
   __shared__ __attribute__((aligned(1024))) char lds[STAGES * STB];
   __shared__ int simd_of[G::WAVES];
 
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if ((threadIdx.x & 63) == 0) simd_of[wave] = simd_id();
+  const int wave0 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if ((threadIdx.x & 63) == 0) simd_of[wave0] = simd_id();
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
 
-  // Equal lengths: the workgroups are persistent (as many as the CUs hold), each running
-  // the tiles fwd_tile_of deals it. Varlen: one tile per workgroup, the heavy-first
-  // schedule over every sequence's query blocks (level = query block), heads interleaved
-  // over the XCDs.
-  for (int it = 0; kPersistent<D> || it == 0; ++it) {
+  // Causal, equal lengths, head_dim 128: the two query blocks paired_tile deals this
+  // workgroup (blocks i and QB-1-i of one head). Otherwise one query block per workgroup;
+  // varlen: the heavy-first schedule over every sequence's query blocks (level = query
+  // block), heads interleaved over the XCDs.
+  for (int it = 0; (kPaired<D> && CAUSAL) || it == 0; ++it) {
+    const FwdArgs<T>& args = kernel_args<FwdArgs<T>>();
+    const Shape& s = args.s;
+    const T* __restrict__ Q = args.Q;
+    const T* __restrict__ K = args.K;
+    const T* __restrict__ V = args.V;
+    T* __restrict__ O = args.O;
+    float* __restrict__ lse = args.lse;
     int b, h, qb, start = 0, N = s.seq;
     uint32_t k_bytes = s.k_bytes, v_bytes = s.v_bytes;
     if (s.cu != nullptr) {
@@ -340,9 +313,10 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
       if (qb * BM >= N) break;  // uniform: the whole workgroup leaves
       k_bytes = uint32_t(((N - 1) * s.k[2] + D) * 2);
       v_bytes = uint32_t(((N - 1) * s.v[2] + D) * 2);
-    } else if constexpr (kPersistent<D>) {
-      int bh;
-      if (!fwd_tile_of<CAUSAL>(s, it, bh, qb)) break;
+    } else if constexpr (kPaired<D> && CAUSAL) {
+      int bh, rank;
+      if (!paired_tile(it, s.tiles / s.q_blocks, s.q_blocks, bh, rank)) break;
+      qb = s.q_blocks - 1 - rank;
       b = bh / s.heads;
       h = bh % s.heads;
     } else {
@@ -359,11 +333,12 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
     // After the first tile: every wave has left the previous tile (its last LDS reads
     // are not followed by a barrier) before this tile's DMA refills the ring.
     if (it > 0) barrier_no_fence();
-    // The lane index passes through an empty asm once per tile, so the per-lane addresses
-    // derived from it are formed inside the tile rather than hoisted and held across the
-    // loop (head_dim 64 runs at 128 registers, where that would spill).
+    // The lane and wave indices pass through an empty asm once per tile, so the addresses
+    // derived from them are formed inside the tile rather than hoisted and held across the
+    // loop.
     int lane = threadIdx.x & 63;
-    if constexpr (kPersistent<D>) asm volatile("" : "+v"(lane));
+    int wave = wave0;
+    if constexpr (kPaired<D> && CAUSAL) asm volatile("" : "+v"(lane), "+s"(wave));
     const int c = lane & 15, g = lane >> 4;
     const int kvh = h / s.group;
     const T* Qh = Q + b * s.q[0] + h * s.q[1] + int64_t(start) * s.q[2];
@@ -382,7 +357,7 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
     // DMA sources (bytes from the head's base, block-relative row). Rows past the sequence
     // end are past the buffer extent and read as zero.
     uint32_t k_src[G::DMA_PER_OP], v_src[G::DMA_PER_OP];
-  #pragma unroll
+#pragma unroll
     for (int x = 0; x < G::DMA_PER_OP; ++x) {
       const int id = wave * G::DMA_PER_OP + x;
       const int row = id * G::ROWS_PER_DMA + lane / G::SLOTS;
@@ -396,17 +371,17 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
     const int last = kv_blocks - 1;
     const uint32_t k_blk = uint32_t(BN * s.k[2]) * 2u, v_blk = uint32_t(BN * s.v[2]) * 2u;
     // The first STAGES - 1 blocks are fetched before anything else.
-  #pragma unroll
+#pragma unroll
     for (int blk = 0; blk < STAGES - 1; ++blk)
       dma_block<D>(rk, rv, lds, k_src, v_src, blk, last, k_blk, v_blk, wave);
 
     // Q fragments (B operand of S^T): query tile qt holds query wq0 + 16 qt + c, k-step kk
     // features 32 kk + 8 g .. +7.
     i32x4 qf[2][KS];
-  #pragma unroll
+#pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       const int query = wq0 + 16 * qt + c;
-  #pragma unroll
+#pragma unroll
       for (int kk = 0; kk < KS; ++kk)
         qf[qt][kk] = query < N
                          ? *reinterpret_cast<const i32x4*>(Qh + query * s.q[2] + kk * 32 + g * 8)
@@ -416,13 +391,13 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
     // so the rotate-half pairs sit in one lane. Queries past the end keep zero tables (their
     // Q is 0).
     if (s.rope_cos != nullptr) {
-  #pragma unroll
+#pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
         const int query = wq0 + 16 * qt + c;
         const int64_t at = int64_t(query) * s.rope_stride + g * 8;
         const T* cr = static_cast<const T*>(s.rope_cos) + at;
         const T* sr = static_cast<const T*>(s.rope_sin) + at;
-  #pragma unroll
+#pragma unroll
         for (int kk = 0; kk < KS / 2; ++kk) {
           const i32x4 cv = query < N ? *reinterpret_cast<const i32x4*>(cr + kk * 32) : i32x4{0, 0, 0, 0};
           const i32x4 sv = query < N ? *reinterpret_cast<const i32x4*>(sr + kk * 32) : i32x4{0, 0, 0, 0};
@@ -434,11 +409,11 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
     // 4 kk + g; V rows 4 g + j (+32 per key step, +16 for k-index 4..7), features
     // 16 ft + 4 q .. +3, with j = c / 4, q = c % 4.
     uint32_t ka[KS], va[FT];
-  #pragma unroll
+#pragma unroll
     for (int kk = 0; kk < KS; ++kk) ka[kk] = c * RB + (((4 * kk + g) ^ G::kswz(c)) * 16);
     {
       const int row = 4 * g + (c >> 2), q = c & 3;
-  #pragma unroll
+#pragma unroll
       for (int ft = 0; ft < FT; ++ft) va[ft] = OPB + row * RB + ((ft ^ G::vswz(row)) * 32) + q * 8;
     }
 
@@ -446,9 +421,9 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
     // wq0 + 16 qt + c. st[qt][kt] register r: score of key n0 + 16 kt + 4 g + r.
     f32x4 acc[FT][2], st[2][4];
     i32x4 pf[2][2], vu[Units<D>::NV][2];
-  #pragma unroll
+#pragma unroll
     for (int ft = 0; ft < FT; ++ft)
-  #pragma unroll
+#pragma unroll
       for (int qt = 0; qt < 2; ++qt) acc[ft][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run[2] = {kNegInf, kNegInf}, l_part[2] = {0.f, 0.f};
     const float sl2 = s.scale_log2;
@@ -465,7 +440,7 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
     // the start of phase 2m (m >= 1) its stage's next block m + STAGES - 2 is fetched,
     // and block m must have landed before phase 2m begins.
     int grp = 0;
-  #pragma unroll
+#pragma unroll
     for (int w = 0; w < G::WAVES; ++w) grp += (w < wave && simd_of[w] == simd_of[wave]) ? 1 : 0;
     grp = __builtin_amdgcn_readfirstlane(grp) & 1;
     const int phases = 2 * kv_blocks + 2;
@@ -509,14 +484,14 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
       const int n0 = j * BN;
       const bool need_mask = n0 + BN > N || (CAUSAL && n0 + BN - 1 > wq0);
       if (__builtin_expect(need_mask, 0)) {
-  #pragma unroll
+#pragma unroll
         for (int qt = 0; qt < 2; ++qt)
-  #pragma unroll
+#pragma unroll
           for (int kt = 0; kt < 4; ++kt) {
             const int k0 = n0 + 16 * kt + 4 * g;  // the lane's first key of this tile
             int lim = N - 1 - k0;                 // last valid offset from k0
             if (CAUSAL) lim = min(lim, wq0 + 16 * qt + c - k0);
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 4; ++r)
               if (r > lim) st[qt][kt][r] = kNegInf;
           }
@@ -580,31 +555,31 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
         // such a maximum.
         float mx[2], m_new[2];
         bool move[2];
-  #pragma unroll
+#pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
           mx[qt] = kNegInf;
-  #pragma unroll
+#pragma unroll
           for (int kt = 0; kt < 4; ++kt)
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 4; ++r) mx[qt] = fmaxf(mx[qt], st[qt][kt][r]);
           move[qt] = mx[qt] * sl2 > m_run[qt] + kLazyRescale;
           m_new[qt] = m_run[qt];
         }
         if (__builtin_expect(__builtin_amdgcn_ballot_w64(move[0] || move[1]) != 0, 0)) {
-  #pragma unroll
+#pragma unroll
           for (int qt = 0; qt < 2; ++qt) {
             const float bm = max_over_column(mx[qt]) * sl2;
             move[qt] = bm > m_run[qt] + kLazyRescale;
             m_new[qt] = move[qt] ? bm : m_run[qt];
           }
         }
-  #pragma unroll
+#pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
           const float neg = -m_new[qt];
           float sum = 0.f;
-  #pragma unroll
+#pragma unroll
           for (int kt = 0; kt < 4; ++kt)
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 4; ++r) {
               const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(st[qt][kt][r], sl2, neg));
               st[qt][kt][r] = pv;
@@ -613,7 +588,7 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
           if (__builtin_amdgcn_ballot_w64(move[qt])) {
             const float alpha = move[qt] ? __builtin_amdgcn_exp2f(m_run[qt] - m_new[qt]) : 1.f;
             l_part[qt] *= alpha;
-  #pragma unroll
+#pragma unroll
             for (int ft = 0; ft < FT; ++ft) acc[ft][qt] *= alpha;
           }
           l_part[qt] += sum;
@@ -634,25 +609,25 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
     // MFMA chains) into the next phase, where it runs beside the partner wave's same kind
     // of work.
     auto pin_mfma = [&]() {
-  #pragma unroll
+#pragma unroll
       for (int qt = 0; qt < 2; ++qt)
-  #pragma unroll
+#pragma unroll
         for (int kt = 0; kt < 4; ++kt) pin(st[qt][kt]);
-  #pragma unroll
+#pragma unroll
       for (int ft = 0; ft < FT; ++ft)
-  #pragma unroll
+#pragma unroll
         for (int qt = 0; qt < 2; ++qt) pin(acc[ft][qt]);
     };
     // The softmax phase ends by issuing the first PREFETCH V units of the next MFMA phase
     // (block j's V tile has landed since phase 2j).
     auto pin_softmax = [&](int j) {
-  #pragma unroll
+#pragma unroll
       for (int qt = 0; qt < 2; ++qt) {
         pin(pf[qt][0]);
         pin(pf[qt][1]);
         asm volatile("" : "+v"(l_part[qt]), "+v"(m_run[qt]));
       }
-  #pragma unroll
+#pragma unroll
       for (int u = 0; u < Units<D>::PREFETCH; ++u) read_v_unit<D>(vu, kbase(j), va, u);
     };
     if (grp) end_phase();
@@ -678,14 +653,14 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
     wait_vmcnt<0>();
 
     // O = O^T / l: acc[ft][qt] register r is feature 16 ft + 4 g + r.
-  #pragma unroll
+#pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       const float l = sum_over_column(l_part[qt]);
       const float inv = 1.0f / l;
       const int query = wq0 + 16 * qt + c;
       if (query < N) {
         T* orow = Oh + query * s.o[2];
-  #pragma unroll
+#pragma unroll
         for (int ft = 0; ft < FT; ++ft) {
           uint2 u;
           u.x = pack2<T>(acc[ft][qt][0] * inv, acc[ft][qt][1] * inv);
@@ -702,26 +677,18 @@ attn_fwd_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* _
   }  // tiles
 }
 
-// Varlen and head_dim 64: one workgroup per tile. Otherwise `items` schedule units (tiles,
-// or causal pairs of tiles), dealt to at most as many persistent workgroups as the device
-// holds.
+// Causal head_dim 128, equal lengths: `items` workgroups (paired_items); otherwise one
+// workgroup per query block.
 template <typename T, int D>
 void launch(bool causal, int64_t items, hipStream_t st, const void* q, const void* k,
             const void* v, void* o, float* lse, const Shape& s) {
-  const void* fn = causal ? reinterpret_cast<const void*>(attn_fwd_dma_kernel<T, D, true>)
-                          : reinterpret_cast<const void*>(attn_fwd_dma_kernel<T, D, false>);
-  int64_t n = kPersistent<D> ? items : int64_t(s.tiles);
-  if (s.cu == nullptr && kPersistent<D>) {
-    const int resident = tk::resident_workgroups(fn, kThreads);
-    if (resident > 0 && resident < n) n = resident;
-  }
+  const int64_t n = kPaired<D> && causal && s.cu == nullptr ? items : int64_t(s.tiles);
   const dim3 grid(static_cast<unsigned>(n));
+  const FwdArgs<T> a{(const T*)q, (const T*)k, (const T*)v, (T*)o, lse, s};
   if (causal)
-    hipLaunchKernelGGL((attn_fwd_dma_kernel<T, D, true>), grid, dim3(kThreads), 0, st,
-                       (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, s);
+    hipLaunchKernelGGL((attn_fwd_dma_kernel<T, D, true>), grid, dim3(kThreads), 0, st, a);
   else
-    hipLaunchKernelGGL((attn_fwd_dma_kernel<T, D, false>), grid, dim3(kThreads), 0, st,
-                       (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, s);
+    hipLaunchKernelGGL((attn_fwd_dma_kernel<T, D, false>), grid, dim3(kThreads), 0, st, a);
 }
 
 int64_t head_extent_bytes(int64_t seq, int64_t head_dim, int64_t seq_stride) {
@@ -769,9 +736,8 @@ void attn_fwd_dma_launch(int dtype, const void* q, const void* k, const void* v,
                                   : (int)(s.q_blocks * batch * heads);
   s.k_bytes = (uint32_t)head_extent_bytes(seq, head_dim, k_strides[2]);
   s.v_bytes = (uint32_t)head_extent_bytes(seq, head_dim, v_strides[2]);
-  const int64_t items = cu_seqlens == nullptr && causal
-                            ? batch * heads * ((s.q_blocks + 1) / 2)
-                            : int64_t(s.tiles);
+  const int64_t items = cu_seqlens == nullptr ? paired_items(batch * heads, s.q_blocks)
+                                              : int64_t(s.tiles);
   if (dtype == TK_DTYPE_F16) {
     if (head_dim == 64) launch<_Float16, 64>(causal, items, stream, q, k, v, o, lse, s);
     else launch<_Float16, 128>(causal, items, stream, q, k, v, o, lse, s);
