@@ -109,6 +109,23 @@ def test_running_maximum_moves_often(dtype, d, causal, kind) -> None:
     torch.testing.assert_close(lse, dev(lse_ref, lse), rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("n", [513, 768])
+def test_paired_causal_blocks_on_the_xcd_path(n) -> None:
+    """Causal head_dim 128 deals query blocks i and QB-1-i to one workgroup: batch x heads
+    a multiple of 8 (each XCD takes its eighth of the heads) and an odd block count (the
+    middle block has no partner), against the oracle."""
+    torch.manual_seed(n + 1)
+    shape = (2, 4, n, 128)
+    q, k, v = (torch.randn(shape, device="cuda", dtype=torch.bfloat16) for _ in range(3))
+    out = torch.empty_like(q)
+    lse = torch.empty(shape[:-1], device="cuda", dtype=torch.float32)
+    _launch_forward(q, k, v, out, lse, causal=True, store_lse=True)
+    o_ref, lse_ref = oracle.attn_fwd(host(q), host(k), host(v), 128 ** -0.5, True, "bfloat16")
+    assert_close(out, dev(o_ref, out))
+    assert_relative_frobenius(out, dev(o_ref, out), max_relative_error=1e-2)
+    torch.testing.assert_close(lse, dev(lse_ref, lse), rtol=1e-5, atol=1e-5)
+
+
 def test_inference_and_training_forward_agree_bitwise() -> None:
     torch.manual_seed(5)
     q, k, v = (torch.randn(1, 4, 700, 128, device="cuda", dtype=torch.bfloat16) for _ in range(3))

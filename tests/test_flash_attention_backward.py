@@ -97,6 +97,26 @@ def test_matches_the_oracle(dtype, d, causal, n) -> None:
         assert_close(g, dev(r, g), rtol=5e-2, atol=5e-2)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_paired_key_blocks_on_the_xcd_path(dtype) -> None:
+    """Causal head_dim 64 dK/dV deals key blocks i and NB-1-i to one workgroup: batch x heads
+    a multiple of 8 (each XCD takes its eighth of the heads) and 3 blocks of 128 keys (the
+    middle one has no partner), against the oracle."""
+    torch.manual_seed(11)
+    shape = (2, 4, 384, 64)
+    q, k, v, do = (torch.randn(shape, device="cuda", dtype=dtype) for _ in range(4))
+    out = torch.empty_like(q)
+    lse = torch.empty(shape[:-1], device="cuda", dtype=torch.float32)
+    _launch_forward(q, k, v, out, lse, causal=True, store_lse=True)
+    dq, dk, dv = _launch_backward(q, k, v, out, lse, do, causal=True)
+    refs = oracle.attn_bwd(
+        host(q), host(k), host(v), host(out), host(do), host(lse), 64 ** -0.5, True, name(dtype)
+    )
+    for g, r in zip((dq, dk, dv), refs):
+        assert_relative_frobenius(g, dev(r, g), max_relative_error=1e-2)
+        assert_close(g, dev(r, g), rtol=5e-2, atol=5e-2)
+
+
 def test_backward_is_bitwise_reproducible() -> None:
     torch.manual_seed(8)
     q, k, v, do = _leaves((2, 4, 640, 128), dtype=torch.bfloat16)
