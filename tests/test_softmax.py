@@ -39,6 +39,19 @@ def test_widths_and_dtypes(dtype: torch.dtype, cols: int) -> None:
     _check(torch.randn(37, cols, device="cuda", dtype=dtype))
 
 
+@pytest.mark.parametrize(("rows", "cols", "dtype"), [(4097, 1000, torch.float32), (4099, 4096, torch.bfloat16), (5000, 64, torch.float16)])
+def test_two_rows_per_wave_with_an_odd_row_count(rows, cols, dtype) -> None:
+    """From 4096 rows on, single-wave rows go two to a wave; an odd count leaves the last
+    wave one row, which it loads twice and stores once."""
+    torch.manual_seed(rows)
+    x = torch.randn(rows, cols, device="cuda", dtype=dtype)
+    out_storage = torch.full((rows + 1, cols), 7.0, device="cuda", dtype=dtype)
+    _launch((x,), out_storage[:rows])
+    assert torch.all(out_storage[rows] == 7.0)
+    expected = dev(oracle.softmax(host(x), name(dtype)), x)
+    assert_close(out_storage[:rows], expected)
+
+
 def test_row_strided_adversarial_view() -> None:
     torch.manual_seed(0)
     x = torch.randn(64, 1000, device="cuda")[::2]
