@@ -13,20 +13,20 @@
 // are four consecutive columns of one row and leave as one 8-byte store.
 //
 // Operands reach LDS by buffer->LDS DMA (buffer_load_dwordx4 ... lds): no VGPR staging.
-// LDS is a ring of kStages stages of 32 KiB (A tile then B tile); K tile t+kAhead is
-// issued while tile t is multiplied, kAhead = kStages - 2, so the stage being refilled
-// was last read two tiles ago and one barrier per K tile orders every reuse. The
-// barrier sits between the wave's row tiles 0-3 and 4-7: rows 0-3 run while rows 4-7
-// of the same K tile are read and tile t + kAhead is issued; rows 4-7 run while the
-// next tile's rows 0-3 and B fragments (a second register set) are read.
+// A and B have rings of their own: A in 64-wide K tiles (three stages of 256 rows x 128 B),
+// B in 32-wide K tiles (four stages of 32 k-rows x 512 B), 160 KiB in all. Each DMA request
+// then covers a whole 128-byte line: with 32-wide A tiles every A row was a 64-byte half
+// line, and the vector memory path (texture data unit 95 % busy, two thirds of it waiting
+// on L1, L1 waiting on L2 two thirds of the time) moved a third more requests than bytes
+// needed. The loop runs 32-wide steps with one barrier each, placed between the wave's
+// row tiles 0-3 and 4-7: rows 0-3 run while rows 4-7 of the same step are read and the
+// step's DMA is issued; rows 4-7 run while the next step's rows 0-3 and B fragments (a
+// second register set) are read.
 //
 // Stage layout (bytes), chosen so every LDS read phase touches 64 distinct banks:
-//   A: 256 rows x 64 B; the 16-byte chunk c (k = 8c .. 8c+7) of row r sits at chunk
-//      c ^ a_swz(r), a_swz(r) = bit 0 of r | bit 2 of r << 1. A fragment (16 rows, lane
-//      group g taking k = 8g .. 8g+7) is one ds_read_b128. Measured on gfx950, an
-//      isolated stream of these reads sustains 256 B/clock/CU with this swizzle and
-//      155 B/clock/CU (four bank-conflict cycles per read) with c ^ ((r >> 2) & 3)
-//      or with none.
+//   A: 256 rows x 128 B; the 16-byte chunk c (k = 8c .. 8c+7 of the 64-wide tile) of row r
+//      sits at chunk c ^ a_swz(r), a_swz(r) = (r >> 1) & 7. A fragment (16 rows, lane
+//      group g taking k = 8g .. 8g+7 of the step's 32-wide half) is one ds_read_b128.
 //   B: 32 k-rows x 512 B, row-major in n; the 32-byte granule g (n = 16g .. 16g+15) of
 //      k-row k sits at granule g ^ (2 * (k & 3) + ((k >> 3) & 1)). Fragments are read
 //      with ds_read_b64_tr_b16, which transposes 4 k x 16 n blocks into the MFMA B
@@ -71,12 +71,15 @@ namespace {
 
 constexpr int BM = 256, BN = 256, BK = 32;
 constexpr int kThreads = 512;  // 8 waves
-constexpr int kStages = 5;
-constexpr int kAhead = kStages - 2;
 constexpr int kGroupM = 4;
 constexpr int kXcds = 8;
-constexpr int kOperandBytes = 256 * BK * 2;  // 16 KiB per operand per stage
-constexpr int kStageBytes = 2 * kOperandBytes;
+// A ring: kAStages stages of one 64-wide K tile (256 rows x 128 B); B ring: kBStages stages
+// of one 32-wide K tile (32 k-rows x 512 B). 96 + 64 KiB: all of the CU's LDS.
+constexpr int kAStages = 3, kBStages = 4;
+constexpr int kABytes = 256 * 64 * 2;        // 32 KiB per A stage
+constexpr int kOperandBytes = 256 * BK * 2;  // 16 KiB per B stage
+constexpr int kBRing = kAStages * kABytes;   // B ring offset
+constexpr int kLdsBytes = kBRing + kBStages * kOperandBytes;
 constexpr uint32_t kOob = 0x80000000u;  // past every buffer's num_records: reads as zero
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -154,25 +157,28 @@ struct Mfma<__bf16> {
   }
 };
 
-// A row swizzle: 16-byte chunk c of row r sits at c ^ a_swz(r).
-__device__ __forceinline__ int a_swz(int r) { return (r & 1) | ((r >> 1) & 2); }
+// A row swizzle (128-byte rows): 16-byte chunk c of row r sits at c ^ a_swz(r). A fragment
+// read phase takes one chunk of 16 consecutive rows: even and odd rows fall in opposite
+// halves of a 256-byte bank row, and (r >> 1) & 7 puts the 8 rows of each half on distinct
+// 16-byte slots.
+__device__ __forceinline__ int a_swz(int r) { return (r >> 1) & 7; }
 
 // B k-row swizzle: 32-byte granule g of k-row k sits at g ^ b_swz(k). A 16x16x32 B
 // fragment read phase covers two 16-lane groups reading k-rows 8 apart, so the swizzle
 // carries bit 3 of k besides the (k & 3) term that separates the 4 rows of one read.
 __device__ __forceinline__ int b_swz(int k) { return 2 * (k & 3) + ((k >> 3) & 1); }
 
-// A fragment of row tile I (16 rows = 1 KiB of the stage).
+// A fragment of row tile I (16 rows = 2 KiB of the stage).
 template <int I>
 __device__ __forceinline__ i32x4 read_a(uint32_t addr) {
-  return lds_read_b128<I * 1024>(addr);
+  return lds_read_b128<I * 2048>(addr);
 }
 
 // B fragment: k-rows +0..3 and +4..7 of this lane group (ROWB bytes per k-row).
 template <int ROWB>
 __device__ __forceinline__ i32x4 read_b(uint32_t addr) {
-  const i32x2 lo = lds_read_tr16<kOperandBytes>(addr);
-  const i32x2 hi = lds_read_tr16<kOperandBytes + 4 * ROWB>(addr);
+  const i32x2 lo = lds_read_tr16<0>(addr);
+  const i32x2 hi = lds_read_tr16<4 * ROWB>(addr);
   return i32x4{lo[0], lo[1], hi[0], hi[1]};
 }
 
@@ -190,7 +196,7 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
                   T* __restrict__ C, Problem p) {
   constexpr int kTileN = kSwiGLU ? 128 : BN;
   constexpr int kRowB = kSwiGLU ? 256 : 512;
-  __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
 
   const int total = p.tiles_m * p.tiles_n;
   int w = blockIdx.x;
@@ -215,12 +221,17 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
   const int ldb = up_half ? p.ldb2 : p.ldb;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
 
-  uint32_t a_src[2], b_src[2];
+  // A DMA x (0..3) of a 64-wide K tile: rows 8 (4 wave + x) .. +7, eight lanes per 128-byte
+  // row; each lane fetches the chunk that belongs at its LDS slot.
+  uint32_t a_src[4], b_src[2];
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    const int r = (wave * 4 + x) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ a_swz(r);
+    a_src[x] = (m0 + r < p.m) ? uint32_t((m0 + r) * p.lda + c * 8) * 2u : kOob;
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int r = (wave * 2 + i) * 16 + (lane >> 2);
-    const int c = (lane & 3) ^ a_swz(r);
-    a_src[i] = (m0 + r < p.m) ? uint32_t((m0 + r) * p.lda + c * 8) * 2u : kOob;
     if constexpr (kSwiGLU) {
       const int L = wave * 2 + i;
       const int kr = 4 * (L & 7) + (lane >> 4);
@@ -235,28 +246,34 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
     }
   }
   const uint32_t b_tile_bytes = uint32_t(BK * ldb) * 2u;
-  const int kt = p.k / BK;
+  const int kt = p.k / BK;      // 32-wide K tiles
+  const int kt64 = (kt + 1) / 2;  // 64-wide A tiles (the last one half used when kt is odd)
 
   float row_scale = 0.f;
   if constexpr (kRowScale)
     if (threadIdx.x < BM) row_scale = p.row_scale[min(m0 + (int)threadIdx.x, p.m - 1)];
 
-  auto dma = [&](int x, int tile, int slot) {
+  // Tiles past the end reload the last one into a stage that is never read, keeping every
+  // step's DMA count constant.
+  auto dma_a = [&](int x, int tile, int slot) {
+    tile = min(tile, kt64 - 1);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        ra, (lds_void*)(lds + slot * kABytes + (wave * 4 + x) * 1024), 16, a_src[x],
+        tile * 128, 0, 0);
+  };
+  auto dma_b = [&](int x, int tile, int slot) {
     tile = min(tile, kt - 1);
-    char* stage = lds + slot * kStageBytes;
-    if (x < 2)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(stage + (wave * 2 + x) * 1024), 16,
-                                               a_src[x], tile * (BK * 2), 0, 0);
-    else
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rb, (lds_void*)(stage + kOperandBytes + (wave * 2 + x - 2) * 1024), 16, b_src[x - 2],
-          tile * b_tile_bytes, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rb, (lds_void*)(lds + kBRing + slot * kOperandBytes + (wave * 2 + x) * 1024), 16,
+        b_src[x], tile * b_tile_bytes, 0, 0);
   };
 
-  // A: row wm + l16 (+16 per row tile), chunk lg swizzled (a_swz reads only the row's
-  // low four bits, the same for every row tile). B: k-rows 8 lg + (l16 >> 2) (+4), columns of N tile j starting
-  // at 4 (l16 & 3).
-  const uint32_t a_addr = (wm + l16) * 64 + ((lg ^ a_swz(l16)) * 16);
+  // A: row wm + l16 (+16 per row tile), chunk lg (first 32-wide half of the 64-wide tile)
+  // or 4 + lg (second half), swizzled (a_swz reads only the row's low four bits, the same
+  // for every row tile). B: k-rows 8 lg + (l16 >> 2) (+4), columns of N tile j starting at
+  // 4 (l16 & 3).
+  const uint32_t a_addr0 = (wm + l16) * 128 + ((lg ^ a_swz(l16)) * 16);
+  const uint32_t a_addr1 = (wm + l16) * 128 + (((4 + lg) ^ a_swz(l16)) * 16);
   uint32_t b_addr[4];
   {
     const int jj = l16 >> 2, q = l16 & 3;
@@ -281,78 +298,95 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll
-  for (int t = 0; t < kAhead; ++t)
-#pragma unroll
-    for (int x = 0; x < 4; ++x) dma(x, t, t);
-  wait_vmcnt<(kAhead - 1) * 4>();
+  // DMA schedule. 32-wide step t issues B tile t + 3 (two instructions per wave) into B
+  // stage (t + 3) % 4 and, when t is odd, the 64-wide A tile (t + 3) / 2 (four per wave)
+  // into A stage ((t + 3) / 2) % 3. A stage reuse: A tile v's last fragments (rows 4-7 of
+  // step 2v + 1) are read in the first half of step 2v + 1 and waited for after that step's
+  // barrier, so every wave is done with them at the barrier of step 2v + 2; tile v + 3
+  // refills the stage from step 2v + 3 on. B stage reuse: B tile t's fragments are read in
+  // the second half of step t - 1 and waited for at the start of step t; tile t + 4 refills
+  // the stage in step t + 1. Step t's barrier needs 32-wide tile t + 1 landed, issued in
+  // step t - 2 or earlier, so each wave waits until at most the 8 instructions of steps
+  // t - 1 and t are in flight. The prologue is steps -3 .. -1 of the same schedule.
+  dma_a(0, 0, 0); dma_a(1, 0, 0); dma_a(2, 0, 0); dma_a(3, 0, 0);
+  dma_b(0, 0, 0); dma_b(1, 0, 0);
+  dma_b(0, 1, 1); dma_b(1, 1, 1);
+  dma_a(0, 1, 1); dma_a(1, 1, 1); dma_a(2, 1, 1); dma_a(3, 1, 1);
+  dma_b(0, 2, 2); dma_b(1, 2, 2);
+  wait_vmcnt<8>();
   barrier_no_fence();
 
   i32x4 a_lo[4], a_hi[4], b0[4], b1[4];
-  a_lo[0] = read_a<0>(lds_base + a_addr);
-  a_lo[1] = read_a<1>(lds_base + a_addr);
-  a_lo[2] = read_a<2>(lds_base + a_addr);
-  a_lo[3] = read_a<3>(lds_base + a_addr);
+  a_lo[0] = read_a<0>(lds_base + a_addr0);
+  a_lo[1] = read_a<1>(lds_base + a_addr0);
+  a_lo[2] = read_a<2>(lds_base + a_addr0);
+  a_lo[3] = read_a<3>(lds_base + a_addr0);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) b0[j] = read_b<kRowB>(lds_base + b_addr[j]);
+  for (int j = 0; j < 4; ++j) b0[j] = read_b<kRowB>(lds_base + kBRing + b_addr[j]);
 
-  // One K tile; B is this tile's B fragments, Bn receives the next tile's.
-  auto step = [&](int t, int stage, int fill, i32x4 (&Bc)[4], i32x4 (&Bn)[4]) {
-    const uint32_t base = lds_base + stage * kStageBytes;
-    const int next = stage + 1 == kStages ? 0 : stage + 1;
-    const uint32_t next_base = lds_base + next * kStageBytes;
+  // One 32-wide step t (half H of the 64-wide A tile in A stage sa; B stage sb). Bc holds
+  // this step's B fragments, Bn receives the next step's. The next step reads A stage
+  // sa_next (the same stage when H == 0) and B stage sb_next.
+  auto step = [&](auto half, int t, int sa, int sa_next, int sb, int sb_next, i32x4 (&Bc)[4],
+                  i32x4 (&Bn)[4]) {
+    constexpr int H = decltype(half)::value;
+    const uint32_t a_cur = lds_base + sa * kABytes + (H ? a_addr1 : a_addr0);
+    const uint32_t a_next = lds_base + sa_next * kABytes + (H ? a_addr0 : a_addr1);
+    const uint32_t b_next = lds_base + kBRing + sb_next * kOperandBytes;
+    // Refill targets: B stage (t + 3) % 4 == (sb + 3) % 4, A stage of tile (t + 3) / 2.
+    const int fill_b = sb == 0 ? 3 : sb - 1;
+    const int fill_a = sa == 0 ? 2 : sa - 1;
     wait_lgkm_pin(a_lo);
     wait_lgkm_pin(Bc);
     sched_fence();
-    // Rows 0-3; read rows 4-7 of this tile, issue tile t + kAhead.
+    // Rows 0-3; read rows 4-7 of this step, issue the DMA.
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
       const int i = x >> 2, j = x & 3;
       acc[i][j] = Mfma<T>::run(Bc[j], a_lo[i], acc[i][j]);
       sched_fence();
       if (j == 0) {
-        if (i == 0) a_hi[0] = read_a<4>(base + a_addr);
-        if (i == 1) a_hi[1] = read_a<5>(base + a_addr);
-        if (i == 2) a_hi[2] = read_a<6>(base + a_addr);
-        if (i == 3) a_hi[3] = read_a<7>(base + a_addr);
+        if (i == 0) a_hi[0] = read_a<4>(a_cur);
+        if (i == 1) a_hi[1] = read_a<5>(a_cur);
+        if (i == 2) a_hi[2] = read_a<6>(a_cur);
+        if (i == 3) a_hi[3] = read_a<7>(a_cur);
       }
-      if (j == 2) dma(i, t + kAhead, fill);
+      if (H == 1 && j == 1) dma_a(i, (t + 3) >> 1, fill_a);
+      if (j == 3 && (i & 1) == 0) dma_b(i >> 1, t + 3, fill_b);
       sched_fence();
     }
-    wait_vmcnt<(kAhead - 1) * 4>();
+    wait_vmcnt<8>();
     barrier_no_fence();
     wait_lgkm_pin(a_hi);
     sched_fence();
-    // Rows 4-7; read rows 0-3 and B of tile t+1.
+    // Rows 4-7; read rows 0-3 and B of step t + 1.
 #pragma unroll
     for (int x = 0; x < 16; ++x) {
       const int i = x >> 2, j = x & 3;
       acc[4 + i][j] = Mfma<T>::run(Bc[j], a_hi[i], acc[4 + i][j]);
       sched_fence();
       if (j == 0) {
-        if (i == 0) a_lo[0] = read_a<0>(next_base + a_addr);
-        if (i == 1) a_lo[1] = read_a<1>(next_base + a_addr);
-        if (i == 2) a_lo[2] = read_a<2>(next_base + a_addr);
-        if (i == 3) a_lo[3] = read_a<3>(next_base + a_addr);
+        if (i == 0) a_lo[0] = read_a<0>(a_next);
+        if (i == 1) a_lo[1] = read_a<1>(a_next);
+        if (i == 2) a_lo[2] = read_a<2>(a_next);
+        if (i == 3) a_lo[3] = read_a<3>(a_next);
       }
-      if (j == 2) Bn[i] = read_b<kRowB>(next_base + b_addr[i]);
+      if (j == 2) Bn[i] = read_b<kRowB>(b_next + b_addr[i]);
       sched_fence();
     }
   };
 
-  int stage = 0, fill = kAhead;
-  auto advance = [&]() {
-    stage = stage + 1 == kStages ? 0 : stage + 1;
-    fill = fill + 1 == kStages ? 0 : fill + 1;
-  };
-  int t = 0;
-  for (; t + 1 < kt; t += 2) {
-    step(t, stage, fill, b0, b1);
-    advance();
-    step(t + 1, stage, fill, b1, b0);
-    advance();
+  // 64-wide A tile u: steps 2u (B stage sb) and 2u + 1 (sb + 1), A stage sa.
+  int sa = 0, sb = 0;
+  for (int u = 0; 2 * u < kt; ++u) {
+    const int sa_next = sa == kAStages - 1 ? 0 : sa + 1;
+    step(std::integral_constant<int, 0>{}, 2 * u, sa, sa, sb, sb + 1, b0, b1);
+    if (2 * u + 1 < kt)
+      step(std::integral_constant<int, 1>{}, 2 * u + 1, sa, sa_next, sb + 1,
+           sb + 2 == kBStages ? 0 : sb + 2, b1, b0);
+    sa = sa_next;
+    sb = sb + 2 == kBStages ? 0 : sb + 2;
   }
-  if (t < kt) step(t, stage, fill, b0, b1);
   wait_vmcnt<0>();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
