@@ -116,7 +116,7 @@ def test_launch_metadata_names_the_kernels_that_launch() -> None:
 
     gemm = REGISTRY["matmul_fp32acc"].benchmark_metadata(4096, torch.float16)
     assert gemm["kernel"] == "gemm_dma_kernel"
-    assert (gemm["block_k"], gemm["num_warps"], gemm["num_stages"]) == (32, 8, 5)
+    assert (gemm["block_k"], gemm["num_warps"], gemm["num_stages"]) == (32, 8, 4)
     assert gemm["mma_opcode"] == "v_mfma_f32_16x16x32_f16"
     attn = REGISTRY["attention_causal"].benchmark_metadata(1024, torch.float16)
     assert attn["kernel"] == "attn_fwd_dma_kernel"

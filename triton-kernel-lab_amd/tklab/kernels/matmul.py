@@ -9,8 +9,8 @@ The reference autotunes 25 Triton configurations per shape
 (``matmul.py:23-75``); this build has a static choice between two kernels and
 reports the one a shape launches in the same metadata keys: row-major operands
 with K % 32 == 0 (every registry shape) take ``gemm_dma_kernel`` (256 x 256
-tiles, K step 32, eight wave64s, a 5-stage buffer->LDS ring,
-``v_mfma_f32_16x16x32``); strided operands or other K take the register-staged
+tiles, K step 32, eight wave64s, buffer->LDS rings of four 32-wide B stages and
+three 64-wide A stages, ``v_mfma_f32_16x16x32``); strided operands or other K take the register-staged
 ``gemm_kernel`` (256 x 256 x 64, four wave64s, ``v_mfma_f32_32x32x16``).
 ``matmul_fp16acc`` keeps its registry entry, but gfx950 MFMA
 accumulates f16 products in float32 only, so both entry points run the same
@@ -36,10 +36,11 @@ from tklab.registry import (
 
 _DTYPES = (torch.float16, torch.bfloat16)
 
-# csrc/gemm_dma.hip (BM, BN, BK, kGroupM, kThreads / 64 waves, kStages): row-major operands
-# with K % 32 == 0. "num_warps" counts wave64s.
+# csrc/gemm_dma.hip (BM, BN, BK, kGroupM, kThreads / 64 waves, kBStages): row-major operands
+# with K % 32 == 0. "num_warps" counts wave64s; "num_stages" is the ring of 32-wide K steps
+# (the B operand's; A is loaded in 64-wide tiles into a ring of kAStages = 3).
 TILE = {"kernel": "gemm_dma_kernel", "block_m": 256, "block_n": 256, "block_k": 32, "group_m": 4,
-        "num_warps": 8, "num_stages": 5}
+        "num_warps": 8, "num_stages": 4}
 _MFMA = {
     torch.float16: "v_mfma_f32_16x16x32_f16",
     torch.bfloat16: "v_mfma_f32_16x16x32_bf16",
