@@ -76,9 +76,10 @@ def test_fold_is_the_rounded_float32_product(dtype) -> None:
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("m", [256, 1000])
-def test_unit_and_power_of_two_row_scales_are_exact(dtype, m) -> None:
-    x, _, _, proj = _inputs(m, 512, 264, dtype, seed=3 + m)
+@pytest.mark.parametrize("m,k", [(256, 512), (1000, 512), (300, 96)])
+def test_unit_and_power_of_two_row_scales_are_exact(dtype, m, k) -> None:
+    """k = 96: an odd count of 32-wide K steps, so the last 64-wide A tile is half used."""
+    x, _, _, proj = _inputs(m, k, 264, dtype, seed=3 + m)
     plain = matmul_fp32acc(x, proj)
     ones = torch.ones(m, device="cuda")
     assert bits_equal(_rowscale(x, proj, ones), plain)
