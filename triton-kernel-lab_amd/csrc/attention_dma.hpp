@@ -117,15 +117,6 @@ __device__ __forceinline__ i32x2 lds_read_tr16(uint32_t addr) {
   return r;
 }
 
-// V^T fragment for 16 keys starting at row ROW0 of the stage's V tile: rows ROW0 .. +3
-// (k-index 0..3 of this lane half) and ROW0 + 8 .. +11 (k-index 4..7).
-template <int ROW0, int RB>
-__device__ __forceinline__ i32x4 read_v(uint32_t addr) {
-  const i32x2 a = lds_read_tr16<ROW0 * RB>(addr);
-  const i32x2 b = lds_read_tr16<(ROW0 + 8) * RB>(addr);
-  return i32x4{a[0], a[1], b[0], b[1]};
-}
-
 // Transposed fragment of a 32-key step starting at row ROW0 of a row-major [keys][D] tile:
 // rows ROW0 + 4g .. +3 (k-index 0..3 of lane group g = lane / 16) and ROW0 + 16 + 4g .. +3
 // (k-index 4..7), the key order of an operand built from two 16x16 accumulators (key
