@@ -42,8 +42,10 @@ def _check_rows(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, rows: torch.T
     [(1, 1, 8), (1, 8, 1), (8, 8, 8), (256, 256, 64), (300, 520, 72), (512, 512, 512),
      (129, 257, 193), (1024, 1024, 1024), (255, 264, 4096), (7, 9, 11),
      # K % 32 == 0 goes through the DMA kernel: fewer K tiles than the prefetch depth,
-     # exactly the prefetch depth, and M/N edges inside one block tile.
-     (1, 8, 32), (33, 40, 32), (300, 520, 96), (257, 136, 160), (520, 1032, 128)],
+     # exactly the prefetch depth, and M/N edges inside one block tile; K = 1056 is an
+     # odd count of 32-wide steps (last 64-wide A tile half used) after many ring wraps.
+     (1, 8, 32), (33, 40, 32), (300, 520, 96), (257, 136, 160), (520, 1032, 128),
+     (520, 264, 1056)],
 )
 def test_small_shapes_match_the_oracle(dtype: torch.dtype, m: int, n: int, k: int) -> None:
     torch.manual_seed(m * 7 + n * 3 + k)

@@ -28,7 +28,7 @@ def _operands(m, n, k, dtype, seed):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize(
     "m,n,k", [(1, 8, 32), (8, 8, 32), (256, 128, 64), (300, 520, 96), (257, 136, 160),
-              (1000, 1032, 256), (2048, 1024, 512)]
+              (1000, 1032, 256), (2048, 1024, 512), (300, 264, 1056)]
 )
 def test_fused_is_bitwise_the_unfused_composition(dtype, m, n, k) -> None:
     x, wg, wu = _operands(m, n, k, dtype, seed=m + n + k)
