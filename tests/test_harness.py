@@ -12,7 +12,13 @@ import pytest
 import torch
 
 import tklab.kernels  # noqa: F401  (registers every spec)
-from tklab.harness.bench import BenchRow, _add_performance_metrics
+from tklab.harness.bench import (
+    BenchRow,
+    _add_performance_metrics,
+    _compose_row,
+    _Timings,
+    _validate_benchmark_request,
+)
 from tklab.harness.jsonio import JsonObject, read_json_object, write_json_atomic
 from tklab.harness.roofline import (
     MI355X_PROFILE,
@@ -28,6 +34,7 @@ from tklab.harness.roofline import (
 from tklab.harness.timing import time_ms
 from tklab.kernels.fused_softmax import SOFTMAX
 from tklab.kernels.matmul import MATMUL_FP32ACC
+from tklab.registry import REGISTRY
 
 # ---------------------------------------------------------------- jsonio
 
@@ -236,6 +243,38 @@ def test_missing_roofs_are_errors() -> None:
         _add_performance_metrics(_row("matmul_fp32acc", 1, 1), spec=MATMUL_FP32ACC, size=512,
                                  dtype=torch.float16, milliseconds=1.0, peak_bw_gbps=None,
                                  cublas_tflops=32.0, theoretical_tflops=None)
+
+
+@pytest.mark.parametrize("name", sorted(REGISTRY))
+def test_rows_keep_their_identity_under_every_specs_metadata(name: str) -> None:
+    """bench_spec lays each spec's benchmark metadata under the row's identity fields, so
+    a metadata key such as the HIP kernel's name never renames the row (the reference's
+    plots group rows by row["kernel"])."""
+    spec = REGISTRY[name]
+    dtype, size = spec.dtypes[0], spec.sizes[0]
+    timings = _Timings(ms=0.5, ms_lo=0.4, ms_hi=0.6, torch_ms=1.0, naive_ms=2.0)
+    row = _compose_row(spec, size=size, dtype=dtype, timings=timings, peak_bw_gbps=5000.0,
+                       cublas_tflops=1000.0, theoretical_tflops=2500.0)
+    assert row["kernel"] == spec.name
+    assert (row["dtype"], row["size"]) == (str(dtype).removeprefix("torch."), size)
+    assert (row["ms"], row["ms_lo"], row["ms_hi"], row["torch_ms"]) == (0.5, 0.4, 0.6, 1.0)
+    assert row["speedup"] == pytest.approx(2.0) and row["speedup_vs_naive"] == pytest.approx(4.0)
+    if spec.benchmark_metadata is not None:
+        for key, value in spec.benchmark_metadata(size, dtype).items():
+            if key not in ("kernel", "dtype", "size"):
+                assert row[key] == value
+    assert ("gbps" in row) == (spec.bound == "memory")
+    assert ("tflops" in row) == (spec.bound == "compute")
+
+
+def test_benchmark_request_validation_runs_before_any_gpu_work() -> None:
+    with pytest.raises(ValueError, match="device index must be non-negative"):
+        _validate_benchmark_request(device=-1, warmup_ms=25, repetition_ms=100)
+    with pytest.raises(ValueError, match="warmup_ms must be positive.*repetition_ms"):
+        _validate_benchmark_request(device=0, warmup_ms=0, repetition_ms=-1)
+    if not torch.cuda.is_available():
+        with pytest.raises(RuntimeError, match="sees 0"):
+            _validate_benchmark_request(device=0, warmup_ms=25, repetition_ms=100)
 
 
 def test_timer_rejects_bad_parameters_before_touching_a_gpu() -> None:

@@ -115,17 +115,17 @@ def test_launch_metadata_names_the_kernels_that_launch() -> None:
     from tklab.kernels import flash_attention, matmul
 
     gemm = REGISTRY["matmul_fp32acc"].benchmark_metadata(4096, torch.float16)
-    assert gemm["kernel"] == "gemm_dma_kernel"
+    assert gemm["hip_kernel"] == "gemm_dma_kernel"
     assert (gemm["block_k"], gemm["num_warps"], gemm["num_stages"]) == (32, 8, 4)
     assert gemm["mma_opcode"] == "v_mfma_f32_16x16x32_f16"
     attn = REGISTRY["attention_causal"].benchmark_metadata(1024, torch.float16)
-    assert attn["kernel"] == "attn_fwd_dma_kernel"
+    assert attn["hip_kernel"] == "attn_fwd_dma_kernel"
     assert (attn["block_m"], attn["block_n"], attn["num_warps"]) == (256, 64, 8)
     assert attn["mma_opcode"] == "v_mfma_f32_16x16x32_f16"
     a = torch.empty(64, 96, dtype=torch.bfloat16)
     b = torch.empty(96, 64, dtype=torch.bfloat16)
-    assert matmul.launch_config(a, b)["kernel"] == "gemm_dma_kernel"
+    assert matmul.launch_config(a, b)["hip_kernel"] == "gemm_dma_kernel"
     assert matmul.launch_config(a, b)["mma_opcode"] == "v_mfma_f32_16x16x32_bf16"
-    assert matmul.launch_config(a[:, :80], b[:80])["kernel"] == "gemm_kernel"
-    assert matmul.launch_config(a, b.t().contiguous().t())["kernel"] == "gemm_kernel"
+    assert matmul.launch_config(a[:, :80], b[:80])["hip_kernel"] == "gemm_kernel"
+    assert matmul.launch_config(a, b.t().contiguous().t())["hip_kernel"] == "gemm_kernel"
     assert flash_attention.FORWARD_TILE["num_stages"] == 4

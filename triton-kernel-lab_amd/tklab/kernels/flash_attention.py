@@ -56,7 +56,7 @@ _LOG2_E = 1.4426950408889634
 # csrc/attention_fwd.hip (Geo<D>: BM, BN, WAVES, STAGES): 256 queries per workgroup as eight
 # wave64s of 32, key blocks of 64, a 4-stage buffer->LDS K/V ring, v_mfma_f32_16x16x32.
 # "num_warps" counts wave64s.
-FORWARD_TILE = {"kernel": "attn_fwd_dma_kernel", "block_m": 256, "block_n": 64, "num_warps": 8,
+FORWARD_TILE = {"hip_kernel": "attn_fwd_dma_kernel", "block_m": 256, "block_n": 64, "num_warps": 8,
                 "num_stages": 4}
 FORWARD_MFMA = {torch.float16: "v_mfma_f32_16x16x32_f16", torch.bfloat16: "v_mfma_f32_16x16x32_bf16"}
 # Backward (csrc/attention_bwd.hip, attention_bwd_dq.hip): dK/dV owns 128 keys per workgroup

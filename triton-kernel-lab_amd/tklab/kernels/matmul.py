@@ -39,14 +39,14 @@ _DTYPES = (torch.float16, torch.bfloat16)
 # csrc/gemm_dma.hip (BM, BN, BK, kGroupM, kThreads / 64 waves, kBStages): row-major operands
 # with K % 32 == 0. "num_warps" counts wave64s; "num_stages" is the ring of 32-wide K steps
 # (the B operand's; A is loaded in 64-wide tiles into a ring of kAStages = 3).
-TILE = {"kernel": "gemm_dma_kernel", "block_m": 256, "block_n": 256, "block_k": 32, "group_m": 4,
+TILE = {"hip_kernel": "gemm_dma_kernel", "block_m": 256, "block_n": 256, "block_k": 32, "group_m": 4,
         "num_warps": 8, "num_stages": 4}
 _MFMA = {
     torch.float16: "v_mfma_f32_16x16x32_f16",
     torch.bfloat16: "v_mfma_f32_16x16x32_bf16",
 }
 # csrc/gemm.hip's register-staged kernel: every other operand layout (double-buffered in registers).
-FALLBACK_TILE = {"kernel": "gemm_kernel", "block_m": 256, "block_n": 256, "block_k": 64,
+FALLBACK_TILE = {"hip_kernel": "gemm_kernel", "block_m": 256, "block_n": 256, "block_k": 64,
                  "group_m": 4, "num_warps": 4, "num_stages": 2}
 _FALLBACK_MFMA = {
     torch.float16: "v_mfma_f32_32x32x16_f16",
