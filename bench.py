@@ -13,9 +13,10 @@ float32 partial rows are not counted).
 rotate over three independent tensor sets (STEP_SETS), so no step finds its tensors
 in the last-level cache from the step before.
 ``roofline`` prices the dominant kernel of the step against 8 TB/s: its
-algorithmic bytes per launch over its average duration, measured with events
-on the launch stream around that kernel inside the timed region (an untimed
-attribution pass with events around every launch picks it; `attribution_ms`). ``traffic`` comes from the
+algorithmic bytes per launch over its average duration, measured with one event
+pair on the launch stream around K back-to-back launches of that kernel over the
+step's tensor sets, after the timed steps (an untimed attribution pass with events
+around every launch picks it; `attribution_ms`). ``traffic`` comes from the
 committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when present.
 ``reference_gpu`` times the reference's PyTorch path for the same step on the GPU.
 ``cpu_baseline`` times that PyTorch path on the host CPU (float32 upcasts, full size);
@@ -87,9 +88,6 @@ def _traffic_from_summary() -> float | None:
 # of seven 128 MiB tensors is only 3.5 times that cache; a single reused set ran the step
 # ~5 % faster).
 STEP_SETS = 3
-# Every SAMPLE_EVERY-th timed step times its dominant kernel with an event pair (coprime
-# with STEP_SETS, so the sampled launches cover every tensor set).
-SAMPLE_EVERY = 4
 
 
 class StepSet:
@@ -143,16 +141,18 @@ STEP_BYTES = {
 
 
 def time_step(torch, step: Step, steps: int, warmup: int) -> tuple[float, str, float, dict]:
-    """W untimed steps, an untimed attribution pass, then K timed steps.
+    """W untimed steps, an untimed attribution pass, K timed steps, then the dominant
+    kernel on its own.
 
-    The attribution pass (20 steps, events around every launch) gives each kernel's
-    mean duration and picks the dominant one. In the timed steps, every SAMPLE_EVERY-th
-    step carries events around that kernel (its mean over those launches is the dominant
-    kernel's duration): an event record between two launches delays the next launch by a
-    few microseconds, so events around every launch would add ~8 % to the step, and
-    around the dominant kernel in every step ~3 %.
-    Returns (ms per timed step, dominant kernel, its mean ms inside the timed region,
-    attribution-pass ms per kernel).
+    The attribution pass (20 steps, events around every launch) gives each kernel's mean
+    duration and picks the dominant one. The K timed steps carry no event but the pair
+    around all of them: an event recorded between two dependent launches delays the
+    second by several microseconds (events around every launch made the step ~8 % slower,
+    and an event pair around one ~90 us kernel read it ~7 % long against the kernel
+    trace). The dominant kernel's duration is then timed the same way: K launches back
+    to back over the STEP_SETS tensor sets between one event pair, on the launch stream.
+    Returns (ms per timed step, dominant kernel, its ms per launch, attribution-pass ms
+    per kernel).
     """
     plans = [step.launches(i) for i in range(len(step.sets))]
     launches = plans[0]
@@ -176,30 +176,29 @@ def time_step(torch, step: Step, steps: int, warmup: int) -> tuple[float, str, f
     dominant = max(attribution, key=attribution.get)
     dom = [name for name, _ in launches].index(dominant)
 
-    sampled = [i for i in range(steps) if i % SAMPLE_EVERY == 0]
-    events = {i: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for i in sampled}
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start.record(stream)
-    for i in range(steps):
-        timed_dom = i in events
-        for j, (_, fn) in enumerate(plans[i % len(plans)]):
-            if timed_dom and j == dom:
-                events[i][0].record(stream)
+    def timed_region(body) -> tuple[float, float]:
+        """(event ms, host ms) around `steps` calls of body(i) on the launch stream."""
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record(stream)
+        for i in range(steps):
+            body(i)
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end), (time.perf_counter() - t0) * 1e3
+
+    def one_step(i):
+        for _, fn in plans[i % len(plans)]:
             fn()
-            if timed_dom and j == dom:
-                events[i][1].record(stream)
-    end.record(stream)
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3
-    ms_step = start.elapsed_time(end) / steps
-    dominant_ms = statistics.fmean(a.elapsed_time(b) for a, b in events.values())
+
+    event_ms, wall_ms = timed_region(one_step)
+    ms_step = event_ms / steps
     # The event clock and the host clock must agree on the timed region.
     if abs(wall_ms / steps - ms_step) > 0.5 * ms_step:
         raise RuntimeError(f"event and host clocks disagree: {ms_step} vs {wall_ms / steps} ms")
+    dominant_ms = timed_region(lambda i: plans[i % len(plans)][dom][1]())[0] / steps
     return ms_step, dominant, dominant_ms, attribution
 
 

@@ -47,3 +47,23 @@ def test_invalid_arguments_fail_before_any_launch() -> None:
     status = lib.tk_softmax_fwd(7, ctypes.c_void_p(16), ctypes.c_void_p(16), 4, 4, 4, 4, None)
     assert status != 0
     assert b"dtype" in lib.tk_last_error()
+
+
+def test_elementwise_limit_is_the_int32_extent() -> None:
+    """Any int32-addressable problem passes the size check (unaligned data takes the
+    one-element-per-chunk path, so chunks == elements); one element more is rejected
+    before any launch."""
+    import torch
+
+    lib = _hip.load_library()
+    unaligned = ctypes.c_void_p(2)
+    too_big = ctypes.c_int64(2**31)
+    status = lib.tk_swiglu_fwd(1, unaligned, unaligned, unaligned, ctypes.c_int64(1), too_big,
+                               too_big, too_big, too_big, None)
+    assert status != 0 and b"problem too large" in lib.tk_last_error()
+    if torch.cuda.is_available():
+        return  # the accepted size would launch on the fake pointers below
+    largest = ctypes.c_int64(2**31 - 1)
+    status = lib.tk_swiglu_fwd(1, unaligned, unaligned, unaligned, ctypes.c_int64(1), largest,
+                               largest, largest, largest, None)
+    assert status != 0 and b"problem too large" not in lib.tk_last_error()

@@ -44,9 +44,9 @@ struct ChunkPos {
 };
 
 template <int VEC>
-__device__ __forceinline__ ChunkPos chunk_pos(int i, const tk::FastDiv& per_row) {
-  const int row = per_row.div(i);
-  return {row, (i - row * static_cast<int>(per_row.d)) * VEC};
+__device__ __forceinline__ ChunkPos chunk_pos(uint32_t i, const tk::FastDiv& per_row) {
+  const uint32_t row = per_row.div(i);
+  return {static_cast<int>(row), static_cast<int>(i - row * per_row.d) * VEC};
 }
 
 // ------------------------------------------------------------------ SwiGLU
@@ -54,16 +54,16 @@ __device__ __forceinline__ ChunkPos chunk_pos(int i, const tk::FastDiv& per_row)
 // y = value * gate * sigmoid(gate)  (src/tklab/kernels/swiglu.py:44-58)
 template <typename T, int VEC>
 __global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(
-    const T* __restrict__ value, const T* __restrict__ gate, T* __restrict__ y, int chunks,
+    const T* __restrict__ value, const T* __restrict__ gate, T* __restrict__ y, uint32_t chunks,
     tk::FastDiv per_row, int64_t vs, int64_t gs, int64_t ys) {
   // A workgroup pass covers kUnroll * kBlock consecutive chunks (one 4 KiB run per
   // wave and tensor), then the grid strides on.
-  const int stride = gridDim.x * kBlock * kUnroll;
-  for (int i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
+  const uint32_t stride = gridDim.x * kBlock * kUnroll;
+  for (uint32_t i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
     float v[kUnroll][VEC], g[kUnroll][VEC];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       tk::load_vec_stream<T, VEC>(value + p.row * vs + p.col, v[u]);
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
 #pragma unroll
@@ -86,16 +86,16 @@ __global__ __launch_bounds__(kBlock) void swiglu_fwd_kernel(
 template <typename T, int VEC>
 __global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(
     const T* __restrict__ dy, const T* __restrict__ value, const T* __restrict__ gate,
-    T* __restrict__ dvalue, T* __restrict__ dgate, int chunks, tk::FastDiv per_row, int64_t dys,
+    T* __restrict__ dvalue, T* __restrict__ dgate, uint32_t chunks, tk::FastDiv per_row, int64_t dys,
     int64_t vs, int64_t gs, int64_t dvs, int64_t dgs) {
   // A workgroup pass covers kUnroll * kBlock consecutive chunks (one 4 KiB run per
   // wave and tensor), then the grid strides on.
-  const int stride = gridDim.x * kBlock * kUnroll;
-  for (int i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
+  const uint32_t stride = gridDim.x * kBlock * kUnroll;
+  for (uint32_t i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
     float d[kUnroll][VEC], v[kUnroll][VEC], g[kUnroll][VEC];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       tk::load_vec_stream<T, VEC>(dy + p.row * dys + p.col, d[u]);
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       float dv[VEC], dg[VEC];
@@ -138,16 +138,16 @@ __device__ __forceinline__ int table_row(int row, const tk::FastDiv& positions) 
 template <typename T, int VEC, bool kPositions = false>
 __global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ cosv, const T* __restrict__ sinv,
-    T* __restrict__ y, int chunks, tk::FastDiv per_row, int half, int64_t xs, int64_t cs,
+    T* __restrict__ y, uint32_t chunks, tk::FastDiv per_row, int half, int64_t xs, int64_t cs,
     int64_t ss, int64_t ys, tk::FastDiv positions = tk::FastDiv()) {
   // A workgroup pass covers kUnroll * kBlock consecutive chunks (one 4 KiB run per
   // wave and tensor), then the grid strides on.
-  const int stride = gridDim.x * kBlock * kUnroll;
-  for (int i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
+  const uint32_t stride = gridDim.x * kBlock * kUnroll;
+  for (uint32_t i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
     float x1[kUnroll][VEC], x2[kUnroll][VEC], co[kUnroll][VEC], si[kUnroll][VEC];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       const T* xr = x + p.row * xs;
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       float y1[VEC], y2[VEC];
@@ -181,17 +181,17 @@ template <typename T, int VEC, bool kPositions = false>
 __global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ cosv,
     const T* __restrict__ sinv, T* __restrict__ dx, T* __restrict__ dcos, T* __restrict__ dsin,
-    int chunks, tk::FastDiv per_row, int half, int64_t dys, int64_t xs, int64_t cs, int64_t ss,
+    uint32_t chunks, tk::FastDiv per_row, int half, int64_t dys, int64_t xs, int64_t cs, int64_t ss,
     int64_t dxs, int64_t dcs, int64_t dss, tk::FastDiv positions = tk::FastDiv()) {
   const bool need_x = dcos != nullptr || dsin != nullptr;
   // A workgroup pass covers kUnroll * kBlock consecutive chunks (one 4 KiB run per
   // wave and tensor), then the grid strides on.
-  const int stride = gridDim.x * kBlock * kUnroll;
-  for (int i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
+  const uint32_t stride = gridDim.x * kBlock * kUnroll;
+  for (uint32_t i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
     float d1[kUnroll][VEC], d2[kUnroll][VEC], co[kUnroll][VEC], si[kUnroll][VEC];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       const T* dyr = dy + p.row * dys;
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       float o1[VEC], o2[VEC];
@@ -241,14 +241,14 @@ __global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
 // weight into the rows of the projection that follows it (W'[k, :] = w[k] * W[k, :]).
 template <typename T, int VEC>
 __global__ __launch_bounds__(kBlock) void scale_rows_kernel(
-    const T* __restrict__ x, const T* __restrict__ scale, T* __restrict__ y, int chunks,
+    const T* __restrict__ x, const T* __restrict__ scale, T* __restrict__ y, uint32_t chunks,
     tk::FastDiv per_row, int64_t xs, int64_t ys) {
-  const int stride = gridDim.x * kBlock * kUnroll;
-  for (int i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
+  const uint32_t stride = gridDim.x * kBlock * kUnroll;
+  for (uint32_t i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
     float v[kUnroll][VEC], sc[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       tk::load_vec_stream<T, VEC>(x + p.row * xs + p.col, v[u]);
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(kBlock) void scale_rows_kernel(
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
 #pragma unroll
@@ -283,9 +283,11 @@ int check_problem(const char* what, int dtype, int64_t rows, int64_t width, int 
   if (rows <= 0 || width <= 0) return tk::fail("%s: empty problem", what);
   *chunks_per_row = width / vec;
   *chunks = rows * *chunks_per_row;
-  // Chunk indices run to chunks + (grid stride) in 32-bit arithmetic.
-  if (*chunks > INT32_MAX - kUnroll * kMaxBlocks * kBlock)
-    return tk::fail("%s: problem too large", what);
+  // Chunk indices are unsigned 32-bit: below INT32_MAX plus one grid stride (at most
+  // kUnroll * kMaxBlocks * kBlock = 2^28), so any int32-addressable problem fits.
+  static_assert(int64_t(INT32_MAX) + kUnroll * kMaxBlocks * kBlock <= int64_t(UINT32_MAX),
+                "grid stride overflows the 32-bit chunk index");
+  if (*chunks > INT32_MAX) return tk::fail("%s: problem too large", what);
   return 0;
 }
 

@@ -223,12 +223,17 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
 
   // A DMA x (0..3) of a 64-wide K tile: rows 8 (4 wave + x) .. +7, eight lanes per 128-byte
   // row; each lane fetches the chunk that belongs at its LDS slot.
-  uint32_t a_src[4], b_src[2];
+  // a_last: the same sources for the last 64-wide tile when only its first 32 columns lie
+  // inside K (kt odd): lanes whose chunk falls in the second half read nothing. The tile's
+  // offset travels in soffset, which the buffer range check does not cover, so without
+  // this the last row of A would be read up to 64 bytes past its end.
+  uint32_t a_src[4], a_last[4], b_src[2];
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
     const int r = (wave * 4 + x) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ a_swz(r);
     a_src[x] = (m0 + r < p.m) ? uint32_t((m0 + r) * p.lda + c * 8) * 2u : kOob;
+    a_last[x] = c < 4 ? a_src[x] : kOob;
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -255,11 +260,12 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
 
   // Tiles past the end reload the last one into a stage that is never read, keeping every
   // step's DMA count constant.
+  const int half_tile = (kt & 1) ? kt64 - 1 : kt64;  // index of a half-used A tile, if any
   auto dma_a = [&](int x, int tile, int slot) {
     tile = min(tile, kt64 - 1);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        ra, (lds_void*)(lds + slot * kABytes + (wave * 4 + x) * 1024), 16, a_src[x],
-        tile * 128, 0, 0);
+        ra, (lds_void*)(lds + slot * kABytes + (wave * 4 + x) * 1024), 16,
+        tile == half_tile ? a_last[x] : a_src[x], tile * 128, 0, 0);
   };
   auto dma_b = [&](int x, int tile, int slot) {
     tile = min(tile, kt - 1);
