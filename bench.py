@@ -70,8 +70,8 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--only", default=None,
-                   help="time only the kernel-table rows whose kernel name contains this text "
-                        "(for profiling one kernel family)")
+                   help="time only the kernel-table rows whose kernel name or config contains "
+                        "this text (for profiling one kernel family or one shape)")
     return p.parse_args()
 
 
@@ -479,7 +479,7 @@ def measured_roofs(torch, device) -> dict:
 
 def kernel_table(torch, device, roofs: dict | None = None, only: str | None = None) -> list[dict]:
     """Per-kernel timings of every benchmark configuration (see the module docstring); with
-    `only`, just the rows whose kernel name contains it."""
+    `only`, just the rows whose kernel name or config contains it."""
     from tklab.kernels import flash_attention as fa
     from tklab.kernels import fused_softmax as sm
     from tklab.kernels import matmul as mm
@@ -550,7 +550,7 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         `ref_make(i)` the torch reference's call on the same copy. `mix` is the kernel's
         read:write byte ratio, whose measured roof gives `frac_mix` for the bytes the kernel
         moves (`moved` times the algorithmic bytes)."""
-        if only and only not in name:
+        if only and only not in name and only not in config:
             return False
         ms = streamed(make, nbytes, reps)
         gbps = nbytes / ms / 1e6
@@ -567,7 +567,7 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         return True
 
     def mfma_row(name, config, fn, flops, dtype, reps=10, ref=None, ref_fn=None):
-        if only and only not in name:
+        if only and only not in name and only not in config:
             return False
         ms = timed(fn, reps)
         tf = flops / ms / 1e9

@@ -83,7 +83,12 @@ def test_config_shapes(dtype: torch.dtype, m: int, n: int, k: int) -> None:
     assert torch.isfinite(c).all()
     rows = torch.cat([torch.arange(0, m, 997, device="cuda"), torch.tensor([m - 1], device="cuda")])
     _check_rows(a, b, c, rows)
-    assert_relative_frobenius(c, torch.mm(a, b), max_relative_error=1e-2)
+    # The whole of C, elementwise, against float32 math on the same operands (the
+    # reference's matmul.py:282-284 compares the float32 product; tolerances.py:7-11 gives
+    # the storage dtype's atol/rtol), so an error confined to a few tiles cannot pass.
+    want = a.float() @ b.float()
+    assert_close(c, want)
+    assert_relative_frobenius(c, want, max_relative_error=1e-2)
 
 
 def test_linearity_in_the_left_operand() -> None:
