@@ -12,18 +12,24 @@
 // Split kernel: one wave per (batch, kv head, split of split_len keys), both
 // products on MFMA (v_mfma_f32_16x16x32), so the VALU work per key does not grow
 // with G and the kernel stays HBM-bound:
-//   S^T (16 keys x 16 heads) = K (16 keys x 32 dims) . Q^T, K fragments loaded
-//     from HBM straight into registers (lane l: key l%16, dims 8*(l/16)..+7 of a
-//     32-dim chunk), Q^T held in registers with heads >= G zero. Lane l then holds
-//     head l%16's scores for keys 4*(l/16)..+3 of the tile; a head's row maximum
-//     is a max over the lane's values and lanes ^16, ^32.
-//   O^T (16 dims x 16 heads) += V^T (16 dims x 32 keys) . P^T, P^T straight from
-//     the score registers (two tiles give a lane 8 keys, the MFMA k-order), V^T
-//     read from a per-wave LDS copy of the 32-key V tile with ds_read_b64_tr_b16
-//     (rows padded so each 32-lane phase hits 32 distinct banks).
-//   Loads of the next 32 keys are issued before the current ones are used.
+//   S^T (16 keys x 16 heads) = K (16 keys x 32 dims) . Q^T, Q^T held in registers with
+//     heads >= G zero. Lane l then holds head l%16's scores for keys 4*(l/16)..+3 of
+//     the tile; a head's row maximum is a max over the lane's values and lanes ^16, ^32.
+//   O^T (16 dims x 16 heads) += V^T (16 dims x 32 keys) . P^T, P^T straight from the
+//     score registers (two tiles give a lane 8 keys, the MFMA k-order), V^T read with
+//     ds_read_b64_tr_b16.
+//   K and V reach LDS by non-temporal buffer->LDS DMA into a ring of 32-key tiles (4
+//     stages at head_dim 128, 8 at 64: 64 KiB, so two waves share a CU), 3 (7) tiles
+//     ahead. Rows past the split's end lie outside the tile's buffer range and arrive as
+//     zeros. Measured on one box (B32 Hq32 Hkv8 L8192 D128): the earlier kernel (tiles
+//     loaded into registers one tile ahead, 4 waves per CU) 0.195-0.201 ms; this ring with
+//     default-policy loads 0.193-0.200 ms at any depth from 1 to 3 tiles ahead (2-4 waves
+//     per CU), also with tiles dealt cyclically over a head's waves; with non-temporal
+//     loads 0.168-0.172 ms at every depth. The bound was the cache policy, not the bytes
+//     in flight or the access order.
 // Combine kernel: one workgroup per (batch, query head) folds the splits in a
 // fixed order (independent of timing) and writes O and the LSE.
+#include "attention_dma.hpp"
 #include "tk_common.hpp"
 
 namespace {
@@ -78,86 +84,188 @@ __device__ __forceinline__ i32x4v load16(const void* p) {
   return *reinterpret_cast<const i32x4v*>(p);
 }
 
-// Elements per LDS row of the V tile: D plus 16 (32 bytes) of padding, so the rows
-// one 32-lane ds_read_b64_tr_b16 phase reads fall on 32 distinct banks.
+constexpr int kTileKeys = 32;  // keys per iteration: two 16-key MFMA tiles
+constexpr uint32_t kOob = 0x80000000u;  // past every buffer's range: reads as zero
+// Cache policy of the K/V loads: non-temporal (`nt`). Each key is read once; with the
+// default policy the same kernel streamed at 5.5 TB/s, non-temporal at 6.4 TB/s (B32 Hq32
+// Hkv8 L8192 D128, same box).
+constexpr int kNonTemporal = 2;
+
+// LDS ring of the split kernel: NS stages, each a 32-key tile of K followed by the same
+// keys of V, rows of D elements stored whole (DMA writes 1 KiB of contiguous LDS per
+// instruction, so the layout is a swizzle, not padding).
 template <int D>
-constexpr int vt_row() {
-  return D + 16;
+struct Ring {
+  static constexpr int RB = D * 2;             // bytes per row
+  static constexpr int TILE = kTileKeys * RB;  // bytes per tensor tile
+  static constexpr int STAGE = 2 * TILE;
+  static constexpr int NS = D == 128 ? 4 : 8;  // 64 KiB
+  static constexpr int IPT = TILE / 1024;      // DMA instructions per tensor tile
+  static constexpr int RPI = 1024 / RB;        // rows per DMA instruction
+  static constexpr int CPR = RB / 16;          // 16-byte chunks per row
+  static constexpr int QTILE = 16 * RB;        // Q^T tile: 16 heads
+  // vmcnt is 6 bits: at most 63 DMA instructions may be outstanding.
+  static_assert((NS - 1) * 2 * IPT < 64, "ring deeper than the vmcnt counter");
+  // K: 16-byte chunk c of row r at slot c ^ kswz(r). A ds_read_b128 phase (16 lanes)
+  // takes one chunk of 16 consecutive rows, on 16 distinct bank groups.
+  static __device__ __forceinline__ int kswz(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
+  // V: 32-byte granule g of row r at granule g ^ vswz(r). A transposed read phase (32
+  // lanes) takes one granule of 8 consecutive rows, on 8 distinct granule positions.
+  static __device__ __forceinline__ int vswz(int r) { return D == 128 ? (r & 7) : ((r >> 1) & 3); }
+};
+
+// A wave-uniform address, asserted to the compiler (each half through readfirstlane), so
+// buffer descriptors built from it stay in scalar registers.
+__device__ __forceinline__ void* uniform_ptr(const void* p) {
+  const uint64_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(a >> 32));
+  return reinterpret_cast<void*>((uint64_t(hi) << 32) | lo);
 }
 
-constexpr int kTileKeys = 32;  // keys per iteration: two 16-key MFMA tiles
+// DMA of the 32-key tile starting at key0 of K and V into ring stage `stage`. The buffer
+// ranges end at the split's last key, so rows past it (and whole tiles past the end,
+// issued to keep the wait counts static) read as zero without a memory access.
+template <typename T, int D>
+__device__ __forceinline__ void ring_dma(char* ring, const T* kbase, const T* vbase,
+                                         int64_t kl, int64_t vl, int key0, int k1, int stage,
+                                         const uint32_t* koff, const uint32_t* voff) {
+  using R = Ring<D>;
+  const int rows = min(max(k1 - key0, 0), kTileKeys);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      uniform_ptr(kbase + int64_t(key0) * kl), (short)0,
+      __builtin_amdgcn_readfirstlane(uint32_t(rows * kl * 2)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      uniform_ptr(vbase + int64_t(key0) * vl), (short)0,
+      __builtin_amdgcn_readfirstlane(uint32_t(rows * vl * 2)), 0x00020000);
+  char* dst = ring + stage * R::STAGE;
+#pragma unroll
+  for (int i = 0; i < R::IPT; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (tk_attn::lds_void*)(dst + i * 1024), 16,
+                                             koff[i], 0, 0, kNonTemporal);
+#pragma unroll
+  for (int i = 0; i < R::IPT; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (tk_attn::lds_void*)(dst + R::TILE + i * 1024),
+                                             16, voff[i], 0, 0, kNonTemporal);
+}
 
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kWave) void gqa_decode_split_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int32_t* __restrict__ seqlens, float* __restrict__ partials, DecodeShape s) {
+  using R = Ring<D>;
+  using tk_attn::i32x2;
+  using tk_attn::lds_read_b128;
+  using tk_attn::lds_read_tr16;
+  using tk_attn::pin;
   constexpr int DC = D / 32;     // 32-dim chunks (QK k-steps)
   constexpr int OC = D / 16;     // 16-dim output chunks (PV MFMAs)
-  constexpr int VCH = kTileKeys * D / 8 / kWave;  // 16-byte V chunks per lane per tile
-  constexpr int VRC = D / 8;     // 16-byte chunks per V row
-  constexpr int VR = vt_row<D>();
-  __shared__ __attribute__((aligned(16))) T vt[kTileKeys * VR];
+  constexpr int NS = R::NS, IPT = R::IPT, RB = R::RB;
+  // The ring, then the Q tile: heads kvh G .. +15 (rows past G zero) x D, K's swizzle.
+  __shared__ __attribute__((aligned(1024))) char ring[NS * R::STAGE + R::QTILE];
 
   const int split = blockIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.z;
-  int len = seqlens != nullptr ? seqlens[b] : s.max_len;
+  // Wave-uniform (readfirstlane): the tile's buffer ranges derive from it and must be
+  // scalar, or the compiler wraps each DMA in a loop over the distinct lane values.
+  int len = seqlens != nullptr ? __builtin_amdgcn_readfirstlane(seqlens[b]) : s.max_len;
   len = min(max(len, 0), s.max_len);
   const int k0 = split * s.split_len;
   if (k0 >= len) return;  // the combine kernel reads only splits below len
   const int k1 = min(k0 + s.split_len, len);
+  const int ntiles = (k1 - k0 + kTileKeys - 1) / kTileKeys;
+  auto tile_key = [&](int j) { return k0 + j * kTileKeys; };
 
   const int lane = threadIdx.x;
   const int row16 = lane & 15;   // key of a K fragment / head of a score or output lane
   const int quad = lane >> 4;    // k-group of an MFMA operand / row group of a result
 
-  // Q^T fragments: head row16 (zero past G), dims 32c + 8*quad .. +7.
-  i32x4v qf[DC];
-#pragma unroll
-  for (int c = 0; c < DC; ++c) {
-    qf[c] = i32x4v{0, 0, 0, 0};
-    if (row16 < G) qf[c] = load16(q + b * s.qb + (kvh * G + row16) * s.qh + 32 * c + 8 * quad);
-  }
   const T* kbase = k + b * s.kb + kvh * s.kh;
   const T* vbase = v + b * s.vb + kvh * s.vh;
+  // DMA sources: instruction i of a tile covers rows RPI i .. +RPI-1; this lane fetches the
+  // chunk that belongs at its LDS slot.
+  uint32_t koff[IPT], voff[IPT];
+#pragma unroll
+  for (int i = 0; i < IPT; ++i) {
+    const int row = i * R::RPI + lane / R::CPR;
+    const int slot = lane % R::CPR;
+    koff[i] = uint32_t(row * s.kl * 2) + uint32_t((slot ^ R::kswz(row)) * 16);
+    const int chunk = (((slot >> 1) ^ R::vswz(row)) << 1) | (slot & 1);
+    voff[i] = uint32_t(row * s.vl * 2) + uint32_t(chunk * 16);
+  }
+  // Q^T tile first, by DMA like K and V, so every load of the kernel is counted by the
+  // explicit waits (a register load of Q made the compiler wait for the whole prologue).
+  {
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(q + b * s.qb + int64_t(kvh) * G * s.qh), (short)0,
+        __builtin_amdgcn_readfirstlane(uint32_t((G - 1) * s.qh * 2 + D * 2)), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < R::QTILE / 1024; ++i) {
+      const int head = i * R::RPI + lane / R::CPR;
+      const int slot = lane % R::CPR;
+      const uint32_t off = head < G ? uint32_t(head * s.qh * 2) + uint32_t((slot ^ R::kswz(head)) * 16)
+                                    : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rq, (tk_attn::lds_void*)(ring + NS * R::STAGE + i * 1024), 16, off, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t)
+    ring_dma<T, D>(ring, kbase, vbase, s.kl, s.vl, tile_key(t), k1, t, koff, voff);
 
-  // Loads of one 32-key tile: K fragments (tile t, chunk c) and V 16-byte chunks.
-  i32x4v kf[2][DC], vf[VCH];
-  auto load_tile = [&](int key0) {
+  // LDS lane addresses. K fragment (tile t2 at +16 t2 rows, an immediate): row row16,
+  // chunk 4c + quad. V^T (ds_read_b64_tr_b16: in each 16-lane group, lane 4j + cc reads
+  // row j of a 4 x 16 block, columns 4cc .. +3): rows 4 quad + (row16 >> 2) (+16 for the
+  // second 16 keys), dims 16c + 4 (row16 & 3) .. +3.
+  const uint32_t ring_base = (uint32_t)(uintptr_t)(tk_attn::lds_void*)ring;
+  uint32_t ka[DC], va[OC];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int key = key0 + 16 * t + row16;
+  for (int c = 0; c < DC; ++c) ka[c] = row16 * RB + (((4 * c + quad) ^ R::kswz(row16)) * 16);
+  {
+    const int trow = 4 * quad + (row16 >> 2);
 #pragma unroll
-      for (int c = 0; c < DC; ++c)
-        kf[t][c] = key < k1 ? load16(kbase + static_cast<int64_t>(key) * s.kl + 32 * c + 8 * quad)
-                            : i32x4v{0, 0, 0, 0};
-    }
+    for (int c = 0; c < OC; ++c)
+      va[c] = R::TILE + trow * RB + ((c ^ R::vswz(trow)) * 32) + 8 * (row16 & 3);
+  }
+
+  // Q^T fragments: head row16 (zero past G), dims 32c + 8*quad .. +7.
+  i32x4v qf[DC];
+  tk_attn::wait_vmcnt<(NS - 1) * 2 * IPT>();
 #pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int id = i * kWave + lane;
-      const int key = key0 + id / VRC;
-      vf[i] = key < k1 ? load16(vbase + static_cast<int64_t>(key) * s.vl + 8 * (id % VRC))
-                       : i32x4v{0, 0, 0, 0};
-    }
-  };
+  for (int c = 0; c < DC; ++c) qf[c] = lds_read_b128<0>(ring_base + NS * R::STAGE + ka[c]);
+  tk_attn::wait_lgkm<0>();
+#pragma unroll
+  for (int c = 0; c < DC; ++c) pin(qf[c]);
 
   f32x4v o[OC];
 #pragma unroll
   for (int c = 0; c < OC; ++c) o[c] = f32x4v{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY;  // running maximum of head row16 (identical in its 4 lanes)
+  float m = -INFINITY;  // reference maximum of head row16 (identical in its 4 lanes)
   float l = 0.f;        // this lane's share of head row16's sum
 
-  load_tile(k0);
-  for (int key0 = k0; key0 < k1; key0 += kTileKeys) {
-    i32x4v kc[2][DC], vc[VCH];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int c = 0; c < DC; ++c) kc[t][c] = kf[t][c];
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) vc[i] = vf[i];
-    if (key0 + kTileKeys < k1) load_tile(key0 + kTileKeys);
+  for (int it = 0; it < ntiles; ++it) {
+    // Tile it has landed once at most the NS - 2 younger tiles' loads are outstanding; the
+    // stage read in the previous iteration (its reads have returned) takes tile it + NS - 1.
+    tk_attn::wait_vmcnt<(NS - 2) * 2 * IPT>();
+    ring_dma<T, D>(ring, kbase, vbase, s.kl, s.vl, tile_key(it + NS - 1), k1,
+                   (it + NS - 1) % NS, koff, voff);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t sb = ring_base + (it % NS) * R::STAGE;
+    const int key0 = tile_key(it);
 
+    i32x4v kc[2][DC];
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      kc[0][c] = lds_read_b128<0>(sb + ka[c]);
+      kc[1][c] = lds_read_b128<16 * RB>(sb + ka[c]);
+    }
+    tk_attn::wait_lgkm<0>();
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      pin(kc[0][c]);
+      pin(kc[1][c]);
+    }
     // Scores, scaled to base 2: sc[t][r] is key key0 + 16t + 4*quad + r.
     float sc[2][4];
 #pragma unroll
@@ -169,55 +277,66 @@ __global__ __launch_bounds__(kWave) void gqa_decode_split_kernel(
       for (int r = 0; r < 4; ++r)
         sc[t][r] = key0 + 16 * t + 4 * quad + r < k1 ? acc[r] * s.scale_log2 : -INFINITY;
     }
+    // V^T fragments, read while the softmax runs, in batches of at most 4 output chunks
+    // (8 reads: lgkmcnt counts at most 15 outstanding LDS instructions).
+    constexpr int HB = OC < 4 ? OC : 4;
+    i32x2 lo[OC], hi[OC];
+#pragma unroll
+    for (int c = 0; c < HB; ++c) {
+      lo[c] = lds_read_tr16<0>(sb + va[c]);
+      hi[c] = lds_read_tr16<16 * RB>(sb + va[c]);
+    }
+    // Lazy rescale: the reference maximum m moves only when the tile's maximum exceeds it
+    // by more than 8 (base-2 units), so p <= 2^8 and o, l are rescaled in a few tiles
+    // instead of nearly every one; O = o / l and LSE = m + log2(l) do not depend on m.
     float bmax = sc[0][0];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) bmax = fmaxf(bmax, sc[t][r]);
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-    const float mnew = fmaxf(m, bmax);  // finite: the tile's first key is live
-    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-    m = mnew;
-    float p[2][4];
+    bmax = tk_attn::max_over_column(bmax);  // finite: the tile's first key is live
+    const bool grow = bmax > m + 8.f;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // wave-uniform: a scalar branch
+      const float mnew = grow ? bmax : m;
+      float alpha = __builtin_amdgcn_exp2f(m - mnew);  // 1 if kept, 0 on the first tile
+      // Defined inside the branch, so the multiplies below cannot be hoisted out of it.
+      asm volatile("" : "+v"(alpha));
+      m = mnew;
+      l *= alpha;
+#pragma unroll
+      for (int c = 0; c < OC; ++c) o[c] *= alpha;
+    }
     float psum = 0.f;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        p[t][r] = __builtin_amdgcn_exp2f(sc[t][r] - mnew);
-        psum += p[t][r];
+        sc[t][r] = __builtin_amdgcn_exp2f(sc[t][r] - m);
+        psum += sc[t][r];
       }
-    l = l * alpha + psum;
+    l += psum;
     // P^T operand: head row16, k-order (tile 0 keys 4*quad..+3, tile 1 keys 4*quad..+3).
-    const i32x4v pf = {pack2<T>(p[0][0], p[0][1]), pack2<T>(p[0][2], p[0][3]),
-                       pack2<T>(p[1][0], p[1][1]), pack2<T>(p[1][2], p[1][3])};
-
-    // V tile to LDS (row-major, padded rows), then V^T fragments by transposed reads.
+    const i32x4v pf = {pack2<T>(sc[0][0], sc[0][1]), pack2<T>(sc[0][2], sc[0][3]),
+                       pack2<T>(sc[1][0], sc[1][1]), pack2<T>(sc[1][2], sc[1][3])};
 #pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int id = i * kWave + lane;
-      *reinterpret_cast<i32x4v*>(vt + (id / VRC) * VR + 8 * (id % VRC)) = vc[i];
-    }
-    // ds_read_b64_tr_b16: in each 16-lane group, lane 4j + c addresses row j and
-    // columns 4c..4c+3 of a 4 x 16 block; lane i receives column i of the 4 rows.
-    const int trow = 4 * quad + (row16 >> 2);
-    const int tcol = 4 * (row16 & 3);
+    for (int c0 = 0; c0 < OC; c0 += HB) {
+      tk_attn::wait_lgkm<0>();
 #pragma unroll
-    for (int c = 0; c < OC; ++c) {
-      o[c] *= alpha;
-      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_s16x4*)(vt + trow * VR + 16 * c + tcol));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_s16x4*)(vt + (16 + trow) * VR + 16 * c + tcol));
-      const i32x4v vtf = {__builtin_bit_cast(int, short2{lo[0], lo[1]}),
-                          __builtin_bit_cast(int, short2{lo[2], lo[3]}),
-                          __builtin_bit_cast(int, short2{hi[0], hi[1]}),
-                          __builtin_bit_cast(int, short2{hi[2], hi[3]})};
-      o[c] = mma16<T>(vtf, pf, o[c]);
+      for (int c = c0; c < c0 + HB; ++c) asm volatile("" : "+v"(lo[c]), "+v"(hi[c]));
+      if (c0 + HB < OC) {
+#pragma unroll
+        for (int c = c0 + HB; c < c0 + 2 * HB; ++c) {
+          lo[c] = lds_read_tr16<0>(sb + va[c]);
+          hi[c] = lds_read_tr16<16 * RB>(sb + va[c]);
+        }
+      }
+#pragma unroll
+      for (int c = c0; c < c0 + HB; ++c)
+        o[c] = mma16<T>(i32x4v{lo[c][0], lo[c][1], hi[c][0], hi[c][1]}, pf, o[c]);
     }
   }
+  // The tiles issued past the end still write (zeros) into this wave's LDS.
+  tk_attn::wait_vmcnt<0>();
 
   // A head's sum is spread over its 4 lanes (row16, +16, +32, +48).
   l += __shfl_xor(l, 16);
@@ -344,6 +463,10 @@ extern "C" int tk_gqa_decode(int dtype, const void* q, const void* k, const void
   for (int64_t st : strides)
     if (st < 0 || (st * 2) % 16 != 0)
       return tk::fail("gqa decode: strides must be non-negative multiples of 8 elements");
+  // The DMA tiles address rows through 32-bit buffer offsets (32 rows, or G heads, apart).
+  for (int64_t st : {q_strides[1], k_strides[2], v_strides[2]})
+    if (st >= (int64_t(1) << 24))
+      return tk::fail("gqa decode: head and key strides must be below 2^24 elements");
   DecodeShape s;
   s.batch = static_cast<int>(batch);
   s.q_heads = static_cast<int>(q_heads);

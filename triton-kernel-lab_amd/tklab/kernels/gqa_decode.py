@@ -26,9 +26,9 @@ from tklab import _hip
 _DTYPES = (torch.float16, torch.bfloat16)
 _HEAD_DIMS = (64, 128)
 _GROUPS = (1, 2, 4, 8)
-# Waves the split kernel aims for: one per SIMD of the 256 CUs (its register
-# footprint allows one resident wave per SIMD), so splits are as long as possible.
-_TARGET_SPLITS = 1024
+# Waves the split kernel aims for: two per CU of the 256 CUs (each holds a 64 KiB
+# LDS ring of K/V tiles), so splits are as long as possible.
+_TARGET_SPLITS = 512
 
 
 def gqa_decode(
