@@ -67,3 +67,17 @@ def test_elementwise_limit_is_the_int32_extent() -> None:
     status = lib.tk_swiglu_fwd(1, unaligned, unaligned, unaligned, ctypes.c_int64(1), largest,
                                largest, largest, largest, None)
     assert status != 0 and b"problem too large" not in lib.tk_last_error()
+
+
+def test_gqa_decode_rejects_row_strides_past_its_32_bit_tile_offsets() -> None:
+    """The decode kernel addresses a 32-key tile (or the G query heads) through 32-bit buffer
+    offsets, so key and head strides of 2^24 elements or more are rejected before any launch."""
+    import pytest
+
+    p = 1 << 20  # 16-byte aligned; never dereferenced
+    ok = _hip.int64_array([32 * 128, 128])
+    kv = _hip.int64_array([8 * 1024 * 128, 1024 * 128, 128])
+    big = _hip.int64_array([0, 0, 1 << 24])
+    with pytest.raises(_hip.HipLibraryError, match="below 2"):
+        _hip.call("tk_gqa_decode", 2, p, p, p, p, None, p, None, 1, 32, 8, 1024, 128, 64, ok, big,
+                  kv, ok, 0.1, None)
