@@ -30,7 +30,11 @@ cache reuse; MFMA rows flush 1 GiB before each launch.
 ``measured_roofs`` holds the ceilings this GPU sustains (the library's copy and
 dense-MFMA calibration kernels, the HBM read:write mixes with the better of two store
 policies); every row and ``roofline`` also carry
-``frac_measured`` against them, beside ``frac`` against the published peaks.
+``frac_measured`` against them, beside ``frac`` against the published peaks. The
+softmax row, a launch of ~23 us, also carries the stream roof of its own read:write mix
+at its own bytes per launch (``matched_roof_GBps``, ``frac_matched``): launches that
+short pay a dispatch ramp and last-wave drain of ~1-2 us that the large-array roofs
+amortize.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu] [--only TEXT]
 """
@@ -545,11 +549,36 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         row["reference_ms"] = round(ref_ms, 4)
         row["speedup"] = round(ref_ms / row["ms"], 3)
 
-    def mem_row(name, config, make, nbytes, mix, reps=30, ref=None, ref_make=None, moved=1.0):
+    def matched_roof(reads: int, writes: int, nbytes: int, reps: int) -> float:
+        """Best tk_roof_stream rate for this read:write mix at exactly `nbytes` per launch
+        (nbytes / (reads + writes) per array), back to back over the same number of rotating
+        copies as the row, over the store policies, tile sizes and grid shapes of
+        measured_roofs. A launch this short pays the dispatch ramp and the drain of its
+        last wave, which the large-array roofs amortize."""
+        from tklab import _hip
+
+        part = nbytes // (reads + writes)
+        copies = max(1, -(-(1 << 30) // nbytes))
+        src = torch.empty(copies * reads * part // 4, dtype=torch.int32, device=device)
+        dst = torch.empty(copies * writes * part // 4, dtype=torch.int32, device=device)
+        stream = torch.cuda.current_stream().cuda_stream
+        best = 0.0
+        for policy, tile, grid in itertools.product((0, 1), (8, 16), (0, 8192)):
+            def make(k, policy=policy, tile=tile, grid=grid):
+                return lambda: _hip.call("tk_roof_stream", src.data_ptr() + k * reads * part,
+                                         dst.data_ptr() + k * writes * part, part, reads, writes,
+                                         policy, tile, grid, stream)
+            best = max(best, nbytes / streamed(make, nbytes, reps) / 1e6)
+        del src, dst
+        return best
+
+    def mem_row(name, config, make, nbytes, mix, reps=30, ref=None, ref_make=None, moved=1.0,
+                size_matched=False):
         """`make(i)` returns the launch for tensor copy i (copy 0 may reuse the originals);
         `ref_make(i)` the torch reference's call on the same copy. `mix` is the kernel's
         read:write byte ratio, whose measured roof gives `frac_mix` for the bytes the kernel
-        moves (`moved` times the algorithmic bytes)."""
+        moves (`moved` times the algorithmic bytes). `size_matched`: also the stream roof of
+        that mix at the row's own bytes per launch (`matched_roof_GBps`, `frac_matched`)."""
         if only and only not in name and only not in config:
             return False
         ms = streamed(make, nbytes, reps)
@@ -559,6 +588,11 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         if roofs:
             row["frac_measured"] = round(gbps / roofs["hbm_GBps"], 4)
             row["frac_mix"] = round(moved * gbps / roofs["stream_mixes_GBps"][mix], 4)
+            if size_matched:
+                reads, writes = (int(v) for v in mix.split(":"))
+                roof = matched_roof(reads, writes, int(moved * nbytes), reps)
+                row["matched_roof_GBps"] = round(roof, 1)
+                row["frac_matched"] = round(moved * gbps / roof, 4)
         if moved != 1.0:
             row["moved_GB/s"] = round(moved * gbps, 1)
         add_reference(row, ref, None if ref_make is None else
@@ -625,7 +659,7 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         return lambda: sm._launch((xi,), yi)
 
     mem_row("tk_softmax_fwd", "f32 4096x4096", softmax_copy, 2 * x.numel() * 4, "1:1",
-            ref="torch.softmax",
+            ref="torch.softmax", size_matched=True,
             ref_make=lambda i: (lambda xi: lambda: torch.softmax(xi, -1))(x if i == 0 else x.clone()))
     del x
     # Online softmax (rows past the single-pass limit): f32 [64, 1048576]. Bytes as the
