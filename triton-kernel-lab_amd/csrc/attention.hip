@@ -378,7 +378,8 @@ attn_fwd_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T* __res
 // takes kPreUnroll passes of kThreads / (D/8) consecutive rows; each thread loads its pieces
 // of kPreUnroll rows before any arithmetic, and the row -> (batch, head, position) split is
 // a multiply-shift division (one row per thread with 64-bit divisions: B4 H32 N8192 D128
-// in 93.6 instead of 89.4 us).
+// in 93.6 instead of 89.4 us). O and dO are read once, non-temporally (B4 H32 N8192 D128
+// 89.5 -> 82.3 us, D64 48.9 -> 43.4 us); eight rows per thread instead of four ran 97 us.
 constexpr int kPreUnroll = 4;
 
 template <typename T, int D>
@@ -399,8 +400,8 @@ __global__ __launch_bounds__(kThreads) void attn_bwd_preprocess_kernel(
       const int b = static_cast<int>(head_div.div(static_cast<uint32_t>(bh)));
       const int h = bh - b * static_cast<int>(head_div.d);
       const int64_t off = b * sb + h * sh + i * sn + part * 8;
-      tk::load_vec<T, 8>(O + off, o[u]);
-      tk::load_vec<T, 8>(dO + off, g[u]);
+      tk::load_vec_stream<T, 8>(O + off, o[u]);
+      tk::load_vec_stream<T, 8>(dO + off, g[u]);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[u][e] = g[u][e] = 0.f;
