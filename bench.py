@@ -662,8 +662,8 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
             ref="torch.softmax", size_matched=True,
             ref_make=lambda i: (lambda xi: lambda: torch.softmax(xi, -1))(x if i == 0 else x.clone()))
     del x
-    # Online softmax (rows past the single-pass limit): f32 [64, 1048576]. Bytes as the
-    # single-pass cost model (one read, one write); the kernel reads each row twice.
+    # Online softmax (rows past the single-pass limit): f32 [64, 1048576], 64 chunks per row,
+    # so the single-read kernel (one read, one write: the single-pass cost model).
     xw = torch.randn(64, 1 << 20, device=device, generator=g)
 
     def online_copy(i):
@@ -671,8 +671,7 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         yi = torch.empty_like(xw)
         return lambda: sm._launch_online((xi,), yi)
 
-    mem_row("tk_softmax_online_fwd", "f32 64x1048576", online_copy, 2 * xw.numel() * 4, "2:1",
-            moved=1.5,
+    mem_row("tk_softmax_online_fwd", "f32 64x1048576", online_copy, 2 * xw.numel() * 4, "1:1",
             ref="torch.softmax",
             ref_make=lambda i: (lambda xi: lambda: torch.softmax(xi, -1))(xw if i == 0 else xw.clone()))
     del xw

@@ -50,10 +50,14 @@ int tk_softmax_fwd(int dtype, const void* x, void* y, int64_t rows, int64_t cols
  * for the rows the single-pass kernel rejects (more than 65536 columns). No
  * reference kernel exists; the reference's validator points callers there
  * (src/tklab/kernels/fused_softmax.py:75-79, "use an online softmax").
- * Each row is split into chunks of 16384 columns: a first launch writes every
- * chunk's (max, sum of exp) into `partials`, float32[2 * rows * ceil(cols / 16384)],
- * a second folds a row's partials in a fixed order and writes y.
- * Two reads and one write per element; deterministic. cols <= 2^31 - 1. */
+ * Each row is split into chunks of 16384 columns whose (max, sum of exp) partials
+ * are folded in a fixed order; deterministic, cols <= 2^31 - 1.
+ * `partials` is the workspace, float32[2 * rows * ceil(cols / 16384)], 8-byte aligned; the
+ * call overwrites it (no clearing needed). Rows of at most 64 chunks (1 048 576 columns)
+ * take one launch that reads x once (one read and one write per element; the workgroups
+ * of a row exchange their partials through the workspace, after a small kernel clears
+ * it); wider rows take two launches (partials, then fold and write: two reads, one
+ * write). */
 int tk_softmax_online_fwd(int dtype, const void* x, void* y, float* partials, int64_t rows,
                           int64_t cols, int64_t x_row_stride, int64_t y_row_stride,
                           void* stream);

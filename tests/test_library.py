@@ -81,3 +81,12 @@ def test_gqa_decode_rejects_row_strides_past_its_32_bit_tile_offsets() -> None:
     with pytest.raises(_hip.HipLibraryError, match="below 2"):
         _hip.call("tk_gqa_decode", 2, p, p, p, p, None, p, None, 1, 32, 8, 1024, 128, 64, ok, big,
                   kv, ok, 0.1, None)
+
+
+def test_online_softmax_rejects_a_misaligned_workspace() -> None:
+    """The single-read kernel publishes each chunk's partial as one 64-bit word."""
+    import pytest
+
+    p = 1 << 20  # 16-byte aligned; never dereferenced
+    with pytest.raises(_hip.HipLibraryError, match="8-byte aligned"):
+        _hip.call("tk_softmax_online_fwd", 0, p, p, p + 4, 2, 100000, 100000, 100000, None)

@@ -130,6 +130,58 @@ def test_online_wide_row_sums_to_one_and_is_deterministic() -> None:
     assert torch.equal(online_softmax(x), y)
 
 
+def test_online_single_read_chunk_limit_and_many_rows() -> None:
+    """Exactly 64 chunks per row (the widest single-read row), one column more (the two-launch
+    path), and 256 rows of 7 chunks (1792 workgroups, many rows in flight at once)."""
+    torch.manual_seed(11)
+    _check_online(torch.randn(2, 1 << 20, device="cuda"))
+    _check_online(torch.randn(2, (1 << 20) + 1, device="cuda", dtype=torch.bfloat16))
+    _check_online(torch.randn(256, 100000, device="cuda"))
+
+
+@pytest.mark.parametrize(("rows", "cols", "dtype"), [
+    (5, 200003, torch.float32), (3, 1 << 20, torch.bfloat16), (7, 70001, torch.float16),
+])
+def test_online_single_read_fallback_gives_the_same_bits(rows, cols, dtype, monkeypatch) -> None:
+    """With its bounded wait set to zero polls every workgroup computes its row's partials from
+    x itself; the result must be bitwise that of the exchange through the workspace."""
+    from tklab.kernels.fused_softmax import online_softmax
+
+    torch.manual_seed(rows + cols)
+    x = torch.randn(rows, cols, device="cuda", dtype=dtype) * 3
+    exchanged = online_softmax(x)
+    monkeypatch.setenv("TKLAB_ONLINE_SOFTMAX_POLLS", "0")
+    recomputed = online_softmax(x)
+    torch.cuda.synchronize()
+    assert torch.equal(recomputed, exchanged)
+    assert_close(exchanged, torch.softmax(x.float(), dim=-1).to(dtype))
+
+
+def test_online_single_read_replays_in_a_graph() -> None:
+    """The single-read call (workspace clear + kernel, no memset) captured once and replayed on
+    new inputs, with eager calls and synchronizations between replays: every replay matches
+    the eager call bitwise."""
+    from tklab.kernels.fused_softmax import _launch_online
+
+    x = torch.randn(8, 300000, device="cuda")
+    y = torch.empty_like(x)
+    _launch_online((x,), y)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _launch_online((x,), y)
+    for seed in range(3):
+        gen = torch.Generator(device="cuda").manual_seed(40 + seed)
+        x.copy_(torch.randn(x.shape, device="cuda", generator=gen) * (seed + 1))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = torch.empty_like(x)
+        _launch_online((x,), eager)
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
+        assert_close(y, torch.softmax(x, dim=-1))
+
+
 def test_online_strided_misaligned_and_masked_rows() -> None:
     from tklab.kernels.fused_softmax import _launch_online
 
