@@ -135,7 +135,17 @@ __device__ __forceinline__ int table_row(int row, const tk::FastDiv& positions) 
     return row;
 }
 
-template <typename T, int VEC, bool kPositions = false>
+// Table loads: non-temporal when the tables hold one row per x row (kStreamTables, each table
+// row read once), plain when rows share them (a broadcast or position-indexed table).
+template <typename T, int VEC, bool kStream>
+__device__ __forceinline__ void load_table(const T* p, float* f) {
+  if constexpr (kStream)
+    tk::load_vec_stream<T, VEC>(p, f);
+  else
+    tk::load_vec<T, VEC>(p, f);
+}
+
+template <typename T, int VEC, bool kPositions = false, bool kStreamTables = false>
 __global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ cosv, const T* __restrict__ sinv,
     T* __restrict__ y, uint32_t chunks, tk::FastDiv per_row, int half, int64_t xs, int64_t cs,
@@ -154,8 +164,8 @@ __global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
       const int tr = table_row<kPositions>(p.row, positions);
       tk::load_vec_stream<T, VEC>(xr + p.col, x1[u]);
       tk::load_vec_stream<T, VEC>(xr + half + p.col, x2[u]);
-      tk::load_vec<T, VEC>(cosv + tr * cs + p.col, co[u]);
-      tk::load_vec<T, VEC>(sinv + tr * ss + p.col, si[u]);
+      load_table<T, VEC, kStreamTables>(cosv + tr * cs + p.col, co[u]);
+      load_table<T, VEC, kStreamTables>(sinv + tr * ss + p.col, si[u]);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -177,7 +187,7 @@ __global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
 
 // dx1 = dy1*cos + dy2*sin; dx2 = dy2*cos - dy1*sin;
 // dcos = dy1*x1 + dy2*x2; dsin = -dy1*x2 + dy2*x1  (src/tklab/kernels/rope.py:102-160)
-template <typename T, int VEC, bool kPositions = false>
+template <typename T, int VEC, bool kPositions = false, bool kStreamTables = false>
 __global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ cosv,
     const T* __restrict__ sinv, T* __restrict__ dx, T* __restrict__ dcos, T* __restrict__ dsin,
@@ -198,8 +208,8 @@ __global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
       const int tr = table_row<kPositions>(p.row, positions);
       tk::load_vec_stream<T, VEC>(dyr + p.col, d1[u]);
       tk::load_vec_stream<T, VEC>(dyr + half + p.col, d2[u]);
-      tk::load_vec<T, VEC>(cosv + tr * cs + p.col, co[u]);
-      tk::load_vec<T, VEC>(sinv + tr * ss + p.col, si[u]);
+      load_table<T, VEC, kStreamTables>(cosv + tr * cs + p.col, co[u]);
+      load_table<T, VEC, kStreamTables>(sinv + tr * ss + p.col, si[u]);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -369,13 +379,21 @@ extern "C" int tk_rope_fwd(int dtype, const void* x, const void* cos, const void
   const tk::FastDiv div(static_cast<uint32_t>(per_row));
   const Grid1D g = chunk_grid(chunks);
   hipStream_t s = tk::as_stream(stream);
+  const bool stream_tables = cos_row_stride != 0 && sin_row_stride != 0;
   TK_DISPATCH_DTYPE(dtype, T,
     TK_DISPATCH_VEC(T, vok,
-      hipLaunchKernelGGL((rope_fwd_kernel<T, VEC>), dim3(g.blocks), dim3(kBlock), 0, s,
-                         static_cast<const T*>(x), static_cast<const T*>(cos),
-                         static_cast<const T*>(sin), static_cast<T*>(y), (int)chunks, div,
-                         (int)half_dim, x_row_stride, cos_row_stride, sin_row_stride,
-                         y_row_stride)));
+      if (stream_tables)
+        hipLaunchKernelGGL((rope_fwd_kernel<T, VEC, false, true>), dim3(g.blocks), dim3(kBlock),
+                           0, s, static_cast<const T*>(x), static_cast<const T*>(cos),
+                           static_cast<const T*>(sin), static_cast<T*>(y), (int)chunks, div,
+                           (int)half_dim, x_row_stride, cos_row_stride, sin_row_stride,
+                           y_row_stride);
+      else
+        hipLaunchKernelGGL((rope_fwd_kernel<T, VEC>), dim3(g.blocks), dim3(kBlock), 0, s,
+                           static_cast<const T*>(x), static_cast<const T*>(cos),
+                           static_cast<const T*>(sin), static_cast<T*>(y), (int)chunks, div,
+                           (int)half_dim, x_row_stride, cos_row_stride, sin_row_stride,
+                           y_row_stride)));
   return tk::check_launch("rope_fwd");
 }
 
@@ -399,15 +417,25 @@ extern "C" int tk_rope_bwd(int dtype, const void* dy, const void* x, const void*
   const tk::FastDiv div(static_cast<uint32_t>(per_row));
   const Grid1D g = chunk_grid(chunks);
   hipStream_t s = tk::as_stream(stream);
+  const bool stream_tables = cos_row_stride != 0 && sin_row_stride != 0;
   TK_DISPATCH_DTYPE(dtype, T,
     TK_DISPATCH_VEC(T, vok,
-      hipLaunchKernelGGL((rope_bwd_kernel<T, VEC>), dim3(g.blocks), dim3(kBlock), 0, s,
-                         static_cast<const T*>(dy), static_cast<const T*>(x),
-                         static_cast<const T*>(cos), static_cast<const T*>(sin),
-                         static_cast<T*>(dx), static_cast<T*>(dcos), static_cast<T*>(dsin),
-                         (int)chunks, div, (int)half_dim, dy_row_stride, x_row_stride,
-                         cos_row_stride, sin_row_stride, dx_row_stride, dcos_row_stride,
-                         dsin_row_stride)));
+      if (stream_tables)
+        hipLaunchKernelGGL((rope_bwd_kernel<T, VEC, false, true>), dim3(g.blocks), dim3(kBlock),
+                           0, s, static_cast<const T*>(dy), static_cast<const T*>(x),
+                           static_cast<const T*>(cos), static_cast<const T*>(sin),
+                           static_cast<T*>(dx), static_cast<T*>(dcos), static_cast<T*>(dsin),
+                           (int)chunks, div, (int)half_dim, dy_row_stride, x_row_stride,
+                           cos_row_stride, sin_row_stride, dx_row_stride, dcos_row_stride,
+                           dsin_row_stride);
+      else
+        hipLaunchKernelGGL((rope_bwd_kernel<T, VEC>), dim3(g.blocks), dim3(kBlock), 0, s,
+                           static_cast<const T*>(dy), static_cast<const T*>(x),
+                           static_cast<const T*>(cos), static_cast<const T*>(sin),
+                           static_cast<T*>(dx), static_cast<T*>(dcos), static_cast<T*>(dsin),
+                           (int)chunks, div, (int)half_dim, dy_row_stride, x_row_stride,
+                           cos_row_stride, sin_row_stride, dx_row_stride, dcos_row_stride,
+                           dsin_row_stride)));
   return tk::check_launch("rope_bwd");
 }
 
