@@ -79,6 +79,11 @@ def parse_args() -> argparse.Namespace:
     return p.parse_args()
 
 
+def progress(message: str) -> None:
+    """One line on stderr per finished phase or row (stdout carries only the JSON line)."""
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
 def _traffic_from_summary() -> float | None:
     """HBM bytes per stage-1 launch from the committed rocprofv3 PMC summary."""
     if not TRAFFIC_SUMMARY.is_file():
@@ -598,6 +603,7 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
         add_reference(row, ref, None if ref_make is None else
                       (lambda: streamed(ref_make, nbytes, reps)))
         rows.append(row)
+        progress(f"{name} {config}: {row['ms']} ms")
         return True
 
     def mfma_row(name, config, fn, flops, dtype, reps=10, ref=None, ref_fn=None):
@@ -612,6 +618,7 @@ def kernel_table(torch, device, roofs: dict | None = None, only: str | None = No
             row["frac_measured"] = round(tf / roof, 4)
         add_reference(row, ref, None if ref_fn is None else (lambda: timed(ref_fn(), reps)))
         rows.append(row)
+        progress(f"{name} {config}: {row['ms']} ms")
         return True
 
     import torch.nn.functional as F
@@ -896,6 +903,7 @@ def main() -> int:
     ms_step, dominant, dominant_ms, attribution = time_step(torch, step, args.steps, args.warmup)
     step_bytes = sum(STEP_BYTES.values())
     value = step_bytes / (ms_step / 1e3) / 1e9
+    progress(f"step {ms_step:.4f} ms ({value:.1f} GB/s), {dominant} {dominant_ms:.5f} ms")
     ref_step_ms = torch_gpu_step_ms(torch, step, max(10, args.steps // 4))
 
     achieved = STEP_BYTES[dominant] / (dominant_ms / 1e3) / 1e9
@@ -943,6 +951,7 @@ def main() -> int:
     del step
     torch.cuda.empty_cache()
     roofs = measured_roofs(torch, device)
+    progress(f"measured roofs: HBM {roofs['hbm_GBps']} GB/s")
     line["measured_roofs"] = roofs
     roofline["measured_peak"] = roofs["hbm_GBps"]
     roofline["frac_measured"] = round(achieved / roofs["hbm_GBps"], 4)
@@ -955,6 +964,7 @@ def main() -> int:
         line["kernels"] = kernel_table(torch, device, roofs, args.only)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch)
+        progress(f"cpu baseline {line['cpu_baseline']['value']} GB/s")
         line["cpu_oracle_port"] = cpu_oracle_port(args.cpu_seconds)
     else:
         line["cpu_baseline"] = None
