@@ -94,3 +94,26 @@ def test_results_are_bitwise_reproducible() -> None:
     a = gqa_decode(q, k, v)
     b = gqa_decode(q, k, v)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("group", [1, 4, 8])
+def test_one_split_writes_the_output_directly(dtype, d, group, monkeypatch) -> None:
+    """With one split per (batch, KV head) the split wave normalizes and writes O and the LSE
+    (no combine pass); empty and clamped lengths write O = 0, LSE = -inf."""
+    import tklab.kernels.gqa_decode as gd
+
+    monkeypatch.setattr(gd, "split_length", lambda b, h, n: max(64, -(-n // 64) * 64))
+    q, k, v = _case(4, 2 * group, 2, 1500, d, dtype, seed=30 + group + d)
+    _check(q, k, v)
+    lens = torch.tensor([1500, 0, 1, 777], device="cuda", dtype=torch.int32)
+    o, lse = _check(q, k, v, lens)
+    assert torch.all(o[1] == 0) and torch.all(torch.isneginf(lse[1]))
+
+
+def test_benchmark_shape_takes_one_split() -> None:
+    from tklab.kernels.gqa_decode import split_length
+
+    assert split_length(32, 8, 8192) == 8192
+    assert split_length(4, 8, 8192) < 8192
