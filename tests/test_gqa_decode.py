@@ -111,9 +111,3 @@ def test_one_split_writes_the_output_directly(dtype, d, group, monkeypatch) -> N
     o, lse = _check(q, k, v, lens)
     assert torch.all(o[1] == 0) and torch.all(torch.isneginf(lse[1]))
 
-
-def test_benchmark_shape_takes_one_split() -> None:
-    from tklab.kernels.gqa_decode import split_length
-
-    assert split_length(32, 8, 8192) == 8192
-    assert split_length(4, 8, 8192) < 8192

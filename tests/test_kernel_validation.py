@@ -244,9 +244,9 @@ def test_gqa_decode_contract() -> None:
         gqa_decode(q.float(), k.float(), k.float())
     with pytest.raises(ValueError, match="requires CUDA"):
         gqa_decode(q, k, k)
-    # Splits: multiples of 64 keys, about 512 waves (two per CU), never longer than the cache;
-    # one split per (batch, KV head) from 256 pairs on.
+    # Splits: multiples of 64 keys, about 512 waves (two per CU), never longer than the cache.
     assert split_length(8, 8, 8192) == 1024
-    assert split_length(32, 8, 8192) == 8192
+    assert split_length(32, 8, 8192) == 4096
+    assert split_length(64, 8, 8192) == 8192
     assert split_length(1, 1, 100) == 64
     assert all(split_length(b, 8, n) % 64 == 0 for b in (1, 7, 64) for n in (1, 999, 70000))

@@ -29,10 +29,6 @@ _GROUPS = (1, 2, 4, 8)
 # Waves the split kernel aims for: two per CU of the 256 CUs (each holds a 64 KiB
 # LDS ring of K/V tiles), so splits are as long as possible.
 _TARGET_SPLITS = 512
-# From this many (batch, KV head) pairs on, one wave per pair covers the whole cache: the
-# split kernel then writes O and the LSE itself and the combine pass is not launched
-# (B32 Hkv8 L8192 D128: one wave per CU streams the cache as fast as two).
-_ONE_SPLIT_PAIRS = 256
 
 
 def gqa_decode(
@@ -69,10 +65,9 @@ def gqa_decode(
 
 
 def split_length(batch: int, kv_heads: int, max_len: int) -> int:
-    """Keys per split-kernel wave: a multiple of 64 giving about _TARGET_SPLITS waves, or the
-    whole cache when there are at least _ONE_SPLIT_PAIRS (batch, KV head) pairs."""
-    if batch * kv_heads >= _ONE_SPLIT_PAIRS:
-        return max(64, -(-max_len // 64) * 64)
+    """Keys per split-kernel wave: a multiple of 64 giving about _TARGET_SPLITS waves (one
+    split per (batch, KV head) once there are that many pairs: the split wave then writes O
+    and the LSE itself and no combine pass runs)."""
     per = math.ceil(batch * kv_heads * max_len / _TARGET_SPLITS)
     return min(max(64, -(-per // 64) * 64), max(64, -(-max_len // 64) * 64))
 
