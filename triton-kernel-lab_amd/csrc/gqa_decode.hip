@@ -412,17 +412,33 @@ __global__ __launch_bounds__(kCombineThreads) void gqa_decode_combine_kernel(
   len = min(max(len, 0), s.max_len);
   const int nsplit = (len + s.split_len - 1) / s.split_len;
   const float* pr = partials + (static_cast<int64_t>(b) * s.q_heads + h) * s.splits * PS;
-  float mx = -INFINITY;
-  for (int i = t; i < nsplit; i += kCombineThreads) mx = fmaxf(mx, pr[i * PS + D]);
-  mx = tk::group_allreduce<kCombineThreads>(mx, tk::MaxOp{}, red);
   const int d = t % D;
   const int slice = t / D;
-  float acc = 0.f, lsum = 0.f;
-  if (mx != -INFINITY) {
-    for (int i = slice; i < nsplit; i += R) {
-      const float w = __builtin_amdgcn_exp2f(pr[i * PS + D] - mx);
-      lsum += pr[i * PS + D + 1] * w;
-      acc += pr[i * PS + d] * w;
+  float mx = -INFINITY, acc = 0.f, lsum = 0.f;
+  if (nsplit <= R) {
+    // At most one split per slice: its m, l and column d are loaded together, before the
+    // maximum is formed (one round trip to memory instead of two); the same folds as below.
+    float mi = -INFINITY, li = 0.f, oi = 0.f;
+    if (slice < nsplit) {
+      mi = pr[slice * PS + D];
+      li = pr[slice * PS + D + 1];
+      oi = pr[slice * PS + d];
+    }
+    mx = tk::group_allreduce<kCombineThreads>(mi, tk::MaxOp{}, red);
+    if (mx != -INFINITY && slice < nsplit) {
+      const float w = __builtin_amdgcn_exp2f(mi - mx);
+      lsum = 0.f + li * w;
+      acc = 0.f + oi * w;
+    }
+  } else {
+    for (int i = t; i < nsplit; i += kCombineThreads) mx = fmaxf(mx, pr[i * PS + D]);
+    mx = tk::group_allreduce<kCombineThreads>(mx, tk::MaxOp{}, red);
+    if (mx != -INFINITY) {
+      for (int i = slice; i < nsplit; i += R) {
+        const float w = __builtin_amdgcn_exp2f(pr[i * PS + D] - mx);
+        lsum += pr[i * PS + D + 1] * w;
+        acc += pr[i * PS + d] * w;
+      }
     }
   }
   acc_s[slice][d] = acc;
