@@ -1,0 +1,245 @@
+"""Seeded random-shape parity sweep over the public entry points.
+
+Each case draws its shape from a fixed seed (so a failure names a reproducible
+shape) inside the limits the entry point documents, and compares the HIP result
+with float32 PyTorch math of the same operation at the tolerances the per-kernel
+tests use: elementwise at the storage dtype's tolerance where the kernel rounds
+once (softmax, norms, SwiGLU, RoPE, GEMM, attention output), relative Frobenius
+for gradients that sum many rounded products (attention backward). The shapes
+favour the edges the kernels special-case: widths off the vector width, row
+counts off the workgroup tiles, sequence lengths off the 64-row blocks, K steps
+off the prefetch depth.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from tklab.harness.tolerances import assert_close, assert_relative_frobenius
+from tklab.kernels.flash_attention import grouped_query_attention
+from tklab.kernels.fused_softmax import online_softmax, softmax
+from tklab.kernels.gqa_decode import gqa_decode
+from tklab.kernels.matmul import matmul_fp32acc
+from tklab.kernels.residual_rms_norm import residual_rms_norm
+from tklab.kernels.rms_norm import rms_norm
+from tklab.kernels.rope import rope
+from tklab.kernels.swiglu import swiglu
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float16, torch.bfloat16]
+CASES = range(8)
+
+
+def _seeded(op: str, case: int) -> np.random.RandomState:
+    """Shape generator of one case (seeded from the op's name bytes, not the salted hash)."""
+    return np.random.RandomState(sum(op.encode()) * 100 + case)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_softmax(case: int) -> None:
+    r = _seeded("softmax", case)
+    rows = int(r.randint(1, 300))
+    cols = int(r.choice([r.randint(1, 4096), r.randint(4096, 65537)]))
+    dtype = [torch.float32, torch.float16, torch.bfloat16][case % 3]
+    torch.manual_seed(case)
+    x = (torch.randn(rows, cols, device="cuda") * float(r.uniform(0.5, 8))).to(dtype)
+    assert_close(softmax(x), torch.softmax(x.float(), dim=-1))
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_online_softmax(case: int) -> None:
+    r = _seeded("online", case)
+    rows = int(r.randint(1, 9))
+    # Up to 80 chunks of 16384 columns: both the single-read kernel (<= 64 chunks) and
+    # the two-launch path, with a ragged last chunk.
+    cols = int(r.randint(1, 80 * 16384))
+    dtype = [torch.float32, torch.bfloat16, torch.float16][case % 3]
+    torch.manual_seed(case)
+    x = (torch.randn(rows, cols, device="cuda") * float(r.uniform(0.5, 8))).to(dtype)
+    y = online_softmax(x)
+    assert_close(y, torch.softmax(x.float(), dim=-1))
+    sums = y.double().sum(dim=1)
+    torch.testing.assert_close(sums, torch.ones_like(sums), rtol=0, atol=2e-2 if dtype != torch.float32 else 1e-4)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_rms_norm_forward_and_backward(case: int) -> None:
+    r = _seeded("rmsnorm", case)
+    rows = int(r.randint(1, 700))
+    cols = int(r.randint(1, 9000))
+    dtype = DTYPES[case % 2] if case < 6 else torch.float32
+    torch.manual_seed(case)
+    x = torch.randn(rows, cols, device="cuda", dtype=dtype, requires_grad=True)
+    w = (1 + 0.1 * torch.randn(cols, device="cuda")).to(dtype).requires_grad_(True)
+    dy = torch.randn(rows, cols, device="cuda", dtype=dtype)
+    y = rms_norm(x, w)
+    dx, dw = torch.autograd.grad(y, (x, w), grad_outputs=dy)
+    xf, wf = x.detach().float().requires_grad_(True), w.detach().float().requires_grad_(True)
+    yf = F.rms_norm(xf, (cols,), wf, eps=1e-6)
+    dxf, dwf = torch.autograd.grad(yf, (xf, wf), grad_outputs=dy.float())
+    assert_close(y, yf)
+    assert_close(dx, dxf)
+    assert_relative_frobenius(dw, dwf, max_relative_error=1e-2)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_residual_rms_norm_forward_and_backward(case: int) -> None:
+    r = _seeded("residual", case)
+    rows = int(r.randint(1, 600))
+    cols = int(r.randint(8, 8200))
+    dtype = DTYPES[case % 2]
+    torch.manual_seed(case)
+    x = torch.randn(rows, cols, device="cuda", dtype=dtype, requires_grad=True)
+    res = torch.randn(rows, cols, device="cuda", dtype=dtype, requires_grad=True)
+    w = (1 + 0.1 * torch.randn(cols, device="cuda")).to(dtype).requires_grad_(True)
+    ds_in = torch.randn(rows, cols, device="cuda", dtype=dtype)
+    dy = torch.randn(rows, cols, device="cuda", dtype=dtype)
+    s, y = residual_rms_norm(x, res, w)
+    grads = torch.autograd.grad((s, y), (x, res, w), grad_outputs=(ds_in, dy))
+    # The residual sum is rounded to the storage dtype before the norm, as the kernel does.
+    s_ref = (x.detach() + res.detach()).float().requires_grad_(True)
+    wf = w.detach().float().requires_grad_(True)
+    y_ref = F.rms_norm(s_ref, (cols,), wf, eps=1e-6)
+    ds_ref, dw_ref = torch.autograd.grad(y_ref, (s_ref, wf), grad_outputs=dy.float())
+    ds_ref = ds_ref + ds_in.float()
+    assert torch.equal(s, x.detach() + res.detach())
+    assert_close(y, y_ref)
+    assert_close(grads[0], ds_ref)
+    assert torch.equal(grads[0], grads[1])
+    assert_relative_frobenius(grads[2], dw_ref, max_relative_error=1e-2)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_swiglu_forward_and_backward(case: int) -> None:
+    r = _seeded("swiglu", case)
+    rows = int(r.randint(1, 500))
+    cols = int(r.randint(1, 5000))
+    dtype = DTYPES[case % 2] if case < 6 else torch.float32
+    torch.manual_seed(case)
+    value = torch.randn(rows, cols, device="cuda", dtype=dtype, requires_grad=True)
+    gate = (torch.randn(rows, cols, device="cuda") * 4).to(dtype).requires_grad_(True)
+    dy = torch.randn(rows, cols, device="cuda", dtype=dtype)
+    y = swiglu(value, gate)
+    dv, dg = torch.autograd.grad(y, (value, gate), grad_outputs=dy)
+    vf, gf = (t.detach().float().requires_grad_(True) for t in (value, gate))
+    yf = vf * F.silu(gf)
+    dvf, dgf = torch.autograd.grad(yf, (vf, gf), grad_outputs=dy.float())
+    assert_close(y, yf)
+    assert_close(dv, dvf)
+    assert_close(dg, dgf)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_rope_forward_and_backward(case: int) -> None:
+    r = _seeded("rope", case)
+    rows = int(r.randint(1, 900))
+    cols = 2 * int(r.randint(1, 160))
+    dtype = DTYPES[case % 2] if case < 6 else torch.float32
+    torch.manual_seed(case)
+    x = torch.randn(rows, cols, device="cuda", dtype=dtype, requires_grad=True)
+    angles = torch.randn(rows, cols // 2, device="cuda") * 3
+    cos = torch.cos(angles).to(dtype).requires_grad_(True)
+    sin = torch.sin(angles).to(dtype).requires_grad_(True)
+    dy = torch.randn(rows, cols, device="cuda", dtype=dtype)
+    y = rope(x, cos, sin)
+    grads = torch.autograd.grad(y, (x, cos, sin), grad_outputs=dy)
+    xf, cf, sf = (t.detach().float().requires_grad_(True) for t in (x, cos, sin))
+    a, b = xf.chunk(2, dim=-1)
+    yf = torch.cat((a * cf - b * sf, b * cf + a * sf), dim=-1)
+    refs = torch.autograd.grad(yf, (xf, cf, sf), grad_outputs=dy.float())
+    assert_close(y, yf)
+    for g, ref in zip(grads, refs):
+        assert_close(g, ref)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_gemm(case: int) -> None:
+    r = _seeded("gemm", case)
+    m = int(r.randint(1, 700))
+    # Even cases take the DMA kernel (K % 32 == 0, N % 8 == 0), odd ones the general path.
+    if case % 2 == 0:
+        n, k = 8 * int(r.randint(1, 140)), 32 * int(r.randint(1, 40))
+    else:
+        n, k = int(r.randint(1, 700)), int(r.randint(1, 900))
+    dtype = DTYPES[(case // 2) % 2]
+    torch.manual_seed(case)
+    scale = k ** -0.25
+    a = (torch.randn(m, k, device="cuda") * scale).to(dtype)
+    b = (torch.randn(k, n, device="cuda") * scale).to(dtype)
+    assert_close(matmul_fp32acc(a, b), a.float() @ b.float())
+
+
+def _attention32(q, k, v, do, causal):
+    """Output and gradients of softmax(Q K^T / sqrt(d)) V in float32, K/V repeated per group."""
+    group = q.shape[1] // k.shape[1]
+    qf = q.detach().float().requires_grad_(True)
+    kf = k.detach().float().requires_grad_(True)
+    vf = v.detach().float().requires_grad_(True)
+    kr = kf.repeat_interleave(group, dim=1)
+    vr = vf.repeat_interleave(group, dim=1)
+    s = torch.matmul(qf, kr.transpose(-2, -1).contiguous()) * q.shape[-1] ** -0.5
+    if causal:
+        n = q.shape[-2]
+        s = s.masked_fill(torch.triu(torch.ones(n, n, dtype=torch.bool, device="cuda"), 1), -torch.inf)
+    o = torch.matmul(torch.softmax(s, dim=-1), vr)
+    grads = torch.autograd.grad(o, (qf, kf, vf), grad_outputs=do.float())
+    return o.detach(), grads
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_attention_forward_and_backward(case: int) -> None:
+    r = _seeded("attention", case)
+    batch = int(r.randint(1, 3))
+    kv_heads = int(r.randint(1, 3))
+    group = int(r.choice([1, 2, 4]))
+    n = int(r.randint(1, 520))
+    d = int(r.choice([64, 128]))
+    causal = bool(case % 2)
+    dtype = DTYPES[(case // 2) % 2]
+    torch.manual_seed(case)
+    shape_q = (batch, kv_heads * group, n, d)
+    q = torch.randn(shape_q, device="cuda", dtype=dtype, requires_grad=True)
+    k = torch.randn(batch, kv_heads, n, d, device="cuda", dtype=dtype, requires_grad=True)
+    v = torch.randn(batch, kv_heads, n, d, device="cuda", dtype=dtype, requires_grad=True)
+    do = torch.randn(shape_q, device="cuda", dtype=dtype)
+    o = grouped_query_attention(q, k, v, causal=causal)
+    got = torch.autograd.grad(o, (q, k, v), grad_outputs=do)
+    o_ref, refs = _attention32(q, k, v, do, causal)
+    assert_close(o, o_ref)
+    for g, ref in zip(got, refs):
+        assert torch.isfinite(g).all()
+        assert_relative_frobenius(g, ref, max_relative_error=1e-2)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_gqa_decode(case: int) -> None:
+    r = _seeded("decode", case)
+    batch = int(r.randint(1, 5))
+    kv_heads = int(r.randint(1, 4))
+    group = int(r.choice([1, 2, 4, 8]))
+    max_len = int(r.randint(1, 3000))
+    d = int(r.choice([64, 128]))
+    dtype = DTYPES[case % 2]
+    torch.manual_seed(case)
+    q = torch.randn(batch, kv_heads * group, d, device="cuda", dtype=dtype)
+    kc = torch.randn(batch, kv_heads, max_len, d, device="cuda", dtype=dtype)
+    vc = torch.randn(batch, kv_heads, max_len, d, device="cuda", dtype=dtype)
+    lens = torch.from_numpy(r.randint(0, max_len + 1, size=batch).astype(np.int32)).cuda()
+    o, lse = gqa_decode(q, kc, vc, lens, return_lse=True)
+    kr = kc.float().repeat_interleave(group, dim=1)
+    vr = vc.float().repeat_interleave(group, dim=1)
+    s = torch.matmul(q.float().unsqueeze(2), kr.transpose(-2, -1).contiguous()).squeeze(2)
+    s = s * d ** -0.5
+    valid = torch.arange(max_len, device="cuda")[None, :] < lens[:, None].long()
+    s = s.masked_fill(~valid[:, None, :], -torch.inf)
+    p = torch.softmax(s, dim=-1).nan_to_num(0.0)
+    o_ref = torch.matmul(p.unsqueeze(2), vr).squeeze(2)
+    lse_ref = torch.logsumexp(s, dim=-1) / np.log(2.0)
+    assert_close(o, o_ref)
+    empty = lens == 0
+    assert torch.all(torch.isneginf(lse[empty]))
+    torch.testing.assert_close(lse[~empty], lse_ref[~empty], rtol=1e-5, atol=1e-5)
