@@ -19,6 +19,7 @@ import torch
 import torch.nn.functional as F
 
 from tklab.harness.tolerances import assert_close, assert_relative_frobenius
+from tklab.kernels._norm_common import EPS
 from tklab.kernels.flash_attention import grouped_query_attention
 from tklab.kernels.fused_softmax import online_softmax, softmax
 from tklab.kernels.gqa_decode import gqa_decode
@@ -79,7 +80,7 @@ def test_rms_norm_forward_and_backward(case: int) -> None:
     y = rms_norm(x, w)
     dx, dw = torch.autograd.grad(y, (x, w), grad_outputs=dy)
     xf, wf = x.detach().float().requires_grad_(True), w.detach().float().requires_grad_(True)
-    yf = F.rms_norm(xf, (cols,), wf, eps=1e-6)
+    yf = F.rms_norm(xf, (cols,), wf, eps=EPS)
     dxf, dwf = torch.autograd.grad(yf, (xf, wf), grad_outputs=dy.float())
     assert_close(y, yf)
     assert_close(dx, dxf)
@@ -103,7 +104,7 @@ def test_residual_rms_norm_forward_and_backward(case: int) -> None:
     # The residual sum is rounded to the storage dtype before the norm, as the kernel does.
     s_ref = (x.detach() + res.detach()).float().requires_grad_(True)
     wf = w.detach().float().requires_grad_(True)
-    y_ref = F.rms_norm(s_ref, (cols,), wf, eps=1e-6)
+    y_ref = F.rms_norm(s_ref, (cols,), wf, eps=EPS)
     ds_ref, dw_ref = torch.autograd.grad(y_ref, (s_ref, wf), grad_outputs=dy.float())
     ds_ref = ds_ref + ds_in.float()
     assert torch.equal(s, x.detach() + res.detach())
