@@ -13,6 +13,9 @@
  *     allocates or frees device memory: every output and workspace is passed in.
  *   - Sizes and strides are in ELEMENTS, as int64_t. Every feature dimension is
  *     unit-stride; the strides given are the remaining (row/batch/head) ones.
+ *     Strides are >= 0 (0 repeats one row, e.g. a broadcast table); a negative
+ *     stride, a size <= 0 or sizes whose product leaves the kernels' index range
+ *     are rejected before anything is enqueued.
  *   - `dtype` is one of TK_DTYPE_*; all tensors of one call share it unless a
  *     parameter says otherwise (statistics and workspaces are float32).
  *   - `stream` is a hipStream_t (0 = the null stream). Work is enqueued

@@ -90,3 +90,104 @@ def test_online_softmax_rejects_a_misaligned_workspace() -> None:
     p = 1 << 20  # 16-byte aligned; never dereferenced
     with pytest.raises(_hip.HipLibraryError, match="8-byte aligned"):
         _hip.call("tk_softmax_online_fwd", 0, p, p, p + 4, 2, 100000, 100000, 100000, None)
+
+
+def _probe_args(name: str, *, dtype: int, pointer, size: int, stride: int, array: list[int]):
+    """Arguments for entry point ``name`` from its signature: the first int32 is the dtype
+    code (the activation kind follows it), pointers, the leading int64 values sizes (two,
+    or three for the GEMMs' m, n, k and RoPE's rows, seq, half_dim), the later int64 values
+    strides, int64 arrays stride tables, floats 0.1."""
+    values, ints, n64 = [], 0, 0
+    sizes = _SIZE_ARGS.get(name, 2)
+    for kind in _hip._SIGNATURES[name]:
+        if kind is _hip._I32:
+            values.append(dtype if ints == 0 else 0)
+            ints += 1
+        elif kind is _hip._P:
+            values.append(pointer)
+        elif kind is _hip._I64:
+            n64 += 1
+            values.append(size if n64 <= sizes else stride)
+        elif kind is _hip._F32:
+            values.append(0.1)
+        else:
+            values.append(_hip.int64_array(array))
+    return values
+
+
+_COMPUTE = sorted(n for n in _hip._SIGNATURES if not n.startswith("tk_roof"))
+_SIZE_ARGS = {"tk_gemm": 3, "tk_gemm_rowscale": 3, "tk_gemm_swiglu": 3, "tk_rope_positions": 3}
+_NO_STRIDES = {"tk_rmsnorm_bwd_stage2", "tk_layernorm_bwd_stage2"}
+
+
+def _rejected_before_launch(name: str, values) -> str:
+    import pytest
+
+    with pytest.raises(_hip.HipLibraryError) as info:
+        _hip.call(name, *values)
+    message = str(info.value)
+    assert "launch failed" not in message, message
+    return message
+
+
+def _cpu_only() -> None:
+    """These probes pass pointers that are never valid device memory: run them only where
+    no GPU could receive a launch."""
+    import pytest
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("argument probes run without a GPU")
+
+
+import pytest  # noqa: E402
+
+
+@pytest.mark.parametrize("name", _COMPUTE)
+def test_every_entry_point_rejects_null_pointers(name: str) -> None:
+    _cpu_only()
+    values = _probe_args(name, dtype=2, pointer=None, size=64, stride=64,
+                         array=[64 * 64 * 128, 64 * 128, 128, 1])
+    assert "null pointer" in _rejected_before_launch(name, values)
+
+
+@pytest.mark.parametrize("name", _COMPUTE)
+def test_every_entry_point_rejects_an_unknown_dtype(name: str) -> None:
+    _cpu_only()
+    values = _probe_args(name, dtype=7, pointer=1 << 20, size=64, stride=64,
+                         array=[64 * 64 * 128, 64 * 128, 128, 1])
+    assert "dtype" in _rejected_before_launch(name, values)
+
+
+@pytest.mark.parametrize("name", _COMPUTE)
+def test_every_entry_point_rejects_negative_sizes(name: str) -> None:
+    """Negative sizes whose product is positive (rows = cols = -1) included: the
+    contiguous-row fold of the elementwise kernels once turned them into one element."""
+    _cpu_only()
+    values = _probe_args(name, dtype=2, pointer=1 << 20, size=-1, stride=-1,
+                         array=[64 * 64 * 128, 64 * 128, 128, 1])
+    _rejected_before_launch(name, values)
+
+
+@pytest.mark.parametrize("name", sorted(set(_COMPUTE) - _NO_STRIDES))
+def test_every_entry_point_rejects_negative_strides(name: str) -> None:
+    """Row strides as int64 arguments, or (attention, decode) stride tables: a negative
+    entry is refused with the layout error, not reached by a launch."""
+    _cpu_only()
+    if _hip._I64P in _hip._SIGNATURES[name]:
+        values = _probe_args(name, dtype=2, pointer=1 << 20, size=64, stride=64,
+                             array=[-64 * 64 * 128, -64 * 128, -128, 1])
+    else:
+        values = _probe_args(name, dtype=2, pointer=1 << 20, size=64, stride=-64,
+                             array=[64 * 64 * 128, 64 * 128, 128, 1])
+    assert "stride" in _rejected_before_launch(name, values)
+
+
+def test_sizes_whose_product_overflows_are_rejected() -> None:
+    _cpu_only()
+    huge = 1 << 40
+    for name in ("tk_swiglu_fwd", "tk_activation_fwd"):
+        values = _probe_args(name, dtype=2, pointer=1 << 20, size=huge, stride=huge, array=[1])
+        if name == "tk_activation_fwd":
+            values[1] = 0  # kind
+        assert "too large" in _rejected_before_launch(name, values)

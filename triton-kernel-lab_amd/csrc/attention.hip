@@ -720,7 +720,8 @@ int check_common(const char* what, int dtype, int64_t batch, int64_t heads, int6
 bool strides_ok(const int64_t* st, int64_t batch, int64_t heads, int64_t seq, int64_t d) {
   for (int i = 0; i < 3; ++i)
     if (st[i] <= 0 || st[i] % 8 != 0) return false;
-  return (batch - 1) * st[0] + (heads - 1) * st[1] + (seq - 1) * st[2] + d - 1 <= INT32_MAX;
+  // 128-bit sum: no stride or size makes it wrap.
+  return tk::extent(batch, st[0], heads, st[1]) + tk::extent(seq, st[2], d, 1) <= INT32_MAX;
 }
 
 }  // namespace
@@ -794,9 +795,11 @@ extern "C" int tk_attn_bwd_preprocess(int dtype, const void* o, const void* dout
                                       int64_t head_dim, const int64_t* strides, void* stream) {
   if (check_common("attn_bwd_preprocess", dtype, batch, heads, seq, head_dim)) return 1;
   if (!o || !dout || !delta || !strides) return tk::fail("attn_bwd_preprocess: null pointer");
-  if (!strides_ok(strides, batch, heads, seq, head_dim) || !tk::aligned16(o) ||
-      !tk::aligned16(dout))
-    return tk::fail("attn_bwd_preprocess: unsupported layout");
+  if (!strides_ok(strides, batch, heads, seq, head_dim))
+    return tk::fail("attn_bwd_preprocess: strides must be positive multiples of 8 within int32 "
+                    "range");
+  if (!tk::aligned16(o) || !tk::aligned16(dout))
+    return tk::fail("attn_bwd_preprocess: tensors must be 16-byte aligned");
   const int64_t rows = batch * heads * seq;
   if (rows > INT32_MAX / 2) return tk::fail("attn_bwd_preprocess: too many rows");
   const int64_t rows_per_block = kThreads / (head_dim / 8) * kPreUnroll;
@@ -1043,7 +1046,7 @@ int varlen_check(const char* what, int dtype, const void* const* ptrs, int nptr,
     if (!st) return tk::fail("%s: null pointer", what);
     const int64_t h = kv_side[i] ? kv_heads : heads;
     if (st[0] <= 0 || st[1] <= 0 || st[0] % 8 || st[1] % 8 ||
-        (total - 1) * st[0] + (h - 1) * st[1] + head_dim - 1 > INT32_MAX)
+        tk::extent(total, st[0], h, st[1]) + head_dim - 1 > INT32_MAX)
       return tk::fail("%s: strides must be positive multiples of 8 within int32 range", what);
     // Each head's rows go through one 32-bit buffer range.
     if (((total - 1) * st[0] + head_dim) * 2 >= (int64_t(1) << 31))

@@ -260,9 +260,8 @@ extern "C" int tk_gemm(int dtype, const void* a, const void* b, void* c, int64_t
     return tk::fail("gemm: strides must be positive");
   // 32-bit element offsets inside the kernel.
   const int64_t lim = INT32_MAX;
-  if (m > lim || n > lim || k > lim || (m - 1) * stride_am + (k - 1) * stride_ak > lim ||
-      (k - 1) * stride_bk + (n - 1) * stride_bn > lim ||
-      (m - 1) * stride_cm + (n - 1) * stride_cn > lim)
+  if (m > lim || n > lim || k > lim || tk::extent(m, stride_am, k, stride_ak) > lim ||
+      tk::extent(k, stride_bk, n, stride_bn) > lim || tk::extent(m, stride_cm, n, stride_cn) > lim)
     return tk::fail("gemm: operand exceeds the int32 offset range");
   const int64_t tiles_m = tk::cdiv(m, BM), tiles_n = tk::cdiv(n, BN);
   if (tiles_m * tiles_n > INT32_MAX) return tk::fail("gemm: too many tiles");
@@ -309,7 +308,7 @@ extern "C" int tk_gemm_swiglu(int dtype, const void* a, const void* b_gate, cons
   if (m <= 0 || n <= 0 || k <= 0) return tk::fail("gemm_swiglu: empty problem");
   if (stride_ym <= 0 || stride_yn <= 0) return tk::fail("gemm_swiglu: strides must be positive");
   const int64_t lim = INT32_MAX;
-  if (m > lim || n > lim || k > lim || (m - 1) * stride_ym + (n - 1) * stride_yn > lim)
+  if (m > lim || n > lim || k > lim || tk::extent(m, stride_ym, n, stride_yn) > lim)
     return tk::fail("gemm_swiglu: operand exceeds the int32 offset range");
   if (!tk::gemm_dma_applies(a, b_gate, m, n, k, stride_am, stride_ak, stride_gk, stride_gn) ||
       !tk::gemm_dma_applies(a, b_up, m, n, k, stride_am, stride_ak, stride_uk, stride_un))
@@ -332,7 +331,7 @@ extern "C" int tk_gemm_rowscale(int dtype, const void* a, const void* b, const f
   if (m <= 0 || n <= 0 || k <= 0) return tk::fail("gemm_rowscale: empty problem");
   if (stride_cm <= 0 || stride_cn <= 0) return tk::fail("gemm_rowscale: strides must be positive");
   const int64_t lim = INT32_MAX;
-  if (m > lim || n > lim || k > lim || (m - 1) * stride_cm + (n - 1) * stride_cn > lim)
+  if (m > lim || n > lim || k > lim || tk::extent(m, stride_cm, n, stride_cn) > lim)
     return tk::fail("gemm_rowscale: operand exceeds the int32 offset range");
   if (!tk::gemm_dma_applies(a, b, m, n, k, stride_am, stride_ak, stride_bk, stride_bn))
     return tk::fail("gemm_rowscale: needs unit inner strides, 16-byte aligned rows, k %% 32 == 0, "

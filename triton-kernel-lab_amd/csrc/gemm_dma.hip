@@ -460,9 +460,11 @@ namespace tk {
 bool gemm_dma_applies(const void* a, const void* b, int64_t m, int64_t n, int64_t k,
                       int64_t stride_am, int64_t stride_ak, int64_t stride_bk,
                       int64_t stride_bn) {
-  // Buffer offsets are 32-bit with kOob (2^31) reserved as "outside".
-  const int64_t a_bytes = ((m - 1) * stride_am + k) * 2;
-  const int64_t b_bytes = ((k - 1) * stride_bk + n) * 2;
+  // Buffer offsets are 32-bit with kOob (2^31) reserved as "outside"; row strides are
+  // positive (the offsets are unsigned).
+  if (m <= 0 || n <= 0 || k <= 0 || stride_am <= 0 || stride_bk <= 0) return false;
+  const __int128 a_bytes = (extent(m, stride_am, 1, 0) + k) * 2;
+  const __int128 b_bytes = (extent(k, stride_bk, 1, 0) + n) * 2;
   return stride_ak == 1 && stride_bn == 1 && k % BK == 0 && n % 8 == 0 && stride_am % 8 == 0 &&
          stride_bk % 8 == 0 && aligned16(a) && aligned16(b) && a_bytes < int64_t(kOob) &&
          b_bytes < int64_t(kOob);

@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
+
 #include "tklab_hip.h"
 
 namespace tk {
@@ -30,6 +32,28 @@ inline int elem_size(int dtype) { return dtype == TK_DTYPE_F32 ? 4 : 2; }
 
 inline bool valid_dtype(int dtype) {
   return dtype == TK_DTYPE_F32 || dtype == TK_DTYPE_F16 || dtype == TK_DTYPE_BF16;
+}
+
+// Row, batch and head strides are element counts >= 0 (0 repeats one row, as broadcast
+// tables do); no kernel here addresses rows before a tensor's base pointer.
+inline bool nonnegative(std::initializer_list<int64_t> strides) {
+  for (int64_t s : strides)
+    if (s < 0) return false;
+  return true;
+}
+
+// (d1 - 1) * s1 + (d2 - 1) * s2, the element offset of a 2-D operand's last element, in
+// 128-bit arithmetic so no stride or size makes it wrap.
+inline __int128 extent(int64_t d1, int64_t s1, int64_t d2, int64_t s2) {
+  return static_cast<__int128>(d1 - 1) * s1 + static_cast<__int128>(d2 - 1) * s2;
+}
+
+// rows * cols of a row-major problem folded into one long row, or -1 when either is not
+// positive or the product leaves int64.
+inline int64_t folded_extent(int64_t rows, int64_t cols) {
+  int64_t n;
+  if (rows <= 0 || cols <= 0 || __builtin_mul_overflow(rows, cols, &n)) return -1;
+  return n;
 }
 
 // ---------------------------------------------------------------- conversions
