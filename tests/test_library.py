@@ -184,10 +184,14 @@ def test_every_entry_point_rejects_negative_strides(name: str) -> None:
 
 
 def test_sizes_whose_product_overflows_are_rejected() -> None:
+    """rows * cols past the 64-bit range (the contiguous-row fold) or rows that end past
+    2^52 elements are refused, whichever check meets them first."""
     _cpu_only()
     huge = 1 << 40
-    for name in ("tk_swiglu_fwd", "tk_activation_fwd"):
+    for name in ("tk_swiglu_fwd", "tk_swiglu_bwd", "tk_activation_fwd", "tk_activation_bwd",
+                 "tk_softmax_fwd", "tk_rmsnorm_fwd", "tk_layernorm_fwd", "tk_vector_add"):
         values = _probe_args(name, dtype=2, pointer=1 << 20, size=huge, stride=huge, array=[1])
-        if name == "tk_activation_fwd":
+        if name.startswith("tk_activation"):
             values[1] = 0  # kind
-        assert "too large" in _rejected_before_launch(name, values)
+        message = _rejected_before_launch(name, values)
+        assert "too large" in message or "in range" in message or "columns" in message, message

@@ -131,8 +131,8 @@ extern "C" int tk_vector_add(int dtype, const void* x, const void* y, void* out,
   if (!tk::valid_dtype(dtype)) return tk::fail("vector_add: unsupported dtype code %d", dtype);
   if (x == nullptr || y == nullptr || out == nullptr) return tk::fail("vector_add: null pointer");
   if (n <= 0) return tk::fail("vector_add: empty problem");
-  if (!tk::nonnegative({x_stride, y_stride, out_stride}))
-    return tk::fail("vector_add: strides must be non-negative");
+  if (!tk::row_strides_ok(n, 1, {x_stride, y_stride, out_stride}))
+    return tk::fail("vector_add: strides must be non-negative and keep rows in range");
   hipStream_t s = tk::as_stream(stream);
   const int vec = 16 / tk::elem_size(dtype);
   const bool vok = x_stride == 1 && y_stride == 1 && out_stride == 1 && n % vec == 0 &&
@@ -155,8 +155,8 @@ extern "C" int tk_activation_fwd(int dtype, int kind, const void* x, void* y, in
   if (!tk::valid_dtype(dtype)) return tk::fail("activation_fwd: unsupported dtype code %d", dtype);
   if (x == nullptr || y == nullptr) return tk::fail("activation_fwd: null pointer");
   if (rows <= 0 || cols <= 0) return tk::fail("activation_fwd: empty problem");
-  if (!tk::nonnegative({x_row_stride, y_row_stride}))
-    return tk::fail("activation_fwd: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, cols, {x_row_stride, y_row_stride}))
+    return tk::fail("activation_fwd: strides must be non-negative and keep rows in range");
   if (x_row_stride == cols && y_row_stride == cols) {
     cols = tk::folded_extent(rows, cols);
     rows = 1;
@@ -183,8 +183,8 @@ extern "C" int tk_activation_bwd(int dtype, int kind, const void* dy, const void
   if (!tk::valid_dtype(dtype)) return tk::fail("activation_bwd: unsupported dtype code %d", dtype);
   if (dy == nullptr || x == nullptr || dx == nullptr) return tk::fail("activation_bwd: null pointer");
   if (rows <= 0 || cols <= 0) return tk::fail("activation_bwd: empty problem");
-  if (!tk::nonnegative({dy_row_stride, x_row_stride, dx_row_stride}))
-    return tk::fail("activation_bwd: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, cols, {dy_row_stride, x_row_stride, dx_row_stride}))
+    return tk::fail("activation_bwd: strides must be non-negative and keep rows in range");
   if (dy_row_stride == cols && x_row_stride == cols && dx_row_stride == cols) {
     cols = tk::folded_extent(rows, cols);
     rows = 1;

@@ -957,9 +957,9 @@ extern "C" int tk_attn_fwd_rope(int dtype, const void* q, const void* k, const v
   if (gqa_check("attn_fwd_rope", dtype, ptrs, 7, batch, heads, kv_heads, seq, head_dim, st, kv, 4))
     return 1;
   if (table_rows < seq) return tk::fail("attn_fwd_rope: the tables need a row per position");
-  if (table_row_stride < head_dim / 2 || (table_row_stride * 2) % 16 != 0 ||
-      !tk::aligned16(rope_cos) || !tk::aligned16(rope_sin))
-    return tk::fail("attn_fwd_rope: table rows must be 16-byte aligned");
+  if (table_row_stride < head_dim / 2 || table_row_stride > INT32_MAX ||
+      (table_row_stride * 2) % 16 != 0 || !tk::aligned16(rope_cos) || !tk::aligned16(rope_sin))
+    return tk::fail("attn_fwd_rope: table rows must be 16-byte aligned, strides below 2^31");
   if (k_strides[1] != seq * k_strides[2] || k_strides[0] != kv_heads * k_strides[1])
     return tk::fail("attn_fwd_rope: K must be [batch][kv_heads][seq] rows of one row stride");
   // K is rotated once into the workspace: every query block re-reads each K block, so a

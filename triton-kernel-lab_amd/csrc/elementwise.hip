@@ -308,8 +308,8 @@ extern "C" int tk_swiglu_fwd(int dtype, const void* value, const void* gate, voi
                              int64_t cols, int64_t value_row_stride, int64_t gate_row_stride,
                              int64_t y_row_stride, void* stream) {
   if (value == nullptr || gate == nullptr || y == nullptr) return tk::fail("swiglu_fwd: null pointer");
-  if (!tk::nonnegative({value_row_stride, gate_row_stride, y_row_stride}))
-    return tk::fail("swiglu_fwd: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, cols, {value_row_stride, gate_row_stride, y_row_stride}))
+    return tk::fail("swiglu_fwd: strides must be non-negative and keep rows in range");
   // A fully contiguous problem is one long row: no per-chunk division work.
   if (rows > 0 && cols > 0 && value_row_stride == cols && gate_row_stride == cols &&
       y_row_stride == cols) {
@@ -342,9 +342,10 @@ extern "C" int tk_swiglu_bwd(int dtype, const void* dy, const void* value, const
                              int64_t dgate_row_stride, void* stream) {
   if (dy == nullptr || value == nullptr || gate == nullptr || dvalue == nullptr || dgate == nullptr)
     return tk::fail("swiglu_bwd: null pointer");
-  if (!tk::nonnegative({dy_row_stride, value_row_stride, gate_row_stride, dvalue_row_stride,
-                        dgate_row_stride}))
-    return tk::fail("swiglu_bwd: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, cols,
+                          {dy_row_stride, value_row_stride, gate_row_stride, dvalue_row_stride,
+                           dgate_row_stride}))
+    return tk::fail("swiglu_bwd: strides must be non-negative and keep rows in range");
   if (rows > 0 && cols > 0 && dy_row_stride == cols && value_row_stride == cols &&
       gate_row_stride == cols && dvalue_row_stride == cols && dgate_row_stride == cols) {
     cols = tk::folded_extent(rows, cols);
@@ -378,8 +379,9 @@ extern "C" int tk_rope_fwd(int dtype, const void* x, const void* cos, const void
                            void* stream) {
   if (x == nullptr || cos == nullptr || sin == nullptr || y == nullptr)
     return tk::fail("rope_fwd: null pointer");
-  if (!tk::nonnegative({x_row_stride, cos_row_stride, sin_row_stride, y_row_stride}))
-    return tk::fail("rope_fwd: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, 2 * half_dim,
+                          {x_row_stride, cos_row_stride, sin_row_stride, y_row_stride}))
+    return tk::fail("rope_fwd: strides must be non-negative and keep rows in range");
   // The second half starts half_dim elements in, so half_dim joins the strides.
   const bool vok = tk::valid_dtype(dtype) &&
                    vector_ok(dtype, half_dim, {x, cos, sin, y},
@@ -417,9 +419,11 @@ extern "C" int tk_rope_bwd(int dtype, const void* dy, const void* x, const void*
     return tk::fail("rope_bwd: null pointer");
   const bool need_x = dcos != nullptr || dsin != nullptr;
   if (need_x && x == nullptr) return tk::fail("rope_bwd: x is required for dcos/dsin");
-  if (!tk::nonnegative({dy_row_stride, need_x ? x_row_stride : 0, cos_row_stride, sin_row_stride,
-                        dx_row_stride, dcos ? dcos_row_stride : 0, dsin ? dsin_row_stride : 0}))
-    return tk::fail("rope_bwd: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, 2 * half_dim,
+                          {dy_row_stride, need_x ? x_row_stride : 0, cos_row_stride,
+                           sin_row_stride, dx_row_stride, dcos ? dcos_row_stride : 0,
+                           dsin ? dsin_row_stride : 0}))
+    return tk::fail("rope_bwd: strides must be non-negative and keep rows in range");
   const bool vok =
       tk::valid_dtype(dtype) &&
       vector_ok(dtype, half_dim, {dy, need_x ? x : nullptr, cos, sin, dx, dcos, dsin},
@@ -457,8 +461,8 @@ extern "C" int tk_scale_rows(int dtype, const void* x, const void* scale, void* 
                              int64_t cols, int64_t x_row_stride, int64_t y_row_stride,
                              void* stream) {
   if (x == nullptr || scale == nullptr || y == nullptr) return tk::fail("scale_rows: null pointer");
-  if (!tk::nonnegative({x_row_stride, y_row_stride}))
-    return tk::fail("scale_rows: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, cols, {x_row_stride, y_row_stride}))
+    return tk::fail("scale_rows: strides must be non-negative and keep rows in range");
   const bool vok = tk::valid_dtype(dtype) &&
                    vector_ok(dtype, cols, {x, y}, {x_row_stride, y_row_stride});
   const int vec = vok ? 16 / tk::elem_size(dtype) : 1;
@@ -484,8 +488,8 @@ extern "C" int tk_rope_positions(int dtype, const void* x, const void* cos, cons
                                  int64_t y_row_stride, int inverse, void* stream) {
   if (x == nullptr || cos == nullptr || sin == nullptr || y == nullptr)
     return tk::fail("rope_positions: null pointer");
-  if (!tk::nonnegative({x_row_stride, table_row_stride, y_row_stride}))
-    return tk::fail("rope_positions: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, 2 * half_dim, {x_row_stride, table_row_stride, y_row_stride}))
+    return tk::fail("rope_positions: strides must be non-negative and keep rows in range");
   if (seq <= 0 || seq > rows || rows % seq != 0)
     return tk::fail("rope_positions: rows must be a positive multiple of seq");
   const bool vok = tk::valid_dtype(dtype) &&

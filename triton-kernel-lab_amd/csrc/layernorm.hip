@@ -210,8 +210,8 @@ extern "C" int tk_layernorm_fwd(int dtype, const void* x, const void* weight, co
                                 void* stream) {
   if (x == nullptr || weight == nullptr || bias == nullptr || y == nullptr)
     return tk::fail("layernorm_fwd: null pointer");
-  if (!tk::nonnegative({x_row_stride, y_row_stride}))
-    return tk::fail("layernorm_fwd: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, cols, {x_row_stride, y_row_stride}))
+    return tk::fail("layernorm_fwd: strides must be non-negative and keep rows in range");
   if (!(eps > 0.f)) return tk::fail("layernorm_fwd: eps must be finite and positive");
   const bool vok = tk::valid_dtype(dtype) &&
                    rows_vector_ok(dtype, cols, {x, weight, bias, y}, {x_row_stride, y_row_stride});
@@ -238,8 +238,8 @@ extern "C" int tk_layernorm_bwd_stage1(int dtype, void* dx, const void* dy, floa
                                        int64_t group_size, void* stream) {
   if (!dx || !dy || !partial_dw || !partial_db || !x || !weight || !mean || !rstd || !locks)
     return tk::fail("layernorm_bwd_stage1: null pointer");
-  if (!tk::nonnegative({x_row_stride, dy_row_stride, dx_row_stride}))
-    return tk::fail("layernorm_bwd_stage1: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, cols, {x_row_stride, dy_row_stride, dx_row_stride}))
+    return tk::fail("layernorm_bwd_stage1: strides must be non-negative and keep rows in range");
   if (group_size <= 0 || group_size > INT32_MAX)
     return tk::fail("layernorm_bwd_stage1: group_size must be positive");
   const bool vok = tk::valid_dtype(dtype) &&
@@ -265,7 +265,8 @@ extern "C" int tk_layernorm_bwd_stage2(int dtype, const float* partial_dw, const
                                        void* stream) {
   if (!tk::valid_dtype(dtype)) return tk::fail("layernorm_bwd_stage2: unsupported dtype code %d", dtype);
   if (!partial_dw || !partial_db || !dw || !db) return tk::fail("layernorm_bwd_stage2: null pointer");
-  if (group_count <= 0 || cols <= 0 || group_count * cols > INT32_MAX)
+  if (group_count <= 0 || cols <= 0 || group_count > INT32_MAX || cols > INT32_MAX ||
+      group_count * cols > INT32_MAX)
     return tk::fail("layernorm_bwd_stage2: bad partial shape");
   hipStream_t s = tk::as_stream(stream);
   TK_DISPATCH_DTYPE(dtype, T,

@@ -336,9 +336,10 @@ extern "C" int tk_rmsnorm_fwd(int dtype, const void* x, const void* residual, co
                               void* stream) {
   if (x == nullptr || (y != nullptr && weight == nullptr) || (y == nullptr && rstd == nullptr))
     return tk::fail("rmsnorm_fwd: null pointer");
-  if (!tk::nonnegative({x_row_stride, residual ? residual_row_stride : 0,
-                        residual_sum ? residual_sum_row_stride : 0, y ? y_row_stride : 0}))
-    return tk::fail("rmsnorm_fwd: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, cols,
+                          {x_row_stride, residual ? residual_row_stride : 0,
+                           residual_sum ? residual_sum_row_stride : 0, y ? y_row_stride : 0}))
+    return tk::fail("rmsnorm_fwd: strides must be non-negative and keep rows in range");
   if (!(eps > 0.f)) return tk::fail("rmsnorm_fwd: eps must be finite and positive");
   const bool vector_ok = tk::valid_dtype(dtype) && rows_vector_ok(
       dtype, cols, {x, residual, weight, residual_sum, y},
@@ -374,9 +375,10 @@ extern "C" int tk_rmsnorm_bwd_stage1(int dtype, void* dx, const void* dy, const 
   if (dx == nullptr || dy == nullptr || partial_dw == nullptr || x == nullptr ||
       weight == nullptr || rstd == nullptr || locks == nullptr)
     return tk::fail("rmsnorm_bwd_stage1: null pointer");
-  if (!tk::nonnegative({x_row_stride, dy_row_stride, incoming_dx ? incoming_dx_row_stride : 0,
-                        dx_row_stride}))
-    return tk::fail("rmsnorm_bwd_stage1: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, cols,
+                          {x_row_stride, dy_row_stride,
+                           incoming_dx ? incoming_dx_row_stride : 0, dx_row_stride}))
+    return tk::fail("rmsnorm_bwd_stage1: strides must be non-negative and keep rows in range");
   if (group_size <= 0 || group_size > INT32_MAX)
     return tk::fail("rmsnorm_bwd_stage1: group_size must be positive");
   const int64_t group_count = group_size < rows ? group_size : rows;
@@ -474,9 +476,10 @@ extern "C" int tk_rmsnorm_bwd_noalloc(int dtype, void* dx, void* dw, const void*
   if (dx == nullptr || dw == nullptr || dy == nullptr || x == nullptr || weight == nullptr ||
       rstd == nullptr)
     return tk::fail("rmsnorm_bwd_noalloc: null pointer");
-  if (!tk::nonnegative({x_row_stride, dy_row_stride, incoming_dx ? incoming_dx_row_stride : 0,
-                        dx_row_stride}))
-    return tk::fail("rmsnorm_bwd_noalloc: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, cols,
+                          {x_row_stride, dy_row_stride,
+                           incoming_dx ? incoming_dx_row_stride : 0, dx_row_stride}))
+    return tk::fail("rmsnorm_bwd_noalloc: strides must be non-negative and keep rows in range");
   if (group_size <= 0 || group_size > INT32_MAX)
     return tk::fail("rmsnorm_bwd_noalloc: group_size must be positive");
   if (rows <= 0 || cols <= 0) return tk::fail("rmsnorm_bwd_noalloc: empty problem");

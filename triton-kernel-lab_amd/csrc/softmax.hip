@@ -356,8 +356,8 @@ extern "C" int tk_softmax_online_fwd(int dtype, const void* x, void* y, float* p
   if ((reinterpret_cast<uintptr_t>(partials) & 7) != 0)
     return tk::fail("online softmax: workspace must be 8-byte aligned");
   if (rows <= 0 || cols <= 0) return tk::fail("online softmax: empty problem");
-  if (!tk::nonnegative({x_row_stride, y_row_stride}))
-    return tk::fail("online softmax: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, cols, {x_row_stride, y_row_stride}))
+    return tk::fail("online softmax: strides must be non-negative and keep rows in range");
   if (cols > INT32_MAX) return tk::fail("online softmax: more than 2^31-1 columns");
   const int64_t chunks = tk::cdiv(cols, kOnlineChunk);
   if (rows * chunks > INT32_MAX) return tk::fail("online softmax: too many chunks");
@@ -402,8 +402,8 @@ extern "C" int tk_softmax_fwd(int dtype, const void* x, void* y, int64_t rows, i
   if (!tk::valid_dtype(dtype)) return tk::fail("softmax: unsupported dtype code %d", dtype);
   if (x == nullptr || y == nullptr) return tk::fail("softmax: null pointer");
   if (rows <= 0 || cols <= 0) return tk::fail("softmax: empty problem");
-  if (!tk::nonnegative({x_row_stride, y_row_stride}))
-    return tk::fail("softmax: strides must be non-negative");
+  if (!tk::row_strides_ok(rows, cols, {x_row_stride, y_row_stride}))
+    return tk::fail("softmax: strides must be non-negative and keep rows in range");
   if (rows > INT32_MAX) return tk::fail("softmax: too many rows");
   tk::RowShape shape;
   if (cols > 65536 || !tk::pick_row_shape(cols, &shape))

@@ -34,18 +34,20 @@ inline bool valid_dtype(int dtype) {
   return dtype == TK_DTYPE_F32 || dtype == TK_DTYPE_F16 || dtype == TK_DTYPE_BF16;
 }
 
-// Row, batch and head strides are element counts >= 0 (0 repeats one row, as broadcast
-// tables do); no kernel here addresses rows before a tensor's base pointer.
-inline bool nonnegative(std::initializer_list<int64_t> strides) {
-  for (int64_t s : strides)
-    if (s < 0) return false;
-  return true;
-}
-
 // (d1 - 1) * s1 + (d2 - 1) * s2, the element offset of a 2-D operand's last element, in
 // 128-bit arithmetic so no stride or size makes it wrap.
 inline __int128 extent(int64_t d1, int64_t s1, int64_t d2, int64_t s2) {
   return static_cast<__int128>(d1 - 1) * s1 + static_cast<__int128>(d2 - 1) * s2;
+}
+
+// Row strides are element counts >= 0 (0 repeats one row, as broadcast tables do; no
+// kernel here addresses rows before a tensor's base pointer), and the last row of a
+// `rows` x `cols` operand ends below 2^52 elements past its base, so no row offset the
+// kernels form in 64-bit arithmetic can wrap. Sizes are checked separately.
+inline bool row_strides_ok(int64_t rows, int64_t cols, std::initializer_list<int64_t> strides) {
+  for (int64_t s : strides)
+    if (s < 0 || extent(rows, s, cols, 1) >= (static_cast<__int128>(1) << 52)) return false;
+  return true;
 }
 
 // rows * cols of a row-major problem folded into one long row, or -1 when either is not
