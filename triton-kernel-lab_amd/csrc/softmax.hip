@@ -37,22 +37,21 @@ __device__ __forceinline__ void softmax_row(float* v, float* scratch) {
 // 4096 x 4096 (one wave per row, all waves resident in one round) one row per wave ran
 // 26.8-27.2 us with libm's expf and 25.6 us with hw_exp; two rows per wave with hw_exp
 // 23.2-23.6 us; three or four rows per wave through two register buffers 27-29 us (too
-// few waves per SIMD).
+// few waves per SIMD). One row group per workgroup (a single wave for rows of up to 4096
+// columns): 23.5-23.7 us against 23.9-24.0 us with four single-wave groups per workgroup.
 template <typename T, int VEC, int RT, int VALS, int P>
-__global__ __launch_bounds__(RT >= 256 ? RT : 256) void softmax_fwd_kernel(
+__global__ __launch_bounds__(RT) void softmax_fwd_kernel(
     const T* __restrict__ x, T* __restrict__ y, int rows, int cols, int64_t x_stride,
     int64_t y_stride) {
   static_assert(P == 1 || RT == 64, "several rows per group only for single-wave rows");
-  constexpr int SLOTS = RT >= 256 ? 1 : 256 / RT;
   __shared__ float scratch[RT / 64];
   const int lane = threadIdx.x % RT;
   // Rows of 16-byte vectors are streamed once: non-temporal buffer loads and stores
   // (f32 4096 x 4096 went from 4.9 to 5.9 TB/s). The row index is wave-uniform and
   // readfirstlane lets the compiler keep each row's buffer resource scalar.
   constexpr bool kBuf = VEC * sizeof(T) == 16;
-  const int row0 = __builtin_amdgcn_readfirstlane((blockIdx.x * SLOTS + threadIdx.x / RT) * P);
-  // SLOTS > 1 only for single-wave rows, which never reach a block barrier.
-  if (row0 >= rows) return;
+  const int row0 = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * P);
+  if (row0 >= rows) return;  // the whole workgroup: row0 is uniform
 
   float v[P][VALS];
 #pragma unroll
@@ -413,11 +412,10 @@ extern "C" int tk_softmax_fwd(int dtype, const void* x, void* y, int64_t rows, i
   const int vec = 16 / es;
   const bool vector_ok = tk::aligned16(x) && tk::aligned16(y) && cols % vec == 0 &&
                          (x_row_stride * es) % 16 == 0 && (y_row_stride * es) % 16 == 0;
-  const int slots = shape.rt >= 256 ? 1 : 256 / shape.rt;
   // Two single-wave rows per wave once that still leaves two waves per SIMD (4096 rows).
   const bool pair = shape.rt == 64 && rows >= 4096;
-  const dim3 grid(static_cast<unsigned>(tk::cdiv(rows, slots * (pair ? 2 : 1))));
-  const dim3 block(shape.rt >= 256 ? shape.rt : 256);
+  const dim3 grid(static_cast<unsigned>(tk::cdiv(rows, pair ? 2 : 1)));
+  const dim3 block(shape.rt);
   hipStream_t s = tk::as_stream(stream);
   TK_DISPATCH_DTYPE(dtype, T,
     TK_DISPATCH_VEC(T, vector_ok,
