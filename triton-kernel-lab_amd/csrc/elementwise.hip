@@ -19,6 +19,10 @@
 namespace {
 
 constexpr int kBlock = 256;
+// The RoPE kernels run one wave per workgroup: bf16 [4,32,4096,128] forward 67.3-67.5 ->
+// 65.8-65.9 us and backward 66.9-67.3 -> 65.4-65.5 us against four waves; the SwiGLU
+// backward ran 3 % slower that way (382-384 -> 394-395 us), so SwiGLU keeps four.
+constexpr int kRopeBlock = 64;
 
 using tk::stable_sigmoid;
 
@@ -32,8 +36,8 @@ struct Grid1D {
   unsigned blocks;
 };
 
-inline Grid1D chunk_grid(int64_t chunks) {
-  int64_t blocks = tk::cdiv(chunks, kBlock * kUnroll);
+inline Grid1D chunk_grid(int64_t chunks, int block = kBlock) {
+  int64_t blocks = tk::cdiv(chunks, int64_t(block) * kUnroll);
   if (blocks > kMaxBlocks) blocks = kMaxBlocks;
   return {static_cast<unsigned>(blocks)};
 }
@@ -146,18 +150,18 @@ __device__ __forceinline__ void load_table(const T* p, float* f) {
 }
 
 template <typename T, int VEC, bool kPositions = false, bool kStreamTables = false>
-__global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
+__global__ __launch_bounds__(kRopeBlock) void rope_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ cosv, const T* __restrict__ sinv,
     T* __restrict__ y, uint32_t chunks, tk::FastDiv per_row, int half, int64_t xs, int64_t cs,
     int64_t ss, int64_t ys, tk::FastDiv positions = tk::FastDiv()) {
-  // A workgroup pass covers kUnroll * kBlock consecutive chunks (one 4 KiB run per
+  // A workgroup pass covers kUnroll * kRopeBlock consecutive chunks (one 4 KiB run per
   // wave and tensor), then the grid strides on.
-  const uint32_t stride = gridDim.x * kBlock * kUnroll;
-  for (uint32_t i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
+  const uint32_t stride = gridDim.x * kRopeBlock * kUnroll;
+  for (uint32_t i0 = blockIdx.x * kRopeBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
     float x1[kUnroll][VEC], x2[kUnroll][VEC], co[kUnroll][VEC], si[kUnroll][VEC];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kRopeBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       const T* xr = x + p.row * xs;
@@ -169,7 +173,7 @@ __global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kRopeBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       float y1[VEC], y2[VEC];
@@ -188,20 +192,20 @@ __global__ __launch_bounds__(kBlock) void rope_fwd_kernel(
 // dx1 = dy1*cos + dy2*sin; dx2 = dy2*cos - dy1*sin;
 // dcos = dy1*x1 + dy2*x2; dsin = -dy1*x2 + dy2*x1  (src/tklab/kernels/rope.py:102-160)
 template <typename T, int VEC, bool kPositions = false, bool kStreamTables = false>
-__global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
+__global__ __launch_bounds__(kRopeBlock) void rope_bwd_kernel(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ cosv,
     const T* __restrict__ sinv, T* __restrict__ dx, T* __restrict__ dcos, T* __restrict__ dsin,
     uint32_t chunks, tk::FastDiv per_row, int half, int64_t dys, int64_t xs, int64_t cs, int64_t ss,
     int64_t dxs, int64_t dcs, int64_t dss, tk::FastDiv positions = tk::FastDiv()) {
   const bool need_x = dcos != nullptr || dsin != nullptr;
-  // A workgroup pass covers kUnroll * kBlock consecutive chunks (one 4 KiB run per
+  // A workgroup pass covers kUnroll * kRopeBlock consecutive chunks (one 4 KiB run per
   // wave and tensor), then the grid strides on.
-  const uint32_t stride = gridDim.x * kBlock * kUnroll;
-  for (uint32_t i0 = blockIdx.x * kBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
+  const uint32_t stride = gridDim.x * kRopeBlock * kUnroll;
+  for (uint32_t i0 = blockIdx.x * kRopeBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
     float d1[kUnroll][VEC], d2[kUnroll][VEC], co[kUnroll][VEC], si[kUnroll][VEC];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kRopeBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       const T* dyr = dy + p.row * dys;
@@ -213,7 +217,7 @@ __global__ __launch_bounds__(kBlock) void rope_bwd_kernel(
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t i = i0 + u * kBlock;
+      const uint32_t i = i0 + u * kRopeBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
       float o1[VEC], o2[VEC];
@@ -390,19 +394,19 @@ extern "C" int tk_rope_fwd(int dtype, const void* x, const void* cos, const void
   int64_t per_row, chunks;
   if (check_problem("rope_fwd", dtype, rows, half_dim, vec, &per_row, &chunks)) return 1;
   const tk::FastDiv div(static_cast<uint32_t>(per_row));
-  const Grid1D g = chunk_grid(chunks);
+  const Grid1D g = chunk_grid(chunks, kRopeBlock);
   hipStream_t s = tk::as_stream(stream);
   const bool stream_tables = cos_row_stride != 0 && sin_row_stride != 0;
   TK_DISPATCH_DTYPE(dtype, T,
     TK_DISPATCH_VEC(T, vok,
       if (stream_tables)
-        hipLaunchKernelGGL((rope_fwd_kernel<T, VEC, false, true>), dim3(g.blocks), dim3(kBlock),
+        hipLaunchKernelGGL((rope_fwd_kernel<T, VEC, false, true>), dim3(g.blocks), dim3(kRopeBlock),
                            0, s, static_cast<const T*>(x), static_cast<const T*>(cos),
                            static_cast<const T*>(sin), static_cast<T*>(y), (int)chunks, div,
                            (int)half_dim, x_row_stride, cos_row_stride, sin_row_stride,
                            y_row_stride);
       else
-        hipLaunchKernelGGL((rope_fwd_kernel<T, VEC>), dim3(g.blocks), dim3(kBlock), 0, s,
+        hipLaunchKernelGGL((rope_fwd_kernel<T, VEC>), dim3(g.blocks), dim3(kRopeBlock), 0, s,
                            static_cast<const T*>(x), static_cast<const T*>(cos),
                            static_cast<const T*>(sin), static_cast<T*>(y), (int)chunks, div,
                            (int)half_dim, x_row_stride, cos_row_stride, sin_row_stride,
@@ -433,13 +437,13 @@ extern "C" int tk_rope_bwd(int dtype, const void* dy, const void* x, const void*
   int64_t per_row, chunks;
   if (check_problem("rope_bwd", dtype, rows, half_dim, vec, &per_row, &chunks)) return 1;
   const tk::FastDiv div(static_cast<uint32_t>(per_row));
-  const Grid1D g = chunk_grid(chunks);
+  const Grid1D g = chunk_grid(chunks, kRopeBlock);
   hipStream_t s = tk::as_stream(stream);
   const bool stream_tables = cos_row_stride != 0 && sin_row_stride != 0;
   TK_DISPATCH_DTYPE(dtype, T,
     TK_DISPATCH_VEC(T, vok,
       if (stream_tables)
-        hipLaunchKernelGGL((rope_bwd_kernel<T, VEC, false, true>), dim3(g.blocks), dim3(kBlock),
+        hipLaunchKernelGGL((rope_bwd_kernel<T, VEC, false, true>), dim3(g.blocks), dim3(kRopeBlock),
                            0, s, static_cast<const T*>(dy), static_cast<const T*>(x),
                            static_cast<const T*>(cos), static_cast<const T*>(sin),
                            static_cast<T*>(dx), static_cast<T*>(dcos), static_cast<T*>(dsin),
@@ -447,7 +451,7 @@ extern "C" int tk_rope_bwd(int dtype, const void* dy, const void* x, const void*
                            cos_row_stride, sin_row_stride, dx_row_stride, dcos_row_stride,
                            dsin_row_stride);
       else
-        hipLaunchKernelGGL((rope_bwd_kernel<T, VEC>), dim3(g.blocks), dim3(kBlock), 0, s,
+        hipLaunchKernelGGL((rope_bwd_kernel<T, VEC>), dim3(g.blocks), dim3(kRopeBlock), 0, s,
                            static_cast<const T*>(dy), static_cast<const T*>(x),
                            static_cast<const T*>(cos), static_cast<const T*>(sin),
                            static_cast<T*>(dx), static_cast<T*>(dcos), static_cast<T*>(dsin),
@@ -500,12 +504,12 @@ extern "C" int tk_rope_positions(int dtype, const void* x, const void* cos, cons
   if (check_problem("rope_positions", dtype, rows, half_dim, vec, &per_row, &chunks)) return 1;
   const tk::FastDiv div(static_cast<uint32_t>(per_row));
   const tk::FastDiv positions(static_cast<uint32_t>(seq));
-  const Grid1D g = chunk_grid(chunks);
+  const Grid1D g = chunk_grid(chunks, kRopeBlock);
   hipStream_t s = tk::as_stream(stream);
   if (inverse) {
     TK_DISPATCH_DTYPE(dtype, T,
       TK_DISPATCH_VEC(T, vok,
-        hipLaunchKernelGGL((rope_bwd_kernel<T, VEC, true>), dim3(g.blocks), dim3(kBlock), 0, s,
+        hipLaunchKernelGGL((rope_bwd_kernel<T, VEC, true>), dim3(g.blocks), dim3(kRopeBlock), 0, s,
                            static_cast<const T*>(x), static_cast<const T*>(nullptr),
                            static_cast<const T*>(cos), static_cast<const T*>(sin),
                            static_cast<T*>(y), static_cast<T*>(nullptr),
@@ -515,7 +519,7 @@ extern "C" int tk_rope_positions(int dtype, const void* x, const void* cos, cons
   } else {
     TK_DISPATCH_DTYPE(dtype, T,
       TK_DISPATCH_VEC(T, vok,
-        hipLaunchKernelGGL((rope_fwd_kernel<T, VEC, true>), dim3(g.blocks), dim3(kBlock), 0, s,
+        hipLaunchKernelGGL((rope_fwd_kernel<T, VEC, true>), dim3(g.blocks), dim3(kRopeBlock), 0, s,
                            static_cast<const T*>(x), static_cast<const T*>(cos),
                            static_cast<const T*>(sin), static_cast<T*>(y), (int)chunks, div,
                            (int)half_dim, x_row_stride, table_row_stride, table_row_stride,
