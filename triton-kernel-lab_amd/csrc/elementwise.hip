@@ -27,6 +27,10 @@ constexpr int kRopeBlock = 64;
 using tk::stable_sigmoid;
 
 constexpr int kUnroll = 4;
+// RoPE: two chunks per thread and pass (one-wave workgroups): forward 66.2-66.5 -> 65.8-66.0
+// us, backward 65.5-65.9 -> 65.1-65.3 us; SwiGLU runs best at four (two: 222 -> 226 us
+// forward, eight: 239 us).
+constexpr int kRopeUnroll = 2;
 // One workgroup per pass of kUnroll * kBlock chunks up to 2^18 passes (beyond that the loop
 // strides): on SwiGLU bf16 16384 x 14336 a grid of 8192 workgroups walking the passes
 // grid-stride ran 231 / 395 us (forward / backward), one workgroup per pass 218 / 379 us.
@@ -36,8 +40,8 @@ struct Grid1D {
   unsigned blocks;
 };
 
-inline Grid1D chunk_grid(int64_t chunks, int block = kBlock) {
-  int64_t blocks = tk::cdiv(chunks, int64_t(block) * kUnroll);
+inline Grid1D chunk_grid(int64_t chunks, int block = kBlock, int unroll = kUnroll) {
+  int64_t blocks = tk::cdiv(chunks, int64_t(block) * unroll);
   if (blocks > kMaxBlocks) blocks = kMaxBlocks;
   return {static_cast<unsigned>(blocks)};
 }
@@ -154,13 +158,15 @@ __global__ __launch_bounds__(kRopeBlock) void rope_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ cosv, const T* __restrict__ sinv,
     T* __restrict__ y, uint32_t chunks, tk::FastDiv per_row, int half, int64_t xs, int64_t cs,
     int64_t ss, int64_t ys, tk::FastDiv positions = tk::FastDiv()) {
-  // A workgroup pass covers kUnroll * kRopeBlock consecutive chunks (one 4 KiB run per
-  // wave and tensor), then the grid strides on.
-  const uint32_t stride = gridDim.x * kRopeBlock * kUnroll;
-  for (uint32_t i0 = blockIdx.x * kRopeBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
-    float x1[kUnroll][VEC], x2[kUnroll][VEC], co[kUnroll][VEC], si[kUnroll][VEC];
+  // A workgroup (one wave) pass covers kRopeUnroll * kRopeBlock consecutive chunks (a 2 KiB
+  // run per tensor), then the grid strides on.
+  constexpr uint32_t kPass = kRopeBlock * kRopeUnroll;
+  const uint32_t stride = gridDim.x * kPass;
+  for (uint32_t i0 = blockIdx.x * kPass + threadIdx.x; i0 < chunks; i0 += stride) {
+    float x1[kRopeUnroll][VEC], x2[kRopeUnroll][VEC];
+    float co[kRopeUnroll][VEC], si[kRopeUnroll][VEC];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < kRopeUnroll; ++u) {
       const uint32_t i = i0 + u * kRopeBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
@@ -172,7 +178,7 @@ __global__ __launch_bounds__(kRopeBlock) void rope_fwd_kernel(
       load_table<T, VEC, kStreamTables>(sinv + tr * ss + p.col, si[u]);
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < kRopeUnroll; ++u) {
       const uint32_t i = i0 + u * kRopeBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
@@ -198,13 +204,15 @@ __global__ __launch_bounds__(kRopeBlock) void rope_bwd_kernel(
     uint32_t chunks, tk::FastDiv per_row, int half, int64_t dys, int64_t xs, int64_t cs, int64_t ss,
     int64_t dxs, int64_t dcs, int64_t dss, tk::FastDiv positions = tk::FastDiv()) {
   const bool need_x = dcos != nullptr || dsin != nullptr;
-  // A workgroup pass covers kUnroll * kRopeBlock consecutive chunks (one 4 KiB run per
-  // wave and tensor), then the grid strides on.
-  const uint32_t stride = gridDim.x * kRopeBlock * kUnroll;
-  for (uint32_t i0 = blockIdx.x * kRopeBlock * kUnroll + threadIdx.x; i0 < chunks; i0 += stride) {
-    float d1[kUnroll][VEC], d2[kUnroll][VEC], co[kUnroll][VEC], si[kUnroll][VEC];
+  // A workgroup (one wave) pass covers kRopeUnroll * kRopeBlock consecutive chunks (a 2 KiB
+  // run per tensor), then the grid strides on.
+  constexpr uint32_t kPass = kRopeBlock * kRopeUnroll;
+  const uint32_t stride = gridDim.x * kPass;
+  for (uint32_t i0 = blockIdx.x * kPass + threadIdx.x; i0 < chunks; i0 += stride) {
+    float d1[kRopeUnroll][VEC], d2[kRopeUnroll][VEC];
+    float co[kRopeUnroll][VEC], si[kRopeUnroll][VEC];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < kRopeUnroll; ++u) {
       const uint32_t i = i0 + u * kRopeBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
@@ -216,7 +224,7 @@ __global__ __launch_bounds__(kRopeBlock) void rope_bwd_kernel(
       load_table<T, VEC, kStreamTables>(sinv + tr * ss + p.col, si[u]);
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < kRopeUnroll; ++u) {
       const uint32_t i = i0 + u * kRopeBlock;
       if (i >= chunks) break;
       const ChunkPos p = chunk_pos<VEC>(i, per_row);
@@ -394,7 +402,7 @@ extern "C" int tk_rope_fwd(int dtype, const void* x, const void* cos, const void
   int64_t per_row, chunks;
   if (check_problem("rope_fwd", dtype, rows, half_dim, vec, &per_row, &chunks)) return 1;
   const tk::FastDiv div(static_cast<uint32_t>(per_row));
-  const Grid1D g = chunk_grid(chunks, kRopeBlock);
+  const Grid1D g = chunk_grid(chunks, kRopeBlock, kRopeUnroll);
   hipStream_t s = tk::as_stream(stream);
   const bool stream_tables = cos_row_stride != 0 && sin_row_stride != 0;
   TK_DISPATCH_DTYPE(dtype, T,
@@ -437,7 +445,7 @@ extern "C" int tk_rope_bwd(int dtype, const void* dy, const void* x, const void*
   int64_t per_row, chunks;
   if (check_problem("rope_bwd", dtype, rows, half_dim, vec, &per_row, &chunks)) return 1;
   const tk::FastDiv div(static_cast<uint32_t>(per_row));
-  const Grid1D g = chunk_grid(chunks, kRopeBlock);
+  const Grid1D g = chunk_grid(chunks, kRopeBlock, kRopeUnroll);
   hipStream_t s = tk::as_stream(stream);
   const bool stream_tables = cos_row_stride != 0 && sin_row_stride != 0;
   TK_DISPATCH_DTYPE(dtype, T,
@@ -504,7 +512,7 @@ extern "C" int tk_rope_positions(int dtype, const void* x, const void* cos, cons
   if (check_problem("rope_positions", dtype, rows, half_dim, vec, &per_row, &chunks)) return 1;
   const tk::FastDiv div(static_cast<uint32_t>(per_row));
   const tk::FastDiv positions(static_cast<uint32_t>(seq));
-  const Grid1D g = chunk_grid(chunks, kRopeBlock);
+  const Grid1D g = chunk_grid(chunks, kRopeBlock, kRopeUnroll);
   hipStream_t s = tk::as_stream(stream);
   if (inverse) {
     TK_DISPATCH_DTYPE(dtype, T,
