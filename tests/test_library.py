@@ -9,6 +9,8 @@ import ctypes
 import re
 from pathlib import Path
 
+import pytest
+
 from tklab import _hip
 
 ROOT = Path(__file__).resolve().parents[1]
@@ -72,8 +74,6 @@ def test_elementwise_limit_is_the_int32_extent() -> None:
 def test_gqa_decode_rejects_row_strides_past_its_32_bit_tile_offsets() -> None:
     """The decode kernel addresses a 32-key tile (or the G query heads) through 32-bit buffer
     offsets, so key and head strides of 2^24 elements or more are rejected before any launch."""
-    import pytest
-
     p = 1 << 20  # 16-byte aligned; never dereferenced
     ok = _hip.int64_array([32 * 128, 128])
     kv = _hip.int64_array([8 * 1024 * 128, 1024 * 128, 128])
@@ -85,8 +85,6 @@ def test_gqa_decode_rejects_row_strides_past_its_32_bit_tile_offsets() -> None:
 
 def test_online_softmax_rejects_a_misaligned_workspace() -> None:
     """The single-read kernel publishes each chunk's partial as one 64-bit word."""
-    import pytest
-
     p = 1 << 20  # 16-byte aligned; never dereferenced
     with pytest.raises(_hip.HipLibraryError, match="8-byte aligned"):
         _hip.call("tk_softmax_online_fwd", 0, p, p, p + 4, 2, 100000, 100000, 100000, None)
@@ -121,8 +119,6 @@ _NO_STRIDES = {"tk_rmsnorm_bwd_stage2", "tk_layernorm_bwd_stage2"}
 
 
 def _rejected_before_launch(name: str, values) -> str:
-    import pytest
-
     with pytest.raises(_hip.HipLibraryError) as info:
         _hip.call(name, *values)
     message = str(info.value)
@@ -133,14 +129,11 @@ def _rejected_before_launch(name: str, values) -> str:
 def _cpu_only() -> None:
     """These probes pass pointers that are never valid device memory: run them only where
     no GPU could receive a launch."""
-    import pytest
     import torch
 
     if torch.cuda.is_available():
         pytest.skip("argument probes run without a GPU")
 
-
-import pytest  # noqa: E402
 
 
 @pytest.mark.parametrize("name", _COMPUTE)
