@@ -10,7 +10,8 @@
 // FLOP/s (MFMA-only with random operands 1.90 vs 1.78 PFLOP/s bf16; this GEMM 1.39 vs
 // 1.29 PFLOP/s at 8192^3 with the same tiles and LDS traffic). The MFMAs compute C^T
 // tiles (the B fragment as the first operand), so a lane's four accumulator registers
-// are four consecutive columns of one row and leave as one 8-byte store.
+// are four consecutive columns of one row (8 bytes once rounded). The epilogue stages the
+// rounded tile in the idle rings and writes whole rows from there.
 //
 // Operands reach LDS by buffer->LDS DMA (buffer_load_dwordx4 ... lds): no VGPR staging.
 // A and B have rings of their own: A in 64-wide K tiles (three stages of 256 rows x 128 B),
@@ -81,6 +82,10 @@ constexpr int kOperandBytes = 256 * BK * 2;  // 16 KiB per B stage
 constexpr int kBRing = kAStages * kABytes;   // B ring offset
 constexpr int kLdsBytes = kBRing + kBStages * kOperandBytes;
 constexpr uint32_t kOob = 0x80000000u;  // past every buffer's num_records: reads as zero
+// Epilogue: the C tile is staged in the ring's LDS (at most 256 rows of 528 bytes), the row
+// scales of the row-scaled variant after it.
+constexpr int kScaleOff = 256 * 528;
+static_assert(kScaleOff + 256 * 4 <= kLdsBytes, "row scales past the LDS block");
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -397,59 +402,94 @@ gemm_dma_kernel(const T* __restrict__ A, const T* __restrict__ B, const T* __res
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
   // acc[i][j] holds C^T: register r of lane l is C[m][n] with m = m0 + wm + 16 i + l % 16 and
-  // n = n0 + (N tile j's first column) + 4 (l / 16) + r, so a lane stores 4 consecutive
-  // columns of one row: one 8-byte store when C rows are contiguous and 8-byte aligned.
+  // n = n0 + (N tile j's first column) + 4 (l / 16) + r: four consecutive columns of one row.
+  // The rings are idle once every wave is here, so when C rows are 16-byte aligned the block
+  // stages its rounded tile in LDS and writes it back as whole rows, 16 bytes per lane, with
+  // non-temporal stores of full 128-byte lines; otherwise each lane stores its four columns.
+  // Staged, the epilogue of fp16 4096^3 took ~4 instead of ~8 us of a ~108 us launch (a
+  // timing-only copy without stores ran 102 us): 4096^3 108.1 -> 104.3 us, 8192^3 784 ->
+  // 773 us, the row-scaled 16384x6144x4096 GEMM 675 -> 645 us. Staged with default-policy
+  // stores: 105.1, 773 and 654 us. Per-lane non-temporal stores write 32-byte segments of
+  // four lines and were 5-14 % slower than default-policy ones.
+  __syncthreads();
+  const float* scales = reinterpret_cast<const float*>(lds + kScaleOff);
+  if constexpr (kRowScale) {
+    if (threadIdx.x < BM) reinterpret_cast<float*>(lds + kScaleOff)[threadIdx.x] = row_scale;
+    __syncthreads();
+  }
+  // The tile's outputs as (row within the tile, column within the tile, four values).
+  auto for_each_out = [&](auto&& emit) {
+    if constexpr (kSwiGLU) {
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            v[r] = static_cast<float>(swiglu_out<T>(acc[i][jj][r], acc[i][jj + 2][r]));
+          emit(wm + i * 16 + l16, (wave & 3) * 32 + jj * 16 + lg * 4, v);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float sc = kRowScale ? scales[wm + i * 16 + l16] : 1.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = kRowScale ? acc[i][j][r] * sc : acc[i][j][r];
+          emit(wm + i * 16 + l16, wn + j * 16 + lg * 4, v);
+        }
+      }
+    }
+  };
+  auto pack4 = [](const float (&v)[4]) {
+    const uint32_t lo = uint32_t(__builtin_bit_cast(uint16_t, tk::from_f32<T>(v[0]))) |
+                        (uint32_t(__builtin_bit_cast(uint16_t, tk::from_f32<T>(v[1]))) << 16);
+    const uint32_t hi = uint32_t(__builtin_bit_cast(uint16_t, tk::from_f32<T>(v[2]))) |
+                        (uint32_t(__builtin_bit_cast(uint16_t, tk::from_f32<T>(v[3]))) << 16);
+    return uint2{lo, hi};
+  };
+  const bool rows16 =
+      p.scn == 1 && (p.scm & 7) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0;
+  if (rows16) {
+    // Stage rows of kTileN values at a stride of kTileN * 2 + 16 bytes (4 dwords past a
+    // multiple of the 64 banks), so the 16 rows x 2 lane groups of an 8-byte write phase hit
+    // distinct banks; then kTileN / 8 lanes per row copy 16 bytes each (p.n % 8 == 0, so a
+    // 16-byte group is wholly inside or outside N).
+    constexpr int kStride = kTileN * 2 + 16;
+    static_assert(BM * kStride <= kScaleOff, "staged tile overlaps the row scales");
+    for_each_out([&](int r, int c, const float (&v)[4]) {
+      *reinterpret_cast<uint2*>(lds + r * kStride + c * 2) = pack4(v);
+    });
+    __syncthreads();
+    constexpr int kLanesPerRow = kTileN / 8;
+    constexpr int kRowsPerPass = kThreads / kLanesPerRow;
+    const int cr = threadIdx.x / kLanesPerRow, cc = (threadIdx.x % kLanesPerRow) * 8;
+#pragma unroll 4
+    for (int pass = 0; pass < BM / kRowsPerPass; ++pass) {
+      const int r = pass * kRowsPerPass + cr;
+      const i32x4 v = *reinterpret_cast<const i32x4*>(lds + r * kStride + cc * 2);
+      if (m0 + r < p.m && n0 + cc < p.n)
+        __builtin_nontemporal_store(v, reinterpret_cast<i32x4*>(C + (m0 + r) * p.scm + n0 + cc));
+    }
+    return;
+  }
   const bool vec = p.scn == 1 && (p.scm & 3) == 0 && (reinterpret_cast<uintptr_t>(C) & 7) == 0;
-  auto store4 = [&](int m, int n, const float (&v)[4]) {
+  for_each_out([&](int r, int c, const float (&v)[4]) {
+    const int m = m0 + r, n = n0 + c;
     if (m >= p.m || n >= p.n) return;
     T* dst = C + m * p.scm + n * p.scn;
     if (vec) {  // p.n % 8 == 0, so n .. n+3 are in range
-      const uint32_t lo = uint32_t(__builtin_bit_cast(uint16_t, tk::from_f32<T>(v[0]))) |
-                          (uint32_t(__builtin_bit_cast(uint16_t, tk::from_f32<T>(v[1]))) << 16);
-      const uint32_t hi = uint32_t(__builtin_bit_cast(uint16_t, tk::from_f32<T>(v[2]))) |
-                          (uint32_t(__builtin_bit_cast(uint16_t, tk::from_f32<T>(v[3]))) << 16);
-      *reinterpret_cast<uint2*>(dst) = uint2{lo, hi};
+      *reinterpret_cast<uint2*>(dst) = pack4(v);
     } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (n + r < p.n) dst[r * p.scn] = tk::from_f32<T>(v[r]);
+      for (int q = 0; q < 4; ++q)
+        if (n + q < p.n) dst[q * p.scn] = tk::from_f32<T>(v[q]);
     }
-  };
-  if constexpr (kSwiGLU) {
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int n = n0 + (wave & 3) * 32 + jj * 16 + lg * 4;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int m = m0 + wm + i * 16 + l16;
-        float v[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          v[r] = static_cast<float>(swiglu_out<T>(acc[i][jj][r], acc[i][jj + 2][r]));
-        store4(m, n, v);
-      }
-    }
-  } else {
-    const float* scales = reinterpret_cast<const float*>(lds);
-    if constexpr (kRowScale) {
-      __syncthreads();
-      if (threadIdx.x < BM) reinterpret_cast<float*>(lds)[threadIdx.x] = row_scale;
-      __syncthreads();
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int m = m0 + wm + i * 16 + l16;
-      const float sc = kRowScale ? scales[wm + i * 16 + l16] : 1.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = n0 + wn + j * 16 + lg * 4;
-        float v[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = kRowScale ? acc[i][j][r] * sc : acc[i][j][r];
-        store4(m, n, v);
-      }
-    }
-  }
+  });
 }
 
 
