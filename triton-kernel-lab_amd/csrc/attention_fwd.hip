@@ -125,6 +125,9 @@ struct Geo {
   // V: 32-byte granule g of row r at granule g ^ vswz(r). A transposed read phase (32
   // lanes) takes one granule of 8 consecutive rows.
   static __device__ __forceinline__ int vswz(int r) { return D == 128 ? (r & 7) : ((r >> 1) & 3); }
+  // O staging: 16-byte granule q of staged row r at q ^ oswz(r). An 8-byte write phase (16
+  // rows x 2 lane groups) and a 16-byte read phase then fall on distinct banks.
+  static __device__ __forceinline__ int oswz(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
 };
 
 // DMA of key/value block `blk` into its ring stage (clamped to `last`: blocks past the end
@@ -280,11 +283,25 @@ attn_fwd_dma_kernel(FwdArgs<T> kernel_arg) {
   constexpr int BM = G::BM, BN = G::BN, KS = G::KS, FT = G::FT, RB = G::RB, OPB = G::OPB,
                 STB = G::STB, STAGES = G::STAGES, DPB = G::DMA_PER_BLOCK;
   __shared__ __attribute__((aligned(1024))) char lds[STAGES * STB];
-  __shared__ int simd_of[G::WAVES];
+  // O staging: 16 rows of D values per wave (one query tile at a time), 32 KiB at head_dim
+  // 128 and 16 KiB at 64, so the ring and the staging fill the CU's 160 KiB (one workgroup
+  // at 128, two at 64). Until the first epilogue it holds each wave's SIMD id.
+  __shared__ __attribute__((aligned(16))) char ostage[G::WAVES * 16 * RB];
 
   const int wave0 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if ((threadIdx.x & 63) == 0) simd_of[wave0] = simd_id();
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_void*)lds;
+  // Ping-pong partner: the two waves that share a SIMD (hardware SIMD id from HW_ID) take
+  // opposite phases; grp is the wave's rank (0 or 1) among them.
+  int grp = 0;
+  {
+    int* simd_of = reinterpret_cast<int*>(ostage);
+    if ((threadIdx.x & 63) == 0) simd_of[wave0] = simd_id();
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < G::WAVES; ++w)
+      grp += (w < wave0 && simd_of[w] == simd_of[wave0]) ? 1 : 0;
+    grp = __builtin_amdgcn_readfirstlane(grp) & 1;
+  }
 
   // Causal, equal lengths, head_dim 128: the two query blocks paired_tile deals this
   // workgroup (blocks i and QB-1-i of one head). Otherwise one query block per workgroup;
@@ -296,8 +313,6 @@ attn_fwd_dma_kernel(FwdArgs<T> kernel_arg) {
     const T* __restrict__ Q = args.Q;
     const T* __restrict__ K = args.K;
     const T* __restrict__ V = args.V;
-    T* __restrict__ O = args.O;
-    float* __restrict__ lse = args.lse;
     int b, h, qb, start = 0, N = s.seq;
     uint32_t k_bytes = s.k_bytes, v_bytes = s.v_bytes;
     if (s.cu != nullptr) {
@@ -344,7 +359,6 @@ attn_fwd_dma_kernel(FwdArgs<T> kernel_arg) {
     const T* Qh = Q + b * s.q[0] + h * s.q[1] + int64_t(start) * s.q[2];
     const T* Kh = K + b * s.k[0] + kvh * s.k[1] + int64_t(start) * s.k[2];
     const T* Vh = V + b * s.v[0] + kvh * s.v[1] + int64_t(start) * s.v[2];
-    T* Oh = O + b * s.o[0] + h * s.o[1] + int64_t(start) * s.o[2];
 
     const int q0 = qb * BM;
     const int wq0 = q0 + wave * G::QW;
@@ -428,7 +442,7 @@ attn_fwd_dma_kernel(FwdArgs<T> kernel_arg) {
     float m_run[2] = {kNegInf, kNegInf}, l_part[2] = {0.f, 0.f};
     const float sl2 = s.scale_log2;
 
-    // Block 0 landed; simd_of visible.
+    // Block 0 landed.
     wait_lgkm<0>();
     wait_vmcnt<(STAGES - 2) * DPB>();
     barrier_no_fence();
@@ -439,10 +453,6 @@ attn_fwd_dma_kernel(FwdArgs<T> kernel_arg) {
     // the other's MFMAs occupy the matrix pipe. Block j is read in phases 2j .. 2j+3; at
     // the start of phase 2m (m >= 1) its stage's next block m + STAGES - 2 is fetched,
     // and block m must have landed before phase 2m begins.
-    int grp = 0;
-#pragma unroll
-    for (int w = 0; w < G::WAVES; ++w) grp += (w < wave && simd_of[w] == simd_of[wave]) ? 1 : 0;
-    grp = __builtin_amdgcn_readfirstlane(grp) & 1;
     const int phases = 2 * kv_blocks + 2;
     int t = 0;
     // Block m + STAGES - 2 (m >= 1) is fetched during this wave's MFMA phase of block m
@@ -652,26 +662,58 @@ attn_fwd_dma_kernel(FwdArgs<T> kernel_arg) {
     // No DMA may still be writing when the workgroup's LDS is released.
     wait_vmcnt<0>();
 
-    // O = O^T / l: acc[ft][qt] register r is feature 16 ft + 4 g + r.
+    // O = O^T / l: acc[ft][qt] register r is feature 16 ft + 4 g + r of query
+    // wq0 + 16 qt + c, 8 bytes once rounded. With 16-byte aligned rows each query tile goes
+    // through the wave's own staging rows and leaves as whole rows, 16 bytes per lane and
+    // full 128-byte lines, with non-temporal stores (the per-lane 8-byte stores wrote
+    // 32-byte pieces of lines). The staging rows belong to one wave: no barrier. The output
+    // pointer, strides and lane indices are formed here afresh rather than held across the
+    // key loop (at head_dim 64 that spilled registers).
+    const FwdArgs<T>& ea = kernel_args<FwdArgs<T>>();
+    int el = threadIdx.x & 63;
+    asm volatile("" : "+v"(el));
+    const int ec = el & 15, eg = el >> 4;
+    const int64_t o_row = ea.s.o[2];
+    T* const Oe = ea.O + b * ea.s.o[0] + h * ea.s.o[1] + int64_t(start) * o_row;
+    char* const orows = ostage + wave * (16 * RB);
+    const bool rows16 = (reinterpret_cast<uintptr_t>(Oe) & 15) == 0 && (o_row & 7) == 0;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       const float l = sum_over_column(l_part[qt]);
       const float inv = 1.0f / l;
-      const int query = wq0 + 16 * qt + c;
-      if (query < N) {
-        T* orow = Oh + query * s.o[2];
+      const int query = wq0 + 16 * qt + ec;
+      if (rows16) {
 #pragma unroll
         for (int ft = 0; ft < FT; ++ft) {
           uint2 u;
           u.x = pack2<T>(acc[ft][qt][0] * inv, acc[ft][qt][1] * inv);
           u.y = pack2<T>(acc[ft][qt][2] * inv, acc[ft][qt][3] * inv);
-          *reinterpret_cast<uint2*>(orow + ft * 16 + g * 4) = u;
+          *reinterpret_cast<uint2*>(orows + ec * RB + (((2 * ft + (eg >> 1)) ^ G::oswz(ec)) * 16) +
+                                    (eg & 1) * 8) = u;
         }
-        if (lse != nullptr && g == 0) {
-          const int64_t at = s.cu != nullptr ? int64_t(h) * s.total + start + query
-                                             : (int64_t(b) * s.heads + h) * N + query;
-          lse[at] = m_run[qt] + __log2f(l);
+        constexpr int LPR = RB / 16, RPI = 64 / LPR;  // lanes per row, rows per instruction
+#pragma unroll
+        for (int p = 0; p < 16 / RPI; ++p) {
+          const int r = p * RPI + el / LPR, q = el % LPR;
+          const i32x4 v = *reinterpret_cast<const i32x4*>(orows + r * RB + ((q ^ G::oswz(r)) * 16));
+          const int row_query = wq0 + 16 * qt + r;
+          if (row_query < N)
+            __builtin_nontemporal_store(v, reinterpret_cast<i32x4*>(Oe + row_query * o_row + q * 8));
         }
+      } else if (query < N) {
+        T* orow = Oe + query * o_row;
+#pragma unroll
+        for (int ft = 0; ft < FT; ++ft) {
+          uint2 u;
+          u.x = pack2<T>(acc[ft][qt][0] * inv, acc[ft][qt][1] * inv);
+          u.y = pack2<T>(acc[ft][qt][2] * inv, acc[ft][qt][3] * inv);
+          *reinterpret_cast<uint2*>(orow + ft * 16 + eg * 4) = u;
+        }
+      }
+      if (query < N && ea.lse != nullptr && eg == 0) {
+        const int64_t at = ea.s.cu != nullptr ? int64_t(h) * ea.s.total + start + query
+                                              : (int64_t(b) * ea.s.heads + h) * N + query;
+        ea.lse[at] = m_run[qt] + __log2f(l);
       }
     }
   }  // tiles
