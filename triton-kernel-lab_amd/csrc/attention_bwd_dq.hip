@@ -65,6 +65,9 @@ struct DqGeo {
   static constexpr int DMA_PER_OP = OPB / 1024 / WAVES;
   static constexpr int DMA_PER_BLOCK = 2 * DMA_PER_OP;
   static constexpr int SLOTS = RB / 16;
+  // dQ staging: 16-byte granule q of staged row r at q ^ oswz(r), so an 8-byte write phase
+  // (16 rows x 2 lane groups) and a 16-byte read phase fall on distinct banks.
+  static __device__ __forceinline__ int oswz(int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); }
   // Read units of the MFMA phase (four LDS instructions each): NT transposed-K units
   // (32-key step s = u / FP, feature tiles 2p, 2p + 1), then KS K-row units, then KS V-row
   // units. DEPTH units are in flight (head_dim 128 holds two to stay within 256
@@ -228,7 +231,11 @@ attn_bwd_dq_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T*
   using G = DqGeo<D>;
   constexpr int BM = G::BM, BN = G::BN, KS = G::KS, FT = G::FT, RB = G::RB, STB = G::STB, STAGES = G::STAGES, DPB = G::DMA_PER_BLOCK;
   __shared__ __attribute__((aligned(1024))) char lds[STAGES * STB];
-  __shared__ int simd_of[G::WAVES];
+  // dQ staging: 16 rows of D values per wave (one query tile at a time); 32 KiB at head_dim
+  // 128, so the ring and the staging fill the CU's 160 KiB. Until the epilogue it holds
+  // each wave's SIMD id.
+  __shared__ __attribute__((aligned(16))) char qstage[G::WAVES * 16 * RB];
+  int* const simd_of = reinterpret_cast<int*>(qstage);
 
   // Workgroup -> (batch*head, query block), as in the forward: XCD-contiguous ranges,
   // causal heaviest-first; varlen: the heavy-first schedule, heads over the XCDs.
@@ -454,18 +461,47 @@ attn_bwd_dq_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T*
   while (t < phases - 1) end_phase();
   wait_vmcnt<0>();
 
-  // dQ = scale (dQ^T)^T: acc[ft][qt] register r is feature 16 ft + 4 g + r.
+  // dQ = scale (dQ^T)^T: acc[ft][qt] register r is feature 16 ft + 4 g + r of query
+  // wq0 + 16 qt + c, 8 bytes once rounded. With 16-byte aligned rows each query tile goes
+  // through the wave's own staging rows (every wave has read the SIMD ids long before) and
+  // leaves as whole rows, 16 bytes per lane and full 128-byte lines, with non-temporal
+  // stores. Lane indices are formed afresh rather than held across the key loop.
+  int el = threadIdx.x & 63;
+  asm volatile("" : "+v"(el));
+  const int ec = el & 15, eg = el >> 4;
+  T* const dQh = dQ + qbase;
+  char* const qrows = qstage + wave * (16 * RB);
+  const bool rows16 = (reinterpret_cast<uintptr_t>(dQh) & 15) == 0 && (s.q[2] & 7) == 0;
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    const int query = wq0 + 16 * qt + c;
-    if (query < N) {
-      T* row = dQ + qbase + int64_t(query) * s.q[2];
+    const int query = wq0 + 16 * qt + ec;
+    if (rows16) {
 #pragma unroll
       for (int ft = 0; ft < FT; ++ft) {
         uint2 u;
         u.x = pack2<T>(acc[ft][qt][0] * s.scale, acc[ft][qt][1] * s.scale);
         u.y = pack2<T>(acc[ft][qt][2] * s.scale, acc[ft][qt][3] * s.scale);
-        *reinterpret_cast<uint2*>(row + ft * 16 + g * 4) = u;
+        *reinterpret_cast<uint2*>(qrows + ec * RB + (((2 * ft + (eg >> 1)) ^ G::oswz(ec)) * 16) +
+                                  (eg & 1) * 8) = u;
+      }
+      constexpr int LPR = RB / 16, RPI = 64 / LPR;  // lanes per row, rows per instruction
+#pragma unroll
+      for (int p = 0; p < 16 / RPI; ++p) {
+        const int r = p * RPI + el / LPR, q = el % LPR;
+        const i32x4 v = *reinterpret_cast<const i32x4*>(qrows + r * RB + ((q ^ G::oswz(r)) * 16));
+        const int row_query = wq0 + 16 * qt + r;
+        if (row_query < N)
+          __builtin_nontemporal_store(
+              v, reinterpret_cast<i32x4*>(dQh + int64_t(row_query) * s.q[2] + q * 8));
+      }
+    } else if (query < N) {
+      T* row = dQh + int64_t(query) * s.q[2];
+#pragma unroll
+      for (int ft = 0; ft < FT; ++ft) {
+        uint2 u;
+        u.x = pack2<T>(acc[ft][qt][0] * s.scale, acc[ft][qt][1] * s.scale);
+        u.y = pack2<T>(acc[ft][qt][2] * s.scale, acc[ft][qt][3] * s.scale);
+        *reinterpret_cast<uint2*>(row + ft * 16 + eg * 4) = u;
       }
     }
   }
