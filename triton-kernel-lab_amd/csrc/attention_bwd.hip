@@ -492,57 +492,35 @@ attn_bwd_dkdv_dma_kernel(const T* __restrict__ Q, const T* __restrict__ K,
 
     // dK = scale (dK^T)^T, dV = (dV^T)^T: register r of tile dt is feature
     // 32 dt + 8 (r / 4) + 4 hi + r % 4 of this lane's key, 8 bytes once rounded (16-byte
-    // granule 4 dt + r / 4 of the row, half hi). With 16-byte aligned rows each of dK and dV
-    // goes through the wave's staging rows (granule q of row r at q ^ row_swz(r)) and
-    // leaves as whole rows, 16 bytes per lane, non-temporal full 128-byte lines; the
-    // per-lane stores wrote 16 bytes to each of 32 rows per instruction.
-    T* const dKh = dK + kvbase;
-    T* const dVh = dV + kvbase;
-    const bool rows16 = ((reinterpret_cast<uintptr_t>(dKh) | reinterpret_cast<uintptr_t>(dVh)) & 15) == 0 &&
-                        (kn & 7) == 0;
-    if (rows16) {
-      char* const krows = kvstage + wave * (G::LW * RB);
-      auto emit = [&](T* dst, const f32x16 (&acc)[DT], float scale) {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            uint2 u;
-            u.x = pack2<T>(acc[dt][g4 * 4 + 0] * scale, acc[dt][g4 * 4 + 1] * scale);
-            u.y = pack2<T>(acc[dt][g4 * 4 + 2] * scale, acc[dt][g4 * 4 + 3] * scale);
-            *reinterpret_cast<uint2*>(krows + l32 * RB + (((4 * dt + g4) ^ G::row_swz(l32)) * 16) +
-                                      hi * 8) = u;
-          }
-        constexpr int LPR = RB / 16, RPI = 64 / LPR;  // lanes per row, rows per instruction
-#pragma unroll
-        for (int p = 0; p < G::LW / RPI; ++p) {
-          const int r = p * RPI + lane / LPR, q = lane % LPR;
-          const i32x4 v =
-              *reinterpret_cast<const i32x4*>(krows + r * RB + ((q ^ G::row_swz(r)) * 16));
-          if (wk0 + r < N)
-            __builtin_nontemporal_store(
-                v, reinterpret_cast<i32x4*>(dst + int64_t(wk0 + r) * kn + q * 8));
-        }
-      };
-      emit(dKh, acc_dk, s.scale);
-      emit(dVh, acc_dv, 1.0f);
-    } else if (key < N) {
-      T* dkr = dKh + int64_t(key) * kn;
-      T* dvr = dVh + int64_t(key) * kn;
+    // granule 4 dt + r / 4 of the row, half hi). Each of dK and dV goes through the wave's
+    // staging rows (granule q of row r at q ^ row_swz(r)) and leaves as whole rows, 16 bytes
+    // per lane, non-temporal full 128-byte lines (per-lane stores wrote 16 bytes to each of
+    // 32 rows per instruction); the entry points accept only 16-byte aligned tensors and
+    // strides that are multiples of 8 elements, so every row is 16-byte aligned.
+    char* const krows = kvstage + wave * (G::LW * RB);
+    auto emit = [&](T* dst, const f32x16 (&acc)[DT], float scale) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
-          const int d = dt * 32 + g4 * 8 + hi * 4;
           uint2 u;
-          u.x = pack2<T>(acc_dk[dt][g4 * 4 + 0] * s.scale, acc_dk[dt][g4 * 4 + 1] * s.scale);
-          u.y = pack2<T>(acc_dk[dt][g4 * 4 + 2] * s.scale, acc_dk[dt][g4 * 4 + 3] * s.scale);
-          *reinterpret_cast<uint2*>(dkr + d) = u;
-          u.x = pack2<T>(acc_dv[dt][g4 * 4 + 0], acc_dv[dt][g4 * 4 + 1]);
-          u.y = pack2<T>(acc_dv[dt][g4 * 4 + 2], acc_dv[dt][g4 * 4 + 3]);
-          *reinterpret_cast<uint2*>(dvr + d) = u;
+          u.x = pack2<T>(acc[dt][g4 * 4 + 0] * scale, acc[dt][g4 * 4 + 1] * scale);
+          u.y = pack2<T>(acc[dt][g4 * 4 + 2] * scale, acc[dt][g4 * 4 + 3] * scale);
+          *reinterpret_cast<uint2*>(krows + l32 * RB + (((4 * dt + g4) ^ G::row_swz(l32)) * 16) +
+                                    hi * 8) = u;
         }
-    }
+      constexpr int LPR = RB / 16, RPI = 64 / LPR;  // lanes per row, rows per instruction
+#pragma unroll
+      for (int p = 0; p < G::LW / RPI; ++p) {
+        const int r = p * RPI + lane / LPR, q = lane % LPR;
+        const i32x4 v = *reinterpret_cast<const i32x4*>(krows + r * RB + ((q ^ G::row_swz(r)) * 16));
+        if (wk0 + r < N)
+          __builtin_nontemporal_store(
+              v, reinterpret_cast<i32x4*>(dst + kvbase + int64_t(wk0 + r) * kn + q * 8));
+      }
+    };
+    emit(dK, acc_dk, s.scale);
+    emit(dV, acc_dv, 1.0f);
   }  // key blocks
 }
 
@@ -1082,11 +1060,13 @@ attn_bwd_dkdv_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K,
     wait_vmcnt<0>();
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     // dK = scale (dK^T)^T, dV = (dV^T)^T: register r of adk / adv [ft][kt] is feature
-    // 16 ft + 4 g + r of key pk0 + 16 kt + c, 8 bytes once rounded. With 16-byte aligned
-    // rows each key tile goes through the pair's exchange buffer (the producer has written
-    // its last fragments and this wave has read them): dK rows then dV rows, 16-byte granule
-    // q of row r at q ^ (r & 15), read back as whole rows and stored 16 bytes per lane as
-    // non-temporal full 128-byte lines. Lane indices are formed afresh here.
+    // 16 ft + 4 g + r of key pk0 + 16 kt + c, 8 bytes once rounded. Each key tile goes
+    // through the pair's exchange buffer (the producer has written its last fragments and
+    // this wave has read them): dK rows then dV rows, 16-byte granule q of row r at
+    // q ^ (r & 15), read back as whole rows and stored 16 bytes per lane as non-temporal full
+    // 128-byte lines; the entry points accept only 16-byte aligned tensors and strides that
+    // are multiples of 8 elements, so every row is 16-byte aligned. Lane indices are formed
+    // afresh here.
     int el = threadIdx.x & 63;
     asm volatile("" : "+v"(el));
     const int ec = el & 15, eg = el >> 4;
@@ -1094,50 +1074,31 @@ attn_bwd_dkdv_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K,
     T* const dVh = dV + kvbase;
     char* const xrows = lds + STAGES * STB + pair * G::XB;
     static_assert(2 * 16 * RB <= G::XB, "two 16-key tiles of rows per exchange buffer");
-    const bool rows16 = ((reinterpret_cast<uintptr_t>(dKh) | reinterpret_cast<uintptr_t>(dVh)) & 15) == 0 &&
-                        (kn & 7) == 0;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
-      const int key = pk0 + 16 * kt + ec;
-      if (rows16) {
 #pragma unroll
-        for (int ft = 0; ft < FT; ++ft) {
-          const int at = ec * RB + (((2 * ft + (eg >> 1)) ^ ec) * 16) + (eg & 1) * 8;
-          uint2 u;
-          u.x = pack2<T>(adk[ft][kt][0] * s.scale, adk[ft][kt][1] * s.scale);
-          u.y = pack2<T>(adk[ft][kt][2] * s.scale, adk[ft][kt][3] * s.scale);
-          *reinterpret_cast<uint2*>(xrows + at) = u;
-          u.x = pack2<T>(adv[ft][kt][0], adv[ft][kt][1]);
-          u.y = pack2<T>(adv[ft][kt][2], adv[ft][kt][3]);
-          *reinterpret_cast<uint2*>(xrows + 16 * RB + at) = u;
-        }
-        constexpr int LPR = RB / 16, RPI = 64 / LPR;  // lanes per row, rows per instruction
+      for (int ft = 0; ft < FT; ++ft) {
+        const int at = ec * RB + (((2 * ft + (eg >> 1)) ^ ec) * 16) + (eg & 1) * 8;
+        uint2 u;
+        u.x = pack2<T>(adk[ft][kt][0] * s.scale, adk[ft][kt][1] * s.scale);
+        u.y = pack2<T>(adk[ft][kt][2] * s.scale, adk[ft][kt][3] * s.scale);
+        *reinterpret_cast<uint2*>(xrows + at) = u;
+        u.x = pack2<T>(adv[ft][kt][0], adv[ft][kt][1]);
+        u.y = pack2<T>(adv[ft][kt][2], adv[ft][kt][3]);
+        *reinterpret_cast<uint2*>(xrows + 16 * RB + at) = u;
+      }
+      constexpr int LPR = RB / 16, RPI = 64 / LPR;  // lanes per row, rows per instruction
 #pragma unroll
-        for (int p = 0; p < 16 / RPI; ++p) {
-          const int r = p * RPI + el / LPR, q = el % LPR;
-          const int from = r * RB + ((q ^ r) * 16);
-          const i32x4 vk = *reinterpret_cast<const i32x4*>(xrows + from);
-          const i32x4 vv = *reinterpret_cast<const i32x4*>(xrows + 16 * RB + from);
-          const int row_key = pk0 + 16 * kt + r;
-          if (row_key < N) {
-            const int64_t to = int64_t(row_key) * kn + q * 8;
-            __builtin_nontemporal_store(vk, reinterpret_cast<i32x4*>(dKh + to));
-            __builtin_nontemporal_store(vv, reinterpret_cast<i32x4*>(dVh + to));
-          }
-        }
-      } else if (key < N) {
-        T* dkr = dKh + int64_t(key) * kn;
-        T* dvr = dVh + int64_t(key) * kn;
-#pragma unroll
-        for (int ft = 0; ft < FT; ++ft) {
-          const int d = 16 * ft + 4 * eg;
-          uint2 u;
-          u.x = pack2<T>(adk[ft][kt][0] * s.scale, adk[ft][kt][1] * s.scale);
-          u.y = pack2<T>(adk[ft][kt][2] * s.scale, adk[ft][kt][3] * s.scale);
-          *reinterpret_cast<uint2*>(dkr + d) = u;
-          u.x = pack2<T>(adv[ft][kt][0], adv[ft][kt][1]);
-          u.y = pack2<T>(adv[ft][kt][2], adv[ft][kt][3]);
-          *reinterpret_cast<uint2*>(dvr + d) = u;
+      for (int p = 0; p < 16 / RPI; ++p) {
+        const int r = p * RPI + el / LPR, q = el % LPR;
+        const int from = r * RB + ((q ^ r) * 16);
+        const i32x4 vk = *reinterpret_cast<const i32x4*>(xrows + from);
+        const i32x4 vv = *reinterpret_cast<const i32x4*>(xrows + 16 * RB + from);
+        const int row_key = pk0 + 16 * kt + r;
+        if (row_key < N) {
+          const int64_t to = int64_t(row_key) * kn + q * 8;
+          __builtin_nontemporal_store(vk, reinterpret_cast<i32x4*>(dKh + to));
+          __builtin_nontemporal_store(vv, reinterpret_cast<i32x4*>(dVh + to));
         }
       }
     }

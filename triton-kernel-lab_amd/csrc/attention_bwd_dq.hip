@@ -462,47 +462,36 @@ attn_bwd_dq_pp_kernel(const T* __restrict__ Q, const T* __restrict__ K, const T*
   wait_vmcnt<0>();
 
   // dQ = scale (dQ^T)^T: acc[ft][qt] register r is feature 16 ft + 4 g + r of query
-  // wq0 + 16 qt + c, 8 bytes once rounded. With 16-byte aligned rows each query tile goes
-  // through the wave's own staging rows (every wave has read the SIMD ids long before) and
-  // leaves as whole rows, 16 bytes per lane and full 128-byte lines, with non-temporal
-  // stores. Lane indices are formed afresh rather than held across the key loop.
+  // wq0 + 16 qt + c, 8 bytes once rounded. Each query tile goes through the wave's own
+  // staging rows (every wave has read the SIMD ids long before) and leaves as whole rows,
+  // 16 bytes per lane and full 128-byte lines, with non-temporal stores; the entry points
+  // accept only 16-byte aligned tensors and strides that are multiples of 8 elements, so
+  // every dQ row is 16-byte aligned. Lane indices are formed afresh rather than held across
+  // the key loop.
   int el = threadIdx.x & 63;
   asm volatile("" : "+v"(el));
   const int ec = el & 15, eg = el >> 4;
   T* const dQh = dQ + qbase;
   char* const qrows = qstage + wave * (16 * RB);
-  const bool rows16 = (reinterpret_cast<uintptr_t>(dQh) & 15) == 0 && (s.q[2] & 7) == 0;
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    const int query = wq0 + 16 * qt + ec;
-    if (rows16) {
 #pragma unroll
-      for (int ft = 0; ft < FT; ++ft) {
-        uint2 u;
-        u.x = pack2<T>(acc[ft][qt][0] * s.scale, acc[ft][qt][1] * s.scale);
-        u.y = pack2<T>(acc[ft][qt][2] * s.scale, acc[ft][qt][3] * s.scale);
-        *reinterpret_cast<uint2*>(qrows + ec * RB + (((2 * ft + (eg >> 1)) ^ G::oswz(ec)) * 16) +
-                                  (eg & 1) * 8) = u;
-      }
-      constexpr int LPR = RB / 16, RPI = 64 / LPR;  // lanes per row, rows per instruction
+    for (int ft = 0; ft < FT; ++ft) {
+      uint2 u;
+      u.x = pack2<T>(acc[ft][qt][0] * s.scale, acc[ft][qt][1] * s.scale);
+      u.y = pack2<T>(acc[ft][qt][2] * s.scale, acc[ft][qt][3] * s.scale);
+      *reinterpret_cast<uint2*>(qrows + ec * RB + (((2 * ft + (eg >> 1)) ^ G::oswz(ec)) * 16) +
+                                (eg & 1) * 8) = u;
+    }
+    constexpr int LPR = RB / 16, RPI = 64 / LPR;  // lanes per row, rows per instruction
 #pragma unroll
-      for (int p = 0; p < 16 / RPI; ++p) {
-        const int r = p * RPI + el / LPR, q = el % LPR;
-        const i32x4 v = *reinterpret_cast<const i32x4*>(qrows + r * RB + ((q ^ G::oswz(r)) * 16));
-        const int row_query = wq0 + 16 * qt + r;
-        if (row_query < N)
-          __builtin_nontemporal_store(
-              v, reinterpret_cast<i32x4*>(dQh + int64_t(row_query) * s.q[2] + q * 8));
-      }
-    } else if (query < N) {
-      T* row = dQh + int64_t(query) * s.q[2];
-#pragma unroll
-      for (int ft = 0; ft < FT; ++ft) {
-        uint2 u;
-        u.x = pack2<T>(acc[ft][qt][0] * s.scale, acc[ft][qt][1] * s.scale);
-        u.y = pack2<T>(acc[ft][qt][2] * s.scale, acc[ft][qt][3] * s.scale);
-        *reinterpret_cast<uint2*>(row + ft * 16 + eg * 4) = u;
-      }
+    for (int p = 0; p < 16 / RPI; ++p) {
+      const int r = p * RPI + el / LPR, q = el % LPR;
+      const i32x4 v = *reinterpret_cast<const i32x4*>(qrows + r * RB + ((q ^ G::oswz(r)) * 16));
+      const int row_query = wq0 + 16 * qt + r;
+      if (row_query < N)
+        __builtin_nontemporal_store(
+            v, reinterpret_cast<i32x4*>(dQh + int64_t(row_query) * s.q[2] + q * 8));
     }
   }
 }

@@ -663,12 +663,13 @@ attn_fwd_dma_kernel(FwdArgs<T> kernel_arg) {
     wait_vmcnt<0>();
 
     // O = O^T / l: acc[ft][qt] register r is feature 16 ft + 4 g + r of query
-    // wq0 + 16 qt + c, 8 bytes once rounded. With 16-byte aligned rows each query tile goes
-    // through the wave's own staging rows and leaves as whole rows, 16 bytes per lane and
-    // full 128-byte lines, with non-temporal stores (the per-lane 8-byte stores wrote
-    // 32-byte pieces of lines). The staging rows belong to one wave: no barrier. The output
-    // pointer, strides and lane indices are formed here afresh rather than held across the
-    // key loop (at head_dim 64 that spilled registers).
+    // wq0 + 16 qt + c, 8 bytes once rounded. Each query tile goes through the wave's own
+    // staging rows and leaves as whole rows, 16 bytes per lane and full 128-byte lines, with
+    // non-temporal stores (the per-lane 8-byte stores wrote 32-byte pieces of lines); the
+    // entry points accept only 16-byte aligned tensors and strides that are multiples of 8
+    // elements, so every O row is 16-byte aligned. The staging rows belong to one wave: no
+    // barrier. The output pointer, strides and lane indices are formed here afresh rather
+    // than held across the key loop (at head_dim 64 that spilled registers).
     const FwdArgs<T>& ea = kernel_args<FwdArgs<T>>();
     int el = threadIdx.x & 63;
     asm volatile("" : "+v"(el));
@@ -676,40 +677,28 @@ attn_fwd_dma_kernel(FwdArgs<T> kernel_arg) {
     const int64_t o_row = ea.s.o[2];
     T* const Oe = ea.O + b * ea.s.o[0] + h * ea.s.o[1] + int64_t(start) * o_row;
     char* const orows = ostage + wave * (16 * RB);
-    const bool rows16 = (reinterpret_cast<uintptr_t>(Oe) & 15) == 0 && (o_row & 7) == 0;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
       const float l = sum_over_column(l_part[qt]);
       const float inv = 1.0f / l;
-      const int query = wq0 + 16 * qt + ec;
-      if (rows16) {
 #pragma unroll
-        for (int ft = 0; ft < FT; ++ft) {
-          uint2 u;
-          u.x = pack2<T>(acc[ft][qt][0] * inv, acc[ft][qt][1] * inv);
-          u.y = pack2<T>(acc[ft][qt][2] * inv, acc[ft][qt][3] * inv);
-          *reinterpret_cast<uint2*>(orows + ec * RB + (((2 * ft + (eg >> 1)) ^ G::oswz(ec)) * 16) +
-                                    (eg & 1) * 8) = u;
-        }
-        constexpr int LPR = RB / 16, RPI = 64 / LPR;  // lanes per row, rows per instruction
-#pragma unroll
-        for (int p = 0; p < 16 / RPI; ++p) {
-          const int r = p * RPI + el / LPR, q = el % LPR;
-          const i32x4 v = *reinterpret_cast<const i32x4*>(orows + r * RB + ((q ^ G::oswz(r)) * 16));
-          const int row_query = wq0 + 16 * qt + r;
-          if (row_query < N)
-            __builtin_nontemporal_store(v, reinterpret_cast<i32x4*>(Oe + row_query * o_row + q * 8));
-        }
-      } else if (query < N) {
-        T* orow = Oe + query * o_row;
-#pragma unroll
-        for (int ft = 0; ft < FT; ++ft) {
-          uint2 u;
-          u.x = pack2<T>(acc[ft][qt][0] * inv, acc[ft][qt][1] * inv);
-          u.y = pack2<T>(acc[ft][qt][2] * inv, acc[ft][qt][3] * inv);
-          *reinterpret_cast<uint2*>(orow + ft * 16 + eg * 4) = u;
-        }
+      for (int ft = 0; ft < FT; ++ft) {
+        uint2 u;
+        u.x = pack2<T>(acc[ft][qt][0] * inv, acc[ft][qt][1] * inv);
+        u.y = pack2<T>(acc[ft][qt][2] * inv, acc[ft][qt][3] * inv);
+        *reinterpret_cast<uint2*>(orows + ec * RB + (((2 * ft + (eg >> 1)) ^ G::oswz(ec)) * 16) +
+                                  (eg & 1) * 8) = u;
       }
+      constexpr int LPR = RB / 16, RPI = 64 / LPR;  // lanes per row, rows per instruction
+#pragma unroll
+      for (int p = 0; p < 16 / RPI; ++p) {
+        const int r = p * RPI + el / LPR, q = el % LPR;
+        const i32x4 v = *reinterpret_cast<const i32x4*>(orows + r * RB + ((q ^ G::oswz(r)) * 16));
+        const int row_query = wq0 + 16 * qt + r;
+        if (row_query < N)
+          __builtin_nontemporal_store(v, reinterpret_cast<i32x4*>(Oe + row_query * o_row + q * 8));
+      }
+      const int query = wq0 + 16 * qt + ec;
       if (query < N && ea.lse != nullptr && eg == 0) {
         const int64_t at = ea.s.cu != nullptr ? int64_t(h) * ea.s.total + start + query
                                               : (int64_t(b) * ea.s.heads + h) * N + query;
